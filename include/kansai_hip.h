@@ -1,0 +1,197 @@
+/*
+ * kansai_hip.h -- C ABI of the MI355X (gfx950) HIP backend for Kansai's
+ * int8 quantize -> int8 matmul -> dequantize path and its fp32 matmul.
+ *
+ * Contract (mirrors the reference's backend contract,
+ * backend/metal/include/kansai/backend/metal/MetalOps.hpp:13-88):
+ *   - plain pointers and int64 sizes; no C++ or torch types;
+ *   - tensor pointers are DEVICE pointers (from kh_alloc, or any device
+ *     allocation on the current device) unless named host_*; outputs are
+ *     caller-allocated; the library never frees caller memory;
+ *   - every function returns an int status, KH_OK (0) on success; on
+ *     failure kh_last_error() gives a message (thread-local);
+ *   - compute calls are ordered on the library stream of the current
+ *     device; kh_synchronize() waits for them and reports data errors
+ *     found on the device (a non-finite value given to a quantizer), the
+ *     asynchronous counterpart of the reference raising ValueError from
+ *     round(nan) (python/kansai/quantize.py:69).
+ *   - row-major, contiguous tensors, as the reference's Tensor
+ *     (core/include/kansai/Tensor.hpp:228-237).
+ *
+ * Quantization arithmetic is the reference's exactly
+ * (python/kansai/quantize.py:66-70, :76):
+ *   m = max|v|; scale = m / 127.0 (binary64) if m > 0 else 1.0;
+ *   q = clamp(round_half_even((double)v / scale), -127, 127);
+ *   dequantized = (float)((double)q * scale).
+ * Scales are binary64 device arrays, like the reference's Python float.
+ */
+#ifndef KANSAI_HIP_H
+#define KANSAI_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KH_OK 0
+#define KH_ERR_NO_DEVICE 1     /* no gfx950 device / library not initialised */
+#define KH_ERR_INVALID_ARG 2   /* shape, pointer or alignment problem */
+#define KH_ERR_OOM 3           /* device allocation failed */
+#define KH_ERR_NONFINITE 4     /* NaN/inf reached a quantizer */
+#define KH_ERR_HIP 5           /* any other HIP runtime error */
+
+/* ---- device, errors --------------------------------------------------- */
+
+/* kan::metal::available() (MetalOps.hpp:15-18): 1 if a gfx950 device is
+ * usable, else 0.  Never fails, never throws. */
+int kh_available(void);
+
+/* Binds the calling thread to `device` and creates its library stream and
+ * scratch state.  Called implicitly by every entry point on device 0 if
+ * never called. */
+int kh_init(int device);
+
+/* Last error message of the calling thread ("" if none). Replaces the
+ * std::runtime_error text the reference throws (MetalOps.mm:259-261). */
+const char* kh_last_error(void);
+
+/* Device facts used for roofline denominators: name (gcnArchName),
+ * compute units, peak engine clock (kHz), memory clock (kHz), bus width
+ * (bits), total global memory (bytes). */
+int kh_device_info(char* name, size_t name_len, int* cus, int* clock_khz,
+                   int* mem_clock_khz, int* bus_width, size_t* total_mem);
+
+/* Waits for all work queued on the library stream, then reports (and
+ * clears) deferred device errors: returns KH_ERR_NONFINITE if a quantizer
+ * met a NaN/inf since the previous synchronize. */
+int kh_synchronize(void);
+
+/* The library stream (a hipStream_t) of the current device, for callers
+ * that record their own events or order their own work after it. */
+int kh_get_stream(void** stream);
+
+/* ---- device memory (hipMalloc-backed pool) ---------------------------- */
+
+/* Device buffers from a caching pool: freed blocks are kept per size class
+ * and reused, so a graph executed repeatedly stops calling hipMalloc after
+ * its first run.  Replaces core/src/Storage.cpp:22-32 (page-aligned host
+ * allocation) and the first-fit core/src/StoragePool.cpp:5-24 for device
+ * memory.  Blocks are 256-byte aligned.  kh_free returns a block to the
+ * pool (stream-ordered: it is reused only by later work on the same
+ * stream).  kh_pool_trim gives all cached blocks back to the driver. */
+int kh_alloc(size_t bytes, void** dptr);
+int kh_free(void* dptr);
+int kh_pool_trim(void);
+/* bytes currently handed out, bytes cached in free lists, number of
+ * hipMalloc calls made so far. */
+int kh_pool_stats(size_t* in_use, size_t* cached, size_t* driver_allocs);
+
+/* Copies.  kh_memcpy_h2d / kh_memcpy_d2h are synchronous with respect to
+ * the host (they order after queued work on the library stream), as the
+ * reference's synchronous backend calls are (MetalOps.mm:317).
+ * kh_memcpy_d2d is stream-ordered. */
+int kh_memcpy_h2d(void* dst, const void* host_src, size_t bytes);
+int kh_memcpy_d2h(void* host_dst, const void* src, size_t bytes);
+int kh_memcpy_d2d(void* dst, const void* src, size_t bytes);
+
+/* ---- timing (HIP events on the library stream) ------------------------ */
+int kh_event_create(void** event);
+int kh_event_record(void* event);
+int kh_event_elapsed_ms(void* start, void* end, float* ms);
+int kh_event_destroy(void* event);
+
+/* ---- quantize / dequantize -------------------------------------------- */
+
+/* quantize_symmetric (python/kansai/quantize.py:50-70) over a whole
+ * tensor of n fp32 values: one scale, written to scale[0]. */
+int kh_quantize_tensor(const float* x, int64_t n, int8_t* q, double* scale);
+
+/* quantize_symmetric applied to each row of a [rows, cols] matrix: one
+ * scale per row (per token).  scales has `rows` entries. */
+int kh_quantize_rows(const float* x, int64_t rows, int64_t cols, int8_t* q, double* scales);
+
+/* quantize_symmetric applied to each column of an nn.Linear weight
+ * (python/kansai/nn.py:74-81 lays it out [in = k, out = n], so a column
+ * is one output channel).  Codes are written packed K-contiguous for the
+ * GEMM: q_packed[j * k + i] = code of w[i, j]; scales has n entries. */
+int kh_quantize_cols_packed(const float* w, int64_t k, int64_t n, int8_t* q_packed, double* scales);
+
+/* Per-tensor scale (one scale for the whole weight, as the reference's
+ * QTensor.from_tensor, quantize.py:95-98) with the same K-contiguous
+ * packing as kh_quantize_cols_packed. */
+int kh_quantize_tensor_packed(const float* w, int64_t k, int64_t n, int8_t* q_packed, double* scale);
+
+/* dequantize (quantize.py:73-77): out[i] = (float)((double)q[i] * scale[0]). */
+int kh_dequantize_tensor(const int8_t* q, int64_t n, const double* scale, float* out);
+
+/* Per-row dequantize: out[r, c] = (float)((double)q[r, c] * scales[r]). */
+int kh_dequantize_rows(const int8_t* q, int64_t rows, int64_t cols, const double* scales, float* out);
+
+/* Dequantize of a packed per-column weight back to the [k, n] fp32 layout
+ * the reference's qlinear multiplies with (quantize.py:115-122):
+ * out[i, j] = (float)((double)q_packed[j * k + i] * scales[scales_n == 1 ? 0 : j]). */
+int kh_dequantize_packed(const int8_t* q_packed, int64_t k, int64_t n, const double* scales,
+                         int64_t scales_n, float* out);
+
+/* ---- int8 GEMM with fused dequantize + bias epilogue ------------------- */
+
+/* acc[i, j] = sum_k a[i, k] * b_packed[j, k]   (int32, exact)
+ * out[i, j] = (float)((double)acc[i, j] * (sa_i * sb_j)) + bias[j]
+ * a: [M, K] int8 row-major (quantized activations); b_packed: [N, K] int8
+ * (a packed weight from kh_quantize_*_packed).  sa has M entries when
+ * sa_per_row != 0 else 1; sb has N entries when sb_per_col != 0 else 1
+ * (binary64, device).  bias (fp32 [N], device) may be NULL.  out (fp32
+ * [M, N]) may be NULL; acc_out (int32 [M, N]) may be NULL; at least one of
+ * them must be given.  The reference has no int8 GEMM (quantize.py:30-44):
+ * this replaces its x.matmul(dequantize(W)).add(bias)
+ * (quantize.py:115-122) on the int8 path.  K <= 133144 keeps the int32
+ * accumulator exact. */
+int kh_gemm_i8(const int8_t* a, const int8_t* b_packed, int64_t M, int64_t N, int64_t K,
+               const double* sa, int sa_per_row, const double* sb, int sb_per_col,
+               const float* bias, float* out, int32_t* acc_out);
+
+/* Per-token activation quantize fused into the GEMM's producer: x fp32
+ * [M, K] is quantized per row into q_scratch (int8 [M, K]) and
+ * sx_scratch (binary64 [M]), then kh_gemm_i8 runs with sa = sx_scratch
+ * (per row).  The decode-style entry point of config C5. */
+int kh_linear_i8(const float* x, int64_t M, int64_t K, const int8_t* b_packed, int64_t N,
+                 const double* sb, int sb_per_col, const float* bias,
+                 int8_t* q_scratch, double* sx_scratch, float* out);
+
+/* The epilogue alone, for an int8_matmul whose dequantize was not fused:
+ * out[i, j] = (float)((double)acc[i, j] * (sa_i * sb_j)) [+ bias[j]].
+ * quantize.py:76 applied to an accumulator. */
+int kh_dequantize_acc(const int32_t* acc, int64_t M, int64_t N, const double* sa, int sa_per_row,
+                      const double* sb, int sb_per_col, const float* bias, float* out);
+
+/* ---- fp32 matmul ------------------------------------------------------- */
+
+/* out (M, N) = a (M, K) @ b (K, N) [+ bias (N)], fp32 row-major; the
+ * signature of kan::metal::matmul / matmul_mps (MetalOps.hpp:27, 35) and
+ * kan::cpu::matmul (backend/cpu/src/Ops.cpp:322-339), with the bias add
+ * of Ops.cpp:34-38 fused when bias != NULL. */
+int kh_matmul_f32(const float* a, const float* b, float* out, int64_t M, int64_t K, int64_t N,
+                  const float* bias);
+
+/* ---- fp32 elementwise around the path ----------------------------------- */
+
+/* out[i] = a[i] + b[i]: kan::metal::add (MetalOps.hpp:51),
+ * kan::cpu::add (backend/cpu/src/Ops.cpp:22-24). */
+int kh_add(const float* a, const float* b, float* out, int64_t n);
+
+/* out[i, j] = x[i, j] + bias[j], then (v > 0 ? v : 0) when relu != 0:
+ * kan::metal::add_bias / bias_relu (MetalOps.hpp:37-43),
+ * kan::cpu::add_bias_broadcast (Ops.cpp:34-38), fused_bias_relu
+ * (backend/cpu/src/Fused.cpp:5-14). */
+int kh_add_bias(const float* x, const float* bias, float* out, int64_t batch, int64_t features, int relu);
+
+/* out[i] = x[i] > 0 ? x[i] : 0: kan::metal::relu (MetalOps.hpp:54),
+ * kan::cpu::relu_fwd (backend/cpu/src/Ops.cpp:197-199). */
+int kh_relu(const float* x, float* out, int64_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KANSAI_HIP_H */

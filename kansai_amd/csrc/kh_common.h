@@ -1,0 +1,66 @@
+// kh_common.h -- shared internals of the gfx950 HIP backend (not part of the
+// C ABI; the ABI is include/kansai_hip.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "kansai_hip.h"
+
+namespace kh {
+
+// ---- errors ---------------------------------------------------------------
+
+// Sets the calling thread's last-error text and returns `code`.
+int fail(int code, const std::string& msg);
+// Maps a HIP error to KH_ERR_HIP / KH_ERR_OOM with context; KH_OK if ok.
+int hip_status(hipError_t e, const char* what);
+// Checks the launch that just happened (hipGetLastError).
+int launch_status(const char* kernel);
+
+// ---- per-device state ------------------------------------------------------
+
+// Bits of the device fault word (set by kernels with a vector atomic OR,
+// read and cleared by kh_synchronize).
+constexpr unsigned kFaultNonFinite = 1u;
+
+struct Device {
+    int id = -1;
+    hipStream_t stream = nullptr;
+    unsigned* fault = nullptr;   // device word, see kFaultNonFinite
+    int cus = 0;
+};
+
+// The calling thread's current device, initialised on first use (device 0
+// unless kh_init chose another).  Returns nullptr and sets the last error
+// when no usable gfx950 device exists.
+Device* current();
+
+// A device scratch area of at least `bytes`, owned by the library, valid
+// until the next scratch() call on the same device.  All library work is
+// ordered on the device's single library stream, so consecutive calls
+// reuse it safely.  Returns nullptr (and sets the last error) on OOM.
+void* scratch(Device* d, size_t bytes);
+
+// ---- argument checks ---------------------------------------------------------
+
+__host__ __device__ inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+}  // namespace kh
+
+#define KH_REQUIRE(cond, msg)                                        \
+    do {                                                             \
+        if (!(cond)) return ::kh::fail(KH_ERR_INVALID_ARG, (msg));   \
+    } while (0)
+
+#define KH_DEVICE_OR_RETURN(d)                                       \
+    ::kh::Device* d = ::kh::current();                               \
+    if (!d) return KH_ERR_NO_DEVICE
+
+// Non-finite detection uses the IEEE bit pattern: for |v| (sign cleared) the
+// unsigned order of the bits is the numeric order, and every NaN/inf pattern
+// is >= 0x7F800000, so a max over bits finds both the absmax and any NaN.
+#define KH_NONFINITE_BITS 0x7F800000u

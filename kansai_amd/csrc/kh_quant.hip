@@ -1,0 +1,670 @@
+// kh_quant.hip -- symmetric int8 quantize / dequantize kernels for gfx950.
+//
+// Semantics are the reference's, bit for bit (python/kansai/quantize.py:66-70
+// and :76):
+//   m = max|v|;  s = m / 127.0 in binary64 (1.0 when m == 0);
+//   q = clamp(round_half_even(fl64(v / s)), -127, 127);
+//   dequantized = (float)((double)q * s).
+//
+// Exact division without paying a binary64 divide per element: with
+// rf = (float)(1.0 / s), the binary32 FMA a = fl32(v * rf + 1.5*2^23) rounds
+// the EXACT product v * rf to the nearest integer k (ties to even) and
+// d = fl32(v * rf - k) is its distance to k.  |v * rf - v / s| <= 7.6e-6 for
+// |v| <= m (rf carries one binary64 and one binary32 rounding, relative
+// 6e-8, on a quotient of magnitude <= 127.0000001), and fl64(v / s) is within
+// 1.5e-14 of v / s, so when |d| <= 0.5 - kTieEps (kTieEps = 2^-15, four
+// times that bound) k is the reference's round(fl64(v / s)).  Elements that
+// fail the test take the exact path: a correctly rounded binary64 divide and
+// rint (ties to even).  Rows whose max is below 2^-64 (where 127/m could
+// overflow binary32) take the exact path throughout.  The fast path cannot
+// leave [-127, 127] (|v * rf| <= 127 * (1 + 2^-23)), so only the exact path
+// clamps.
+//
+// Memory layout: x, q row-major contiguous; per-row kernels keep the whole
+// row in registers between the absmax and the quantize step, so each fp32
+// value crosses HBM once (5 bytes moved per element: 4 read + 1 written).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "kh_common.h"
+
+#pragma clang fp contract(off)
+
+namespace {
+
+// Native clang vectors (the nontemporal builtins reject HIP's struct vectors).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kTieEps = 1.0f / 32768.0f;
+// |v * rf - k| <= kFastHalf  <=>  v * rf is at least kTieEps from a half-integer.
+constexpr float kFastHalf = 0.5f - kTieEps;
+constexpr unsigned kFastMinBits = 0x1F800000u;  // 2^-64
+// 1.5 * 2^23: for |x| < 2^22, fl32(x + kMagic) = kMagic + rint(x) (binary32
+// spacing is 1 there; kMagic is even so ties go to the even integer), and the
+// low byte of its bit pattern is rint(x) as a two's-complement int8.
+constexpr float kMagic = 12582912.0f;
+
+__device__ __forceinline__ unsigned abs_bits(float v) { return __float_as_uint(v) & 0x7FFFFFFFu; }
+
+// Running absmax over raw bit patterns without masking each value: the
+// unsigned max is dominated by negative values (sign bit set) and the signed
+// max by positive ones.  Both keep NaN/inf patterns, which compare above
+// every finite magnitude.
+struct AbsMax {
+    unsigned umax = 0;
+    int smax = 0;
+    __device__ __forceinline__ void add4(f32x4 v) {
+        const unsigned b0 = __float_as_uint(v.x), b1 = __float_as_uint(v.y);
+        const unsigned b2 = __float_as_uint(v.z), b3 = __float_as_uint(v.w);
+        umax = max(umax, max(max(b0, b1), max(b2, b3)));
+        smax = max(smax, max(max((int)b0, (int)b1), max((int)b2, (int)b3)));
+    }
+    __device__ __forceinline__ void add1(float v) {
+        const unsigned b = __float_as_uint(v);
+        umax = max(umax, b);
+        smax = max(smax, (int)b);
+    }
+    // |max| as bits (>= 0x7F800000 if any value was NaN or inf).
+    __device__ __forceinline__ unsigned bits() const { return max(umax & 0x7FFFFFFFu, (unsigned)max(smax, 0)); }
+};
+
+__device__ __forceinline__ unsigned wave_max(unsigned v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = max(v, (unsigned)__shfl_xor((int)v, off, 64));
+    return v;
+}
+
+struct Scale {
+    double s;    // the reference's binary64 scale
+    float rf;    // binary32 reciprocal for the fast path
+    bool fast;   // fast path allowed for this slice
+    bool bad;    // slice holds NaN or +-inf
+};
+
+// quantize.py:67-68 from the absmax bit pattern.
+__device__ __forceinline__ Scale make_scale(unsigned mbits) {
+    Scale r;
+    r.bad = mbits >= KH_NONFINITE_BITS;
+    const float m = __uint_as_float(mbits);
+    r.s = r.bad ? __longlong_as_double(0x7FF8000000000000LL) : (m > 0.0f ? (double)m / 127.0 : 1.0);
+    r.rf = r.bad ? 0.0f : (float)(1.0 / r.s);
+    r.fast = !r.bad && mbits >= kFastMinBits;
+    return r;
+}
+
+__device__ __forceinline__ void flag_nonfinite(unsigned* fault) { atomicOr(fault, kh::kFaultNonFinite); }
+
+// quantize.py:69 exactly: binary64 divide, rint (ties to even), clamp.
+__device__ __forceinline__ int quant_exact(float v, double s) {
+    const int q = (int)rint((double)v / s);
+    return min(127, max(-127, q));
+}
+
+// Fast path for one value: a's low byte is the code; `ok` is cleared when
+// the exact path is needed.
+__device__ __forceinline__ unsigned quant_fast(float v, float rf, bool& ok) {
+    const float a = __builtin_fmaf(v, rf, kMagic);
+    const float d = __builtin_fmaf(v, rf, -(a - kMagic));
+    ok = ok && (fabsf(d) <= kFastHalf);
+    return __float_as_uint(a);
+}
+
+__device__ __forceinline__ int quant_one(float v, const Scale& sc) {
+    if (sc.bad) return 0;
+    if (sc.fast) {
+        bool ok = true;
+        const unsigned a = quant_fast(v, sc.rf, ok);
+        if (ok) return (int)(int8_t)(a & 0xFFu);
+    }
+    return quant_exact(v, sc.s);
+}
+
+// Four values -> four packed codes (byte e = code of v[e]) by the fast path.
+__device__ __forceinline__ unsigned pack4_fast(f32x4 v, float rf, bool& ok) {
+    const unsigned a0 = quant_fast(v.x, rf, ok);
+    const unsigned a1 = quant_fast(v.y, rf, ok);
+    const unsigned a2 = quant_fast(v.z, rf, ok);
+    const unsigned a3 = quant_fast(v.w, rf, ok);
+    // v_perm_b32: byte 0 of each source into bytes 0..3.
+    return __builtin_amdgcn_perm(a1, a0, 0x0c0c0400u) | __builtin_amdgcn_perm(a3, a2, 0x04000c0cu);
+}
+
+// Four values -> four packed codes, each by the fast path where it is
+// decisive and by the exact path otherwise.
+__device__ __forceinline__ unsigned pack4_checked(f32x4 v, const Scale& sc) {
+    if (sc.bad) return 0u;
+    const unsigned b0 = (unsigned)(quant_one(v.x, sc) & 0xFF);
+    const unsigned b1 = (unsigned)(quant_one(v.y, sc) & 0xFF);
+    const unsigned b2 = (unsigned)(quant_one(v.z, sc) & 0xFF);
+    const unsigned b3 = (unsigned)(quant_one(v.w, sc) & 0xFF);
+    return b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+}
+
+__device__ __forceinline__ unsigned pack4(f32x4 v, const Scale& sc) {
+    if (sc.fast) {
+        bool ok = true;
+        const unsigned w = pack4_fast(v, sc.rf, ok);
+        if (ok) return w;
+    }
+    return pack4_checked(v, sc);
+}
+
+// ---------------------------------------------------------------------------
+// Per-row quantize, row held in registers.  ROW_THREADS = 64 * WAVES_PER_ROW
+// threads own one row; a 256-thread block owns 256 / ROW_THREADS rows.
+// Requires cols % 4 == 0, x 16-byte and q 4-byte aligned, cols <= ROW_THREADS * 4 * VPT.
+// ---------------------------------------------------------------------------
+// Buffer resources (V#) over one row: loads beyond num_records return 0 and
+// stores beyond it are dropped, so the row edge needs no per-access test,
+// and each access needs one VGPR offset (the per-step offset is an SGPR).
+constexpr int kBufferFlags = 0x00020000;  // dword 3 of a raw gfx9 buffer resource (32-bit data)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* base, int64_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kBufferFlags);
+}
+
+template <int WAVES_PER_ROW, int VPT>
+__global__ __launch_bounds__(256) void quant_rows_reg_kernel(const float* __restrict__ x, int8_t* __restrict__ q,
+                                                             double* __restrict__ scales, int64_t rows,
+                                                             int64_t cols, unsigned* __restrict__ fault) {
+    constexpr int ROW_THREADS = 64 * WAVES_PER_ROW;
+    constexpr int ROWS_PER_BLOCK = 256 / ROW_THREADS;
+    __shared__ unsigned red[4];
+    const int lt = threadIdx.x % ROW_THREADS;
+    const int sub = threadIdx.x / ROW_THREADS;
+    const int64_t row = (int64_t)blockIdx.x * ROWS_PER_BLOCK + sub;
+    const bool active = row < rows;
+    // An inactive slot (past the last row) gets an empty resource: loads read 0.
+    const __amdgpu_buffer_rsrc_t xr = row_rsrc(x + (active ? row : 0) * cols, active ? cols * 4 : 0);
+
+    f32x4 v[VPT];
+    AbsMax am;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        v[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, lt * 16, i * ROW_THREADS * 16, 0));
+        am.add4(v[i]);
+    }
+    unsigned mb = wave_max(am.bits());
+    if (WAVES_PER_ROW > 1) {
+        const int w = threadIdx.x / 64;
+        if ((threadIdx.x & 63) == 0) red[w] = mb;
+        __syncthreads();
+        const int w0 = sub * WAVES_PER_ROW;
+        mb = red[w0];
+#pragma unroll
+        for (int i = 1; i < WAVES_PER_ROW; ++i) mb = max(mb, red[w0 + i]);
+    }
+    if (!active) return;
+    const Scale sc = make_scale(mb);
+    if (lt == 0) {
+        scales[row] = sc.s;
+        if (sc.bad) flag_nonfinite(fault);
+    }
+    // Fast path for every element, stored as it is produced; the registers
+    // holding the row die group by group.  Threads with an undecided element
+    // (about one wave in five) then redo their groups from memory.
+    const __amdgpu_buffer_rsrc_t qr = row_rsrc(q + row * cols, cols);
+    bool ok = sc.fast;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i)
+        __builtin_amdgcn_raw_buffer_store_b32(pack4_fast(v[i], sc.rf, ok), qr, lt * 4, i * ROW_THREADS * 4, 0);
+    if (!ok) {
+#pragma unroll 1
+        for (int i = 0; i < VPT; ++i) {
+            const f32x4 vv = __builtin_bit_cast(
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, lt * 16, i * ROW_THREADS * 16, 0));
+            __builtin_amdgcn_raw_buffer_store_b32(pack4(vv, sc), qr, lt * 4, i * ROW_THREADS * 4, 0);
+        }
+    }
+}
+
+// Per-row quantize for any shape/alignment: one block per row, two passes
+// (the second pass re-reads the row, normally from L2).
+__global__ __launch_bounds__(256) void quant_rows_generic_kernel(const float* __restrict__ x, int8_t* __restrict__ q,
+                                                                 double* __restrict__ scales, int64_t cols,
+                                                                 unsigned* __restrict__ fault) {
+    __shared__ unsigned red[4];
+    const int64_t row = blockIdx.x;
+    const float* xr = x + row * cols;
+    AbsMax am;
+    for (int64_t c = threadIdx.x; c < cols; c += 256) am.add1(xr[c]);
+    unsigned mb = wave_max(am.bits());
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x / 64] = mb;
+    __syncthreads();
+    mb = max(max(red[0], red[1]), max(red[2], red[3]));
+    const Scale sc = make_scale(mb);
+    if (threadIdx.x == 0) {
+        scales[row] = sc.s;
+        if (sc.bad) flag_nonfinite(fault);
+    }
+    int8_t* qr = q + row * cols;
+    for (int64_t c = threadIdx.x; c < cols; c += 256) qr[c] = (int8_t)quant_one(xr[c], sc);
+}
+
+// ---------------------------------------------------------------------------
+// Per-tensor quantize: pass 1 writes one absmax (as bits) per block into
+// `partials`; pass 2 reduces the partials in every block, then quantizes.
+// VEC: x 16-byte aligned and q 4-byte aligned (float4 body, scalar tail).
+// ---------------------------------------------------------------------------
+template <bool VEC>
+__global__ __launch_bounds__(256) void absmax_partials_kernel(const float* __restrict__ x, int64_t n,
+                                                              unsigned* __restrict__ partials) {
+    __shared__ unsigned red[4];
+    AbsMax am;
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    if (VEC) {
+        const int64_t n4 = n >> 2;
+        const f32x4* x4 = reinterpret_cast<const f32x4*>(x);
+        for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride) am.add4(x4[i]);
+        if (blockIdx.x == 0)
+            for (int64_t i = n4 * 4 + threadIdx.x; i < n; i += 256) am.add1(x[i]);
+    } else {
+        for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) am.add1(x[i]);
+    }
+    unsigned mb = wave_max(am.bits());
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x / 64] = mb;
+    __syncthreads();
+    if (threadIdx.x == 0) partials[blockIdx.x] = max(max(red[0], red[1]), max(red[2], red[3]));
+}
+
+// Reduces partials[0..count) across the block; every thread gets the max.
+__device__ __forceinline__ unsigned block_reduce_partials(const unsigned* __restrict__ partials, int count,
+                                                          unsigned* red) {
+    unsigned mb = 0;
+    for (int i = threadIdx.x; i < count; i += blockDim.x) mb = max(mb, partials[i]);
+    mb = wave_max(mb);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x / 64] = mb;
+    __syncthreads();
+    mb = red[0];
+    for (int i = 1; i < (int)(blockDim.x / 64); ++i) mb = max(mb, red[i]);
+    return mb;
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void quant_tensor_kernel(const float* __restrict__ x, int64_t n,
+                                                           int8_t* __restrict__ q, double* __restrict__ scale,
+                                                           const unsigned* __restrict__ partials, int nparts,
+                                                           unsigned* __restrict__ fault) {
+    __shared__ unsigned red[4];
+    const unsigned mb = block_reduce_partials(partials, nparts, red);
+    const Scale sc = make_scale(mb);
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        scale[0] = sc.s;
+        if (sc.bad) flag_nonfinite(fault);
+    }
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    if (VEC) {
+        const int64_t n4 = n >> 2;
+        const f32x4* x4 = reinterpret_cast<const f32x4*>(x);
+        unsigned* q4 = reinterpret_cast<unsigned*>(q);
+        for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride) q4[i] = pack4(x4[i], sc);
+        if (blockIdx.x == 0)
+            for (int64_t i = n4 * 4 + threadIdx.x; i < n; i += 256) q[i] = (int8_t)quant_one(x[i], sc);
+    } else {
+        for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) q[i] = (int8_t)quant_one(x[i], sc);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Per-column (per output channel) absmax of a [k, n] weight, and the
+// transpose-quantize that packs codes K-contiguous ([n, k]).
+// ---------------------------------------------------------------------------
+__global__ void fill_u32_kernel(unsigned* __restrict__ p, int64_t count, unsigned value) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < count) p[i] = value;
+}
+
+constexpr int kColRowsPerBlock = 128;
+
+__global__ __launch_bounds__(256) void col_absmax_kernel(const float* __restrict__ w, int64_t k, int64_t n,
+                                                         unsigned* __restrict__ colmax) {
+    const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (j >= n) return;
+    const int64_t i0 = (int64_t)blockIdx.y * kColRowsPerBlock;
+    const int64_t i1 = min(k, i0 + kColRowsPerBlock);
+    AbsMax am;
+    for (int64_t i = i0; i < i1; ++i) am.add1(w[i * n + j]);
+    atomicMax(colmax + j, am.bits());
+}
+
+constexpr int kTile = 64;
+
+// PER_COL: maxbits = colmax[n]; otherwise maxbits = partials[nparts] reduced
+// to one per-tensor absmax.  Writes q_packed[j * k + i] and the scales.
+template <bool PER_COL>
+__global__ __launch_bounds__(256) void pack_quant_kernel(const float* __restrict__ w, int64_t k, int64_t n,
+                                                         const unsigned* __restrict__ maxbits, int nparts,
+                                                         int8_t* __restrict__ qp, double* __restrict__ scales,
+                                                         unsigned* __restrict__ fault) {
+    __shared__ __attribute__((aligned(16))) int8_t tile[kTile][kTile + 4];
+    __shared__ double s_col[kTile];
+    __shared__ float rf_col[kTile];
+    __shared__ unsigned char flags_col[kTile];  // bit0 fast, bit1 bad
+    __shared__ unsigned red[4];
+    const int64_t i0 = (int64_t)blockIdx.y * kTile;
+    const int64_t j0 = (int64_t)blockIdx.x * kTile;
+    const int t = threadIdx.x;
+
+    if (PER_COL) {
+        if (t < kTile) {
+            const int64_t j = j0 + t;
+            const Scale sc = make_scale(j < n ? maxbits[j] : 0u);
+            s_col[t] = sc.s;
+            rf_col[t] = sc.rf;
+            flags_col[t] = (sc.fast ? 1 : 0) | (sc.bad ? 2 : 0);
+            if (blockIdx.y == 0 && j < n) {
+                scales[j] = sc.s;
+                if (sc.bad) flag_nonfinite(fault);
+            }
+        }
+    } else {
+        const unsigned mb = block_reduce_partials(maxbits, nparts, red);
+        const Scale sc = make_scale(mb);
+        if (t < kTile) {
+            s_col[t] = sc.s;
+            rf_col[t] = sc.rf;
+            flags_col[t] = (sc.fast ? 1 : 0) | (sc.bad ? 2 : 0);
+        }
+        if (blockIdx.x == 0 && blockIdx.y == 0 && t == 0) {
+            scales[0] = sc.s;
+            if (sc.bad) flag_nonfinite(fault);
+        }
+    }
+    __syncthreads();
+
+    // Read: thread (r = t / 64, c = t % 64) covers rows r, r+4, ..., column c.
+    const int c = t & 63;
+    const int r0 = t >> 6;
+    Scale sc;
+    sc.s = s_col[c];
+    sc.rf = rf_col[c];
+    sc.fast = flags_col[c] & 1;
+    sc.bad = flags_col[c] & 2;
+    const int64_t j = j0 + c;
+#pragma unroll 4
+    for (int r = r0; r < kTile; r += 4) {
+        const int64_t i = i0 + r;
+        int code = 0;
+        if (i < k && j < n) code = quant_one(w[i * n + j], sc);
+        tile[c][r] = (int8_t)code;
+    }
+    __syncthreads();
+
+    // Write: thread (jj = t / 4, part = t % 4) writes 16 consecutive k of column j0 + jj.
+    const int jj = t >> 2;
+    const int ii = (t & 3) * 16;
+    const int64_t jo = j0 + jj;
+    if (jo >= n) return;
+    const int64_t io = i0 + ii;
+    int8_t* dst = qp + jo * k + io;
+    if (io + 16 <= k && kh::aligned(dst, 16)) {
+        uint4 v;
+        v.x = *reinterpret_cast<const unsigned*>(&tile[jj][ii + 0]);
+        v.y = *reinterpret_cast<const unsigned*>(&tile[jj][ii + 4]);
+        v.z = *reinterpret_cast<const unsigned*>(&tile[jj][ii + 8]);
+        v.w = *reinterpret_cast<const unsigned*>(&tile[jj][ii + 12]);
+        *reinterpret_cast<uint4*>(dst) = v;
+    } else {
+        for (int e = 0; e < 16 && io + e < k; ++e) dst[e] = tile[jj][ii + e];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Dequantize (quantize.py:76): out = (float)((double)q * s).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float deq_one(int8_t q, double s) { return (float)((double)q * s); }
+
+__device__ __forceinline__ f32x4 deq4(unsigned w, double s) {
+    return f32x4{deq_one((int8_t)(w & 0xFF), s), deq_one((int8_t)((w >> 8) & 0xFF), s),
+                 deq_one((int8_t)((w >> 16) & 0xFF), s), deq_one((int8_t)(w >> 24), s)};
+}
+
+// Vector dequantize.  Block (bx, row) covers kDeqPerBlock consecutive codes of
+// one row (per-row scale uniform over the block; per-tensor: rows == 1).
+// Each lane reads 4 codes (one u32) and writes one 16-byte float4 per step,
+// so every load and store instruction covers a contiguous span of the wave.
+// Requires cols % 4 == 0, q 4-byte and out 16-byte aligned.
+constexpr int kDeqSteps = 4;
+constexpr int kDeqPerBlock = 256 * 4 * kDeqSteps;
+
+__global__ __launch_bounds__(256) void dequant_vec_kernel(const int8_t* __restrict__ q, int64_t cols,
+                                                          const double* __restrict__ scales, int per_row,
+                                                          float* __restrict__ out) {
+    const int64_t row = blockIdx.y;
+    const double s = scales[per_row ? row : 0];
+    const int64_t c4 = cols >> 2;
+    const unsigned* qr = reinterpret_cast<const unsigned*>(q + row * cols);
+    f32x4* orow = reinterpret_cast<f32x4*>(out + row * cols);
+    const int64_t base = (int64_t)blockIdx.x * (kDeqPerBlock / 4) + threadIdx.x;
+#pragma unroll
+    for (int step = 0; step < kDeqSteps; ++step) {
+        const int64_t i = base + step * 256;
+        if (i < c4) __builtin_nontemporal_store(deq4(__builtin_nontemporal_load(qr + i), s), orow + i);
+    }
+}
+
+// Any shape / alignment.
+__global__ __launch_bounds__(256) void dequant_generic_kernel(const int8_t* __restrict__ q, int64_t n, int64_t cols,
+                                                              const double* __restrict__ scales, int per_row,
+                                                              float* __restrict__ out) {
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride)
+        out[i] = deq_one(q[i], scales[per_row ? i / cols : 0]);
+}
+
+// out[i, j] = (float)((double)qp[j * k + i] * s_j), back to the [k, n] layout.
+__global__ __launch_bounds__(256) void dequant_packed_kernel(const int8_t* __restrict__ qp, int64_t k, int64_t n,
+                                                             const double* __restrict__ scales, int64_t scales_n,
+                                                             float* __restrict__ out) {
+    __shared__ __attribute__((aligned(16))) int8_t tile[kTile][kTile + 4];
+    const int64_t i0 = (int64_t)blockIdx.y * kTile;
+    const int64_t j0 = (int64_t)blockIdx.x * kTile;
+    const int t = threadIdx.x;
+    // Read codes: thread (jj = t / 4) reads 16 k of column j0 + jj.
+    {
+        const int jj = t >> 2;
+        const int ii = (t & 3) * 16;
+        for (int e = 0; e < 16; ++e) {
+            const int64_t i = i0 + ii + e, j = j0 + jj;
+            tile[jj][ii + e] = (i < k && j < n) ? qp[j * k + i] : (int8_t)0;
+        }
+    }
+    __syncthreads();
+    const int c = t & 63;
+    const int64_t j = j0 + c;
+    if (j >= n) return;
+    const double s = scales[scales_n == 1 ? 0 : j];
+    for (int r = t >> 6; r < kTile; r += 4) {
+        const int64_t i = i0 + r;
+        if (i < k) out[i * n + j] = deq_one(tile[c][r], s);
+    }
+}
+
+int grid_for(int64_t work_items, int per_thread, int cap) {
+    int64_t g = (work_items + 256LL * per_thread - 1) / (256LL * per_thread);
+    if (g < 1) g = 1;
+    if (g > cap) g = cap;
+    return (int)g;
+}
+
+constexpr int kMaxPartials = 1024;
+
+}  // namespace
+
+
+namespace {
+
+__global__ void fill_f64_kernel(double* __restrict__ p, int64_t count, double value) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < count) p[i] = value;
+}
+
+// Empty slices: max() defaults to 0.0, so the scale is 1.0 (quantize.py:67-68).
+int fill_scales_one(kh::Device* d, double* scales, int64_t count) {
+    fill_f64_kernel<<<(unsigned)((count + 255) / 256), 256, 0, d->stream>>>(scales, count, 1.0);
+    return kh::launch_status("fill_f64");
+}
+
+// Pass 1 of a per-tensor quantize: per-block absmax bits into library scratch.
+int tensor_absmax(kh::Device* d, const float* x, int64_t n, bool vec, unsigned** partials, int* nparts) {
+    const int g = grid_for(vec ? (n >> 2) : n, 8, kMaxPartials);
+    unsigned* p = static_cast<unsigned*>(kh::scratch(d, kMaxPartials * sizeof(unsigned)));
+    if (!p) return KH_ERR_OOM;
+    if (vec)
+        absmax_partials_kernel<true><<<g, 256, 0, d->stream>>>(x, n, p);
+    else
+        absmax_partials_kernel<false><<<g, 256, 0, d->stream>>>(x, n, p);
+    *partials = p;
+    *nparts = g;
+    return kh::launch_status("absmax_partials");
+}
+
+}  // namespace
+
+extern "C" {
+
+int kh_quantize_tensor(const float* x, int64_t n, int8_t* q, double* scale) {
+    KH_REQUIRE(n >= 0, "kh_quantize_tensor: negative size");
+    KH_REQUIRE(scale, "kh_quantize_tensor: null scale");
+    KH_REQUIRE(n == 0 || (x && q), "kh_quantize_tensor: null pointer");
+    KH_DEVICE_OR_RETURN(d);
+    if (n == 0) return fill_scales_one(d, scale, 1);
+    const bool vec = kh::aligned(x, 16) && kh::aligned(q, 4);
+    unsigned* partials = nullptr;
+    int nparts = 0;
+    int rc = tensor_absmax(d, x, n, vec, &partials, &nparts);
+    if (rc) return rc;
+    const int g = grid_for(vec ? (n >> 2) : n, 8, 8192);
+    if (vec)
+        quant_tensor_kernel<true><<<g, 256, 0, d->stream>>>(x, n, q, scale, partials, nparts, d->fault);
+    else
+        quant_tensor_kernel<false><<<g, 256, 0, d->stream>>>(x, n, q, scale, partials, nparts, d->fault);
+    return kh::launch_status("quant_tensor");
+}
+
+int kh_quantize_rows(const float* x, int64_t rows, int64_t cols, int8_t* q, double* scales) {
+    KH_REQUIRE(rows >= 0 && cols >= 0, "kh_quantize_rows: negative shape");
+    if (rows == 0) return KH_OK;
+    KH_REQUIRE(scales, "kh_quantize_rows: null scales");
+    KH_REQUIRE(cols == 0 || (x && q), "kh_quantize_rows: null pointer");
+    KH_REQUIRE(rows <= 0x7FFFFFFFLL, "kh_quantize_rows: too many rows");
+    KH_DEVICE_OR_RETURN(d);
+    if (cols == 0) return fill_scales_one(d, scales, rows);
+    const bool vec = (cols % 4 == 0) && kh::aligned(x, 16) && kh::aligned(q, 4);
+    const unsigned per_row = (unsigned)rows;
+    const unsigned four_rows = (unsigned)((rows + 3) / 4);
+    if (vec && cols <= 256)
+        quant_rows_reg_kernel<1, 1><<<four_rows, 256, 0, d->stream>>>(x, q, scales, rows, cols, d->fault);
+    else if (vec && cols <= 1024)
+        quant_rows_reg_kernel<1, 4><<<four_rows, 256, 0, d->stream>>>(x, q, scales, rows, cols, d->fault);
+    else if (vec && cols <= 4096)
+        quant_rows_reg_kernel<4, 4><<<per_row, 256, 0, d->stream>>>(x, q, scales, rows, cols, d->fault);
+    else if (vec && cols <= 16384)
+        quant_rows_reg_kernel<4, 16><<<per_row, 256, 0, d->stream>>>(x, q, scales, rows, cols, d->fault);
+    else if (vec && cols <= 32768)
+        quant_rows_reg_kernel<4, 32><<<per_row, 256, 0, d->stream>>>(x, q, scales, rows, cols, d->fault);
+    else
+        quant_rows_generic_kernel<<<per_row, 256, 0, d->stream>>>(x, q, scales, cols, d->fault);
+    return kh::launch_status("quant_rows");
+}
+
+static int quantize_packed(const float* w, int64_t k, int64_t n, int8_t* qp, double* scales, bool per_col) {
+    KH_DEVICE_OR_RETURN(d);
+    const unsigned gx = (unsigned)((n + kTile - 1) / kTile);
+    const unsigned gy = (unsigned)((k + kTile - 1) / kTile);
+    if (per_col) {
+        unsigned* colmax = static_cast<unsigned*>(kh::scratch(d, (size_t)n * sizeof(unsigned)));
+        if (!colmax) return KH_ERR_OOM;
+        fill_u32_kernel<<<(unsigned)((n + 255) / 256), 256, 0, d->stream>>>(colmax, n, 0u);
+        dim3 g1((unsigned)((n + 255) / 256), (unsigned)((k + kColRowsPerBlock - 1) / kColRowsPerBlock));
+        col_absmax_kernel<<<g1, 256, 0, d->stream>>>(w, k, n, colmax);
+        pack_quant_kernel<true><<<dim3(gx, gy), 256, 0, d->stream>>>(w, k, n, colmax, 0, qp, scales, d->fault);
+    } else {
+        unsigned* partials = nullptr;
+        int nparts = 0;
+        int rc = tensor_absmax(d, w, k * n, kh::aligned(w, 16), &partials, &nparts);
+        if (rc) return rc;
+        pack_quant_kernel<false><<<dim3(gx, gy), 256, 0, d->stream>>>(w, k, n, partials, nparts, qp, scales, d->fault);
+    }
+    return kh::launch_status("pack_quant");
+}
+
+int kh_quantize_cols_packed(const float* w, int64_t k, int64_t n, int8_t* q_packed, double* scales) {
+    KH_REQUIRE(k >= 0 && n >= 0, "kh_quantize_cols_packed: negative shape");
+    if (n == 0) return KH_OK;
+    KH_REQUIRE(scales, "kh_quantize_cols_packed: null scales");
+    if (k == 0) {
+        KH_DEVICE_OR_RETURN(d);
+        return fill_scales_one(d, scales, n);
+    }
+    KH_REQUIRE(w && q_packed, "kh_quantize_cols_packed: null pointer");
+    KH_REQUIRE(n <= 0x7FFFFFFFLL * 64 && k <= 0xFFFFLL * 64, "kh_quantize_cols_packed: shape too large");
+    return quantize_packed(w, k, n, q_packed, scales, true);
+}
+
+int kh_quantize_tensor_packed(const float* w, int64_t k, int64_t n, int8_t* q_packed, double* scale) {
+    KH_REQUIRE(k >= 0 && n >= 0, "kh_quantize_tensor_packed: negative shape");
+    KH_REQUIRE(scale, "kh_quantize_tensor_packed: null scale");
+    if (k == 0 || n == 0) {
+        KH_DEVICE_OR_RETURN(d);
+        return fill_scales_one(d, scale, 1);
+    }
+    KH_REQUIRE(w && q_packed, "kh_quantize_tensor_packed: null pointer");
+    KH_REQUIRE(n <= 0x7FFFFFFFLL * 64 && k <= 0xFFFFLL * 64, "kh_quantize_tensor_packed: shape too large");
+    return quantize_packed(w, k, n, q_packed, scale, false);
+}
+
+static int dequant(const int8_t* q, int64_t rows, int64_t cols, const double* scales, float* out, bool per_row) {
+    KH_DEVICE_OR_RETURN(d);
+    const bool vec = (cols % 4 == 0) && kh::aligned(q, 4) && kh::aligned(out, 16);
+    if (vec && rows <= 0x7FFFFFFFLL && (cols + kDeqPerBlock - 1) / kDeqPerBlock <= 0x7FFFFFFFLL) {
+        dim3 g((unsigned)((cols + kDeqPerBlock - 1) / kDeqPerBlock), (unsigned)rows);
+        if (rows > 65535) {
+            // grid.y is limited to 65535: walk the rows in slabs.
+            for (int64_t r0 = 0; r0 < rows; r0 += 65535) {
+                const int64_t nr = min((int64_t)65535, rows - r0);
+                dim3 gs(g.x, (unsigned)nr);
+                dequant_vec_kernel<<<gs, 256, 0, d->stream>>>(q + r0 * cols, cols, scales + (per_row ? r0 : 0),
+                                                            per_row ? 1 : 0, out + r0 * cols);
+            }
+        } else {
+            dequant_vec_kernel<<<g, 256, 0, d->stream>>>(q, cols, scales, per_row ? 1 : 0, out);
+        }
+    } else {
+        const int64_t n = rows * cols;
+        const int g = grid_for(n, 16, 16384);
+        dequant_generic_kernel<<<g, 256, 0, d->stream>>>(q, n, cols, scales, per_row ? 1 : 0, out);
+    }
+    return kh::launch_status("dequant");
+}
+
+int kh_dequantize_tensor(const int8_t* q, int64_t n, const double* scale, float* out) {
+    KH_REQUIRE(n >= 0, "kh_dequantize_tensor: negative size");
+    if (n == 0) return KH_OK;
+    KH_REQUIRE(q && scale && out, "kh_dequantize_tensor: null pointer");
+    return dequant(q, 1, n, scale, out, false);
+}
+
+int kh_dequantize_rows(const int8_t* q, int64_t rows, int64_t cols, const double* scales, float* out) {
+    KH_REQUIRE(rows >= 0 && cols >= 0, "kh_dequantize_rows: negative shape");
+    if (rows == 0 || cols == 0) return KH_OK;
+    KH_REQUIRE(q && scales && out, "kh_dequantize_rows: null pointer");
+    return dequant(q, rows, cols, scales, out, true);
+}
+
+int kh_dequantize_packed(const int8_t* q_packed, int64_t k, int64_t n, const double* scales, int64_t scales_n,
+                         float* out) {
+    KH_REQUIRE(k >= 0 && n >= 0, "kh_dequantize_packed: negative shape");
+    if (k == 0 || n == 0) return KH_OK;
+    KH_REQUIRE(q_packed && scales && out, "kh_dequantize_packed: null pointer");
+    KH_REQUIRE(scales_n == 1 || scales_n == n, "kh_dequantize_packed: scales_n must be 1 or n");
+    KH_REQUIRE(n <= 0x7FFFFFFFLL * 64 && k <= 0xFFFFLL * 64, "kh_dequantize_packed: shape too large");
+    KH_DEVICE_OR_RETURN(d);
+    dim3 g((unsigned)((n + kTile - 1) / kTile), (unsigned)((k + kTile - 1) / kTile));
+    dequant_packed_kernel<<<g, 256, 0, d->stream>>>(q_packed, k, n, scales, scales_n, out);
+    return kh::launch_status("dequant_packed");
+}
+
+}  // extern "C"

@@ -1,0 +1,357 @@
+// kh_runtime.hip -- device selection, errors, the device memory pool, copies,
+// events and deferred-error reporting for the gfx950 backend.
+//
+// Replaces, for device memory, the reference's page-aligned host Storage
+// (core/src/Storage.cpp:22-32) and its first-fit StoragePool
+// (core/src/StoragePool.cpp:5-24): a graph run repeatedly through the KIR
+// memory planner draws its intermediates from here and, after the first
+// run, never calls hipMalloc again.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "kh_common.h"
+
+namespace kh {
+
+namespace {
+
+thread_local std::string t_last_error;
+thread_local int t_device = -1;
+
+constexpr int kMaxDevices = 16;
+
+struct Pool {
+    std::mutex mu;
+    std::unordered_map<size_t, std::vector<void*>> free_lists;  // size class -> blocks
+    std::unordered_map<void*, size_t> live;                     // block -> size class
+    size_t in_use = 0;
+    size_t cached = 0;
+    size_t driver_allocs = 0;
+};
+
+struct DeviceSlot {
+    Device dev;
+    Pool pool;
+    std::mutex scratch_mu;
+    void* scratch = nullptr;
+    size_t scratch_bytes = 0;
+    bool ready = false;
+};
+
+std::mutex g_init_mu;
+DeviceSlot g_slots[kMaxDevices];
+
+// Size classes: 256-byte granules up to 1 MiB, 64 KiB granules above.  A
+// graph replays the same sizes every call, so exact-class reuse converges
+// after one run (the reasoning of the reference's plan_memory docstring,
+// python/kansai/kir.py:918-925).
+size_t size_class(size_t bytes) {
+    if (bytes == 0) bytes = 1;
+    const size_t g = bytes <= (1u << 20) ? 256 : (64u << 10);
+    return (bytes + g - 1) / g * g;
+}
+
+bool is_gfx950(int dev) {
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, dev) != hipSuccess) return false;
+    return std::strncmp(p.gcnArchName, "gfx950", 6) == 0;
+}
+
+int init_slot(int dev) {
+    DeviceSlot& s = g_slots[dev];
+    if (s.ready) return KH_OK;
+    int rc = hip_status(hipSetDevice(dev), "hipSetDevice");
+    if (rc) return rc;
+    hipDeviceProp_t p;
+    rc = hip_status(hipGetDeviceProperties(&p, dev), "hipGetDeviceProperties");
+    if (rc) return rc;
+    s.dev.id = dev;
+    s.dev.cus = p.multiProcessorCount;
+    // Default priority on purpose (all streams at one priority).
+    rc = hip_status(hipStreamCreateWithFlags(&s.dev.stream, hipStreamNonBlocking), "hipStreamCreate");
+    if (rc) return rc;
+    rc = hip_status(hipMalloc(reinterpret_cast<void**>(&s.dev.fault), 256), "hipMalloc(fault word)");
+    if (rc) return rc;
+    rc = hip_status(hipMemset(s.dev.fault, 0, 256), "hipMemset(fault word)");
+    if (rc) return rc;
+    s.ready = true;
+    return KH_OK;
+}
+
+}  // namespace
+
+int fail(int code, const std::string& msg) {
+    t_last_error = msg;
+    return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+    if (e == hipSuccess) return KH_OK;
+    const int code = (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) ? KH_ERR_OOM : KH_ERR_HIP;
+    return fail(code, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+int launch_status(const char* kernel) {
+    return hip_status(hipGetLastError(), kernel);
+}
+
+Device* current() {
+    int dev = t_device < 0 ? 0 : t_device;
+    {
+        std::lock_guard<std::mutex> lk(g_init_mu);
+        if (!g_slots[dev].ready) {
+            int n = 0;
+            if (hipGetDeviceCount(&n) != hipSuccess || n <= dev) {
+                fail(KH_ERR_NO_DEVICE, "kansai_hip: no HIP device available");
+                return nullptr;
+            }
+            if (!is_gfx950(dev)) {
+                fail(KH_ERR_NO_DEVICE, "kansai_hip: device is not gfx950 (MI355X); this backend targets gfx950 only");
+                return nullptr;
+            }
+            if (init_slot(dev) != KH_OK) return nullptr;
+        }
+    }
+    if (t_device != dev) {
+        if (hipSetDevice(dev) != hipSuccess) {
+            fail(KH_ERR_HIP, "hipSetDevice failed");
+            return nullptr;
+        }
+        t_device = dev;
+    }
+    return &g_slots[dev].dev;
+}
+
+void* scratch(Device* d, size_t bytes) {
+    DeviceSlot& s = g_slots[d->id];
+    std::lock_guard<std::mutex> lk(s.scratch_mu);
+    if (bytes <= s.scratch_bytes) return s.scratch;
+    size_t want = bytes < (1u << 20) ? (1u << 20) : size_class(bytes);
+    if (s.scratch) {
+        // The old area may still be read by queued work.
+        if (hipStreamSynchronize(d->stream) != hipSuccess) {
+            fail(KH_ERR_HIP, "hipStreamSynchronize before growing scratch");
+            return nullptr;
+        }
+        (void)hipFree(s.scratch);
+        s.scratch = nullptr;
+        s.scratch_bytes = 0;
+    }
+    void* p = nullptr;
+    if (hip_status(hipMalloc(&p, want), "hipMalloc(scratch)") != KH_OK) return nullptr;
+    s.scratch = p;
+    s.scratch_bytes = want;
+    return p;
+}
+
+}  // namespace kh
+
+using kh::fail;
+using kh::hip_status;
+
+extern "C" {
+
+int kh_available(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return 0;
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, 0) != hipSuccess) return 0;
+    return std::strncmp(p.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+}
+
+int kh_init(int device) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0)
+        return fail(KH_ERR_NO_DEVICE, "kansai_hip: no HIP device available");
+    if (device < 0 || device >= n || device >= kh::kMaxDevices)
+        return fail(KH_ERR_INVALID_ARG, "kh_init: device index out of range");
+    kh::t_device = device;
+    return kh::current() ? KH_OK : KH_ERR_NO_DEVICE;
+}
+
+const char* kh_last_error(void) { return kh::t_last_error.c_str(); }
+
+int kh_device_info(char* name, size_t name_len, int* cus, int* clock_khz, int* mem_clock_khz, int* bus_width,
+                   size_t* total_mem) {
+    KH_DEVICE_OR_RETURN(d);
+    hipDeviceProp_t p;
+    int rc = hip_status(hipGetDeviceProperties(&p, d->id), "hipGetDeviceProperties");
+    if (rc) return rc;
+    if (name && name_len) {
+        std::strncpy(name, p.gcnArchName, name_len - 1);
+        name[name_len - 1] = '\0';
+    }
+    if (cus) *cus = p.multiProcessorCount;
+    if (clock_khz) *clock_khz = p.clockRate;
+    if (mem_clock_khz) *mem_clock_khz = p.memoryClockRate;
+    if (bus_width) *bus_width = p.memoryBusWidth;
+    if (total_mem) *total_mem = p.totalGlobalMem;
+    return KH_OK;
+}
+
+int kh_synchronize(void) {
+    KH_DEVICE_OR_RETURN(d);
+    int rc = hip_status(hipStreamSynchronize(d->stream), "hipStreamSynchronize");
+    if (rc) return rc;
+    unsigned fault = 0;
+    rc = hip_status(hipMemcpy(&fault, d->fault, sizeof(unsigned), hipMemcpyDeviceToHost), "read fault word");
+    if (rc) return rc;
+    if (fault) {
+        const unsigned zero = 0;
+        rc = hip_status(hipMemcpy(d->fault, &zero, sizeof(unsigned), hipMemcpyHostToDevice), "clear fault word");
+        if (rc) return rc;
+        if (fault & kh::kFaultNonFinite)
+            return fail(KH_ERR_NONFINITE, "cannot quantize a non-finite value (NaN or inf)");
+    }
+    return KH_OK;
+}
+
+int kh_get_stream(void** stream) {
+    KH_REQUIRE(stream, "kh_get_stream: null out pointer");
+    KH_DEVICE_OR_RETURN(d);
+    *stream = d->stream;
+    return KH_OK;
+}
+
+// ---- pool -------------------------------------------------------------------
+
+int kh_alloc(size_t bytes, void** dptr) {
+    KH_REQUIRE(dptr, "kh_alloc: null out pointer");
+    KH_DEVICE_OR_RETURN(d);
+    kh::Pool& pool = kh::g_slots[d->id].pool;
+    const size_t cls = kh::size_class(bytes);
+    {
+        std::lock_guard<std::mutex> lk(pool.mu);
+        auto it = pool.free_lists.find(cls);
+        if (it != pool.free_lists.end() && !it->second.empty()) {
+            void* p = it->second.back();
+            it->second.pop_back();
+            pool.live[p] = cls;
+            pool.cached -= cls;
+            pool.in_use += cls;
+            *dptr = p;
+            return KH_OK;
+        }
+    }
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, cls);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        kh_pool_trim();  // give cached blocks back and retry once
+        e = hipMalloc(&p, cls);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            return fail(KH_ERR_OOM, "kh_alloc: out of device memory for " + std::to_string(bytes) + " bytes");
+        }
+    }
+    std::lock_guard<std::mutex> lk(pool.mu);
+    pool.live[p] = cls;
+    pool.in_use += cls;
+    pool.driver_allocs += 1;
+    *dptr = p;
+    return KH_OK;
+}
+
+int kh_free(void* dptr) {
+    if (!dptr) return KH_OK;
+    KH_DEVICE_OR_RETURN(d);
+    kh::Pool& pool = kh::g_slots[d->id].pool;
+    std::lock_guard<std::mutex> lk(pool.mu);
+    auto it = pool.live.find(dptr);
+    if (it == pool.live.end()) return fail(KH_ERR_INVALID_ARG, "kh_free: pointer was not allocated by kh_alloc");
+    const size_t cls = it->second;
+    pool.live.erase(it);
+    pool.free_lists[cls].push_back(dptr);
+    pool.in_use -= cls;
+    pool.cached += cls;
+    return KH_OK;
+}
+
+int kh_pool_trim(void) {
+    KH_DEVICE_OR_RETURN(d);
+    int rc = hip_status(hipStreamSynchronize(d->stream), "hipStreamSynchronize");
+    if (rc) return rc;
+    kh::Pool& pool = kh::g_slots[d->id].pool;
+    std::lock_guard<std::mutex> lk(pool.mu);
+    for (auto& kv : pool.free_lists)
+        for (void* p : kv.second) (void)hipFree(p);
+    pool.free_lists.clear();
+    pool.cached = 0;
+    return KH_OK;
+}
+
+int kh_pool_stats(size_t* in_use, size_t* cached, size_t* driver_allocs) {
+    KH_DEVICE_OR_RETURN(d);
+    kh::Pool& pool = kh::g_slots[d->id].pool;
+    std::lock_guard<std::mutex> lk(pool.mu);
+    if (in_use) *in_use = pool.in_use;
+    if (cached) *cached = pool.cached;
+    if (driver_allocs) *driver_allocs = pool.driver_allocs;
+    return KH_OK;
+}
+
+// ---- copies -------------------------------------------------------------------
+
+int kh_memcpy_h2d(void* dst, const void* host_src, size_t bytes) {
+    if (bytes == 0) return KH_OK;
+    KH_REQUIRE(dst && host_src, "kh_memcpy_h2d: null pointer");
+    KH_DEVICE_OR_RETURN(d);
+    int rc = hip_status(hipMemcpyAsync(dst, host_src, bytes, hipMemcpyHostToDevice, d->stream), "hipMemcpyAsync(H2D)");
+    if (rc) return rc;
+    return hip_status(hipStreamSynchronize(d->stream), "hipStreamSynchronize");
+}
+
+int kh_memcpy_d2h(void* host_dst, const void* src, size_t bytes) {
+    if (bytes == 0) return KH_OK;
+    KH_REQUIRE(host_dst && src, "kh_memcpy_d2h: null pointer");
+    KH_DEVICE_OR_RETURN(d);
+    int rc = hip_status(hipMemcpyAsync(host_dst, src, bytes, hipMemcpyDeviceToHost, d->stream), "hipMemcpyAsync(D2H)");
+    if (rc) return rc;
+    return hip_status(hipStreamSynchronize(d->stream), "hipStreamSynchronize");
+}
+
+int kh_memcpy_d2d(void* dst, const void* src, size_t bytes) {
+    if (bytes == 0) return KH_OK;
+    KH_REQUIRE(dst && src, "kh_memcpy_d2d: null pointer");
+    KH_DEVICE_OR_RETURN(d);
+    return hip_status(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, d->stream), "hipMemcpyAsync(D2D)");
+}
+
+// ---- events -------------------------------------------------------------------
+
+int kh_event_create(void** event) {
+    KH_REQUIRE(event, "kh_event_create: null out pointer");
+    KH_DEVICE_OR_RETURN(d);
+    hipEvent_t e;
+    int rc = hip_status(hipEventCreate(&e), "hipEventCreate");
+    if (rc) return rc;
+    *event = e;
+    return KH_OK;
+}
+
+int kh_event_record(void* event) {
+    KH_REQUIRE(event, "kh_event_record: null event");
+    KH_DEVICE_OR_RETURN(d);
+    return hip_status(hipEventRecord(static_cast<hipEvent_t>(event), d->stream), "hipEventRecord");
+}
+
+int kh_event_elapsed_ms(void* start, void* end, float* ms) {
+    KH_REQUIRE(start && end && ms, "kh_event_elapsed_ms: null argument");
+    int rc = hip_status(hipEventSynchronize(static_cast<hipEvent_t>(end)), "hipEventSynchronize");
+    if (rc) return rc;
+    return hip_status(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(end)),
+                      "hipEventElapsedTime");
+}
+
+int kh_event_destroy(void* event) {
+    if (!event) return KH_OK;
+    return hip_status(hipEventDestroy(static_cast<hipEvent_t>(event)), "hipEventDestroy");
+}
+
+}  // extern "C"

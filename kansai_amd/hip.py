@@ -1,0 +1,220 @@
+"""The HIP backend's tensor-level operations.
+
+The role core/src/MetalOps.cpp plays for the reference's Metal backend
+(core/src/MetalOps.cpp:8-140): check shapes, allocate the output (here from
+the device pool), call the raw-pointer kernel.  Every function takes and
+returns DeviceTensors; work is queued on the library stream and nothing
+waits unless a result is downloaded or synchronize() is called.
+"""
+
+from __future__ import annotations
+
+from . import _native as N
+from .device import DeviceTensor
+
+available = N.available
+synchronize = N.synchronize
+
+
+def _need(t: DeviceTensor, dtype: str, ndim: int | None, what: str):
+    if not isinstance(t, DeviceTensor):
+        raise TypeError(f"{what}: expected a DeviceTensor, got {type(t).__name__}")
+    if t.dtype != dtype:
+        raise TypeError(f"{what}: expected {dtype}, got {t.dtype}")
+    if ndim is not None and len(t.shape) != ndim:
+        raise RuntimeError(f"{what}: expected a {ndim}-D tensor, got shape {t.shape}")
+
+
+def _opt(t):
+    return t.ptr if t is not None else None
+
+
+# ---------------------------------------------------------------------------
+# quantize / dequantize (python/kansai/quantize.py:50-77)
+# ---------------------------------------------------------------------------
+
+def quantize_tensor(x: DeviceTensor):
+    """Per-tensor symmetric int8: (codes int8 like x, scale float64[1])."""
+    _need(x, "float32", None, "quantize_tensor")
+    q = DeviceTensor(x.shape, "int8")
+    s = DeviceTensor([1], "float64")
+    N.call("kh_quantize_tensor", x.ptr, x.numel(), q.ptr, s.ptr)
+    return q, s
+
+
+def quantize_rows(x: DeviceTensor):
+    """Per-row (per-token) symmetric int8 of a 2-D tensor: (codes, scales[rows])."""
+    _need(x, "float32", 2, "quantize_rows")
+    rows, cols = x.shape
+    q = DeviceTensor(x.shape, "int8")
+    s = DeviceTensor([rows], "float64")
+    N.call("kh_quantize_rows", x.ptr, rows, cols, q.ptr, s.ptr)
+    return q, s
+
+
+def quantize_cols_packed(w: DeviceTensor):
+    """Per-output-channel int8 of an [in, out] weight, packed [out, in]."""
+    _need(w, "float32", 2, "quantize_cols_packed")
+    k, n = w.shape
+    q = DeviceTensor([n, k], "int8")
+    s = DeviceTensor([n], "float64")
+    N.call("kh_quantize_cols_packed", w.ptr, k, n, q.ptr, s.ptr)
+    return q, s
+
+
+def quantize_tensor_packed(w: DeviceTensor):
+    """Per-tensor int8 of an [in, out] weight, packed [out, in]."""
+    _need(w, "float32", 2, "quantize_tensor_packed")
+    k, n = w.shape
+    q = DeviceTensor([n, k], "int8")
+    s = DeviceTensor([1], "float64")
+    N.call("kh_quantize_tensor_packed", w.ptr, k, n, q.ptr, s.ptr)
+    return q, s
+
+
+def dequantize_tensor(q: DeviceTensor, scale: DeviceTensor) -> DeviceTensor:
+    _need(q, "int8", None, "dequantize_tensor")
+    _need(scale, "float64", None, "dequantize_tensor(scale)")
+    out = DeviceTensor(q.shape, "float32")
+    N.call("kh_dequantize_tensor", q.ptr, q.numel(), scale.ptr, out.ptr)
+    return out
+
+
+def dequantize_rows(q: DeviceTensor, scales: DeviceTensor) -> DeviceTensor:
+    _need(q, "int8", 2, "dequantize_rows")
+    _need(scales, "float64", 1, "dequantize_rows(scales)")
+    rows, cols = q.shape
+    if scales.shape[0] != rows:
+        raise RuntimeError("dequantize_rows: one scale per row required")
+    out = DeviceTensor(q.shape, "float32")
+    N.call("kh_dequantize_rows", q.ptr, rows, cols, scales.ptr, out.ptr)
+    return out
+
+
+def dequantize_packed(qp: DeviceTensor, scales: DeviceTensor) -> DeviceTensor:
+    """Packed [out, in] codes back to the fp32 [in, out] weight."""
+    _need(qp, "int8", 2, "dequantize_packed")
+    _need(scales, "float64", 1, "dequantize_packed(scales)")
+    n, k = qp.shape
+    if scales.shape[0] not in (1, n):
+        raise RuntimeError("dequantize_packed: scales must have 1 or out entries")
+    out = DeviceTensor([k, n], "float32")
+    N.call("kh_dequantize_packed", qp.ptr, k, n, scales.ptr, scales.shape[0], out.ptr)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# int8 GEMM
+# ---------------------------------------------------------------------------
+
+def _scale_mode(s: DeviceTensor, count: int, what: str) -> int:
+    _need(s, "float64", 1, what)
+    if s.shape[0] == count and count != 1:
+        return 1
+    if s.shape[0] == 1:
+        return 0
+    raise RuntimeError(f"{what}: expected 1 or {count} scales, got {s.shape[0]}")
+
+
+def gemm_i8(a: DeviceTensor, b_packed: DeviceTensor, sa: DeviceTensor | None = None,
+            sb: DeviceTensor | None = None, bias: DeviceTensor | None = None, *,
+            want_out: bool = True, want_acc: bool = False):
+    """a [M, K] int8, b_packed [N, K] int8 -> out fp32 [M, N] (fused
+    dequantize + bias) and/or acc int32 [M, N].  Returns (out, acc)."""
+    _need(a, "int8", 2, "gemm_i8(a)")
+    _need(b_packed, "int8", 2, "gemm_i8(b)")
+    M, K = a.shape
+    Nn, K2 = b_packed.shape
+    if K != K2:
+        raise RuntimeError(f"gemm_i8: incompatible shapes {a.shape} x {b_packed.shape}^T")
+    sa_mode = sb_mode = 0
+    if want_out:
+        sa_mode = _scale_mode(sa, M, "gemm_i8(sa)")
+        sb_mode = _scale_mode(sb, Nn, "gemm_i8(sb)")
+    if bias is not None:
+        _need(bias, "float32", 1, "gemm_i8(bias)")
+        if bias.shape[0] != Nn:
+            raise RuntimeError("gemm_i8: bias must have N entries")
+    out = DeviceTensor([M, Nn], "float32") if want_out else None
+    acc = DeviceTensor([M, Nn], "int32") if want_acc else None
+    N.call("kh_gemm_i8", a.ptr, b_packed.ptr, M, Nn, K, _opt(sa) if want_out else None, sa_mode,
+           _opt(sb) if want_out else None, sb_mode, _opt(bias), _opt(out), _opt(acc))
+    return out, acc
+
+
+def dequantize_acc(acc: DeviceTensor, sa: DeviceTensor, sb: DeviceTensor,
+                   bias: DeviceTensor | None = None) -> DeviceTensor:
+    _need(acc, "int32", 2, "dequantize_acc")
+    M, Nn = acc.shape
+    sa_mode = _scale_mode(sa, M, "dequantize_acc(sa)")
+    sb_mode = _scale_mode(sb, Nn, "dequantize_acc(sb)")
+    out = DeviceTensor([M, Nn], "float32")
+    N.call("kh_dequantize_acc", acc.ptr, M, Nn, sa.ptr, sa_mode, sb.ptr, sb_mode, _opt(bias), out.ptr)
+    return out
+
+
+def linear_i8(x: DeviceTensor, b_packed: DeviceTensor, sb: DeviceTensor,
+              bias: DeviceTensor | None = None) -> DeviceTensor:
+    """Per-token dynamic quantize of x [M, K] fp32, then the int8 GEMM with
+    the fused epilogue."""
+    _need(x, "float32", 2, "linear_i8(x)")
+    _need(b_packed, "int8", 2, "linear_i8(w)")
+    M, K = x.shape
+    Nn, K2 = b_packed.shape
+    if K != K2:
+        raise RuntimeError(f"linear_i8: incompatible shapes {x.shape} x {b_packed.shape}^T")
+    sb_mode = _scale_mode(sb, Nn, "linear_i8(sb)")
+    q = DeviceTensor([M, K], "int8")
+    sx = DeviceTensor([M], "float64")
+    out = DeviceTensor([M, Nn], "float32")
+    N.call("kh_linear_i8", x.ptr, M, K, b_packed.ptr, Nn, sb.ptr, sb_mode, _opt(bias), q.ptr, sx.ptr, out.ptr)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# fp32
+# ---------------------------------------------------------------------------
+
+def matmul(a: DeviceTensor, b: DeviceTensor, bias: DeviceTensor | None = None) -> DeviceTensor:
+    """kan::metal_matmul's contract (core/src/MetalOps.cpp:10-17): 2-D,
+    a.shape[1] == b.shape[0], else RuntimeError("incompatible shapes")."""
+    _need(a, "float32", 2, "matmul(a)")
+    _need(b, "float32", 2, "matmul(b)")
+    if a.shape[1] != b.shape[0]:
+        raise RuntimeError("matmul: incompatible shapes")
+    M, K = a.shape
+    Nn = b.shape[1]
+    if bias is not None:
+        _need(bias, "float32", 1, "matmul(bias)")
+        if bias.shape[0] != Nn:
+            raise RuntimeError("matmul: bias must have N entries")
+    out = DeviceTensor([M, Nn], "float32")
+    N.call("kh_matmul_f32", a.ptr, b.ptr, out.ptr, M, K, Nn, _opt(bias))
+    return out
+
+
+def add(a: DeviceTensor, b: DeviceTensor) -> DeviceTensor:
+    _need(a, "float32", None, "add")
+    _need(b, "float32", None, "add")
+    if list(a.shape) != list(b.shape):
+        raise RuntimeError("add: shapes must match")
+    out = DeviceTensor(a.shape, "float32")
+    N.call("kh_add", a.ptr, b.ptr, out.ptr, a.numel())
+    return out
+
+
+def add_bias(x: DeviceTensor, bias: DeviceTensor, relu: bool = False) -> DeviceTensor:
+    _need(x, "float32", 2, "add_bias")
+    _need(bias, "float32", 1, "add_bias(bias)")
+    if bias.shape[0] != x.shape[1]:
+        raise RuntimeError("add_bias: bias must have features entries")
+    out = DeviceTensor(x.shape, "float32")
+    N.call("kh_add_bias", x.ptr, bias.ptr, out.ptr, x.shape[0], x.shape[1], 1 if relu else 0)
+    return out
+
+
+def relu(x: DeviceTensor) -> DeviceTensor:
+    _need(x, "float32", None, "relu")
+    out = DeviceTensor(x.shape, "float32")
+    N.call("kh_relu", x.ptr, out.ptr, x.numel())
+    return out

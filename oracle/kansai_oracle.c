@@ -14,7 +14,7 @@
  *     FE_TONEAREST mode (ties to even); NOT C `round()` (ties away).
  *   - `core.from_flat` converts each binary64 to binary32 with
  *     round-to-nearest-even, which is C's `(float)d`.
- * Build with -O2 -fno-fast-math -ffp-contract=off so no FMA contraction
+ * Build with -O3 -fno-fast-math -ffp-contract=off so no FMA contraction
  * or reassociation changes a result.
  *
  * Parity pins (tests/test_oracle.py): the reference test's own known-answer

@@ -1,0 +1,178 @@
+"""GPU parity: int8 GEMM (exact int32 accumulators, bit-exact fused
+dequantize + bias epilogue) and the fp32 matmul (rounding-bound agreement
+with the reference's own compiled i-k-j loop and with float64)."""
+
+import numpy as np
+import pytest
+
+from conftest import golden_names, load_golden
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def hip():
+    from kansai_amd import hip as H
+    from kansai_amd.device import DeviceTensor
+    assert H.available(), "no gfx950 device"
+    return H, DeviceTensor
+
+
+def bits32(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def run_gemm(H, D, a, bt, sa, sb, bias):
+    out, acc = H.gemm_i8(D.from_host(a), D.from_host(bt), D.from_host(np.asarray(sa, np.float64)),
+                         D.from_host(np.asarray(sb, np.float64)), D.from_host(bias) if bias is not None else None,
+                         want_out=True, want_acc=True)
+    return out.numpy(), acc.numpy()
+
+
+@pytest.mark.parametrize("name", golden_names("gemm_i8_"))
+def test_gemm_i8_golden(hip, name):
+    H, D = hip
+    g = load_golden(name)
+    out, acc = run_gemm(H, D, g["a"], g["bt"], g["sa"], g["sb"], g["bias"])
+    np.testing.assert_array_equal(acc, g["acc"])
+    np.testing.assert_array_equal(bits32(out), bits32(g["out"]))
+
+
+SHAPES = [
+    (64, 512, 512),      # C1's int8 Linear
+    (1, 1, 16), (1, 4096, 4096), (8, 4096, 4096), (32, 11008, 4096),  # C5 decode shapes
+    (16384, 65, 384),    # C4 vocab head: N=65 edge tile
+    (256, 1536, 384), (256, 384, 1536),
+    (129, 257, 80), (300, 200, 48), (2048, 2048, 512), (2304, 2176, 1024),
+    (33, 40, 130), (100, 50, 77), (5, 7, 3),  # K % 16 != 0: byte-gather path
+]
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_gemm_i8_vs_oracle(hip, M, N, K):
+    H, D = hip
+    gen = np.random.Generator(np.random.PCG64(M * 1_000_003 + N * 1009 + K))
+    a = gen.integers(-127, 128, (M, K), dtype=np.int8)
+    bt = gen.integers(-127, 128, (N, K), dtype=np.int8)
+    sa = gen.uniform(1e-3, 5e-2, M)
+    sb = gen.uniform(1e-3, 5e-2, N)
+    bias = gen.standard_normal(N).astype(np.float32)
+    out, acc = run_gemm(H, D, a, bt, sa, sb, bias)
+    # check a row sample against the oracle when the full product is large
+    rows = np.arange(M) if M * N * K <= 2 ** 31 else gen.choice(M, size=64, replace=False)
+    eacc = O.ko_gemm_i8(a[rows], bt)
+    np.testing.assert_array_equal(acc[rows], eacc)
+    eout = O.ko_epilogue(eacc, sa[rows], sb, bias)
+    np.testing.assert_array_equal(bits32(out[rows]), bits32(eout))
+
+
+def test_gemm_i8_per_tensor_scales_and_no_bias(hip):
+    H, D = hip
+    gen = np.random.Generator(np.random.PCG64(12))
+    a = gen.integers(-127, 128, (200, 320), dtype=np.int8)
+    bt = gen.integers(-127, 128, (96, 320), dtype=np.int8)
+    out, acc = run_gemm(H, D, a, bt, [0.01], [0.02], None)
+    eacc = O.ko_gemm_i8(a, bt)
+    np.testing.assert_array_equal(acc, eacc)
+    np.testing.assert_array_equal(bits32(out), bits32(O.ko_epilogue(eacc, [0.01], [0.02], None)))
+
+
+def test_gemm_i8_extreme_values(hip):
+    """All -127: the largest accumulator magnitude, 127*127*K."""
+    H, D = hip
+    K = 8192
+    a = np.full((64, K), -127, np.int8)
+    bt = np.full((128, K), -127, np.int8)
+    a[1] = 127
+    _, acc = run_gemm(H, D, a, bt, [1.0], [1.0], None)
+    assert (acc[0] == 127 * 127 * K).all() and (acc[1] == -127 * 127 * K).all()
+
+
+def test_gemm_i8_c3a_full_size(hip):
+    """Config C3a: M=N=K=8192, A,B uniform in [-127,127], per-tensor scales
+    0.01/0.02, fused dequantize to fp32.  128 sampled rows are checked
+    bit-exactly against the oracle (accumulators and outputs)."""
+    H, D = hip
+    M = N = K = 8192
+    gen = np.random.Generator(np.random.PCG64(3))
+    a = gen.integers(-127, 128, (M, K), dtype=np.int8)
+    bt = gen.integers(-127, 128, (N, K), dtype=np.int8)
+    out, acc = run_gemm(H, D, a, bt, [0.01], [0.02], None)
+    rows = gen.choice(M, size=128, replace=False)
+    eacc = O.ko_gemm_i8(a[rows], bt)
+    np.testing.assert_array_equal(acc[rows], eacc)
+    np.testing.assert_array_equal(bits32(out[rows]), bits32(O.ko_epilogue(eacc, [0.01], [0.02], None)))
+    # column sample too (the tile grid's other axis)
+    cols = gen.choice(N, size=64, replace=False)
+    eacc_c = (a.astype(np.int64)[::97] @ bt[cols].astype(np.int64).T).astype(np.int32)
+    np.testing.assert_array_equal(acc[::97][:, cols], eacc_c)
+
+
+def test_linear_i8_per_token(hip):
+    """kh_linear_i8: per-token quantize fused ahead of the GEMM (config C5)."""
+    H, D = hip
+    gen = np.random.Generator(np.random.PCG64(8))
+    for M in (1, 8, 32):
+        K, N = 4096, 1024
+        x = gen.standard_normal((M, K), dtype=np.float32)
+        w = (gen.standard_normal((K, N), dtype=np.float32) * np.float32(0.02))
+        bias = gen.standard_normal(N).astype(np.float32)
+        qw, sw = O.ko_quantize_cols_packed(w)
+        out = H.linear_i8(D.from_host(x), D.from_host(qw), D.from_host(sw), D.from_host(bias)).numpy()
+        qx, sx = O.ko_quantize_rows(x)
+        expect = O.ko_epilogue(O.ko_gemm_i8(qx, qw), sx, sw, bias)
+        np.testing.assert_array_equal(bits32(out), bits32(expect))
+
+
+def test_dequantize_acc_matches_fused(hip):
+    H, D = hip
+    gen = np.random.Generator(np.random.PCG64(9))
+    a = gen.integers(-127, 128, (70, 96), dtype=np.int8)
+    bt = gen.integers(-127, 128, (50, 96), dtype=np.int8)
+    sa, sb = gen.uniform(1e-3, 1e-1, 70), gen.uniform(1e-3, 1e-1, 50)
+    bias = gen.standard_normal(50).astype(np.float32)
+    out, acc = run_gemm(H, D, a, bt, sa, sb, bias)
+    sep = H.dequantize_acc(D.from_host(acc), D.from_host(sa), D.from_host(sb), D.from_host(bias)).numpy()
+    np.testing.assert_array_equal(bits32(sep), bits32(out))
+
+
+# ---------------------------------------------------------------------------
+# fp32 matmul
+# ---------------------------------------------------------------------------
+
+def _f32_bound(a, b):
+    K = a.shape[1]
+    return 2 * K * np.finfo(np.float32).eps * (np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64)) + 1e-30
+
+
+@pytest.mark.parametrize("M,K,N", [(17, 19, 15), (100, 77, 50), (1, 1, 1), (64, 512, 512), (16, 32, 24),
+                                   (257, 129, 131), (512, 1024, 768), (1024, 1024, 1024)])
+def test_matmul_f32_vs_reference(hip, M, K, N):
+    H, D = hip
+    gen = np.random.Generator(np.random.PCG64(M + 7 * K + 13 * N))
+    a = gen.standard_normal((M, K), dtype=np.float32)
+    b = gen.standard_normal((K, N), dtype=np.float32)
+    bias = gen.standard_normal(N).astype(np.float32)
+    got = H.matmul(D.from_host(a), D.from_host(b), D.from_host(bias)).numpy()
+    ref64 = a.astype(np.float64) @ b.astype(np.float64) + bias.astype(np.float64)
+    bound = _f32_bound(a, b) + np.abs(bias) * np.finfo(np.float32).eps
+    assert (np.abs(got - ref64) <= bound).all()
+    ref = O.ref_add_bias(O.ref_matmul(a, b), bias) if O.ref_available() else O.ko_add_bias(O.ko_matmul_f32(a, b), bias)
+    assert (np.abs(got - ref) <= 2 * bound).all()
+    # the reference's own GPU-vs-CPU bar (tests/test_metal_backend.py:22)
+    if K <= 32:
+        assert np.abs(got - ref).max() < 1e-3
+
+
+def test_matmul_f32_c3b_full_size(hip):
+    """Config C3b: M=N=K=4096 ~N(0,1); sampled rows against float64."""
+    H, D = hip
+    n = 4096
+    gen = np.random.Generator(np.random.PCG64(4))
+    a = gen.standard_normal((n, n), dtype=np.float32)
+    b = gen.standard_normal((n, n), dtype=np.float32)
+    got = H.matmul(D.from_host(a), D.from_host(b)).numpy()
+    rows = gen.choice(n, size=64, replace=False)
+    ref64 = a[rows].astype(np.float64) @ b.astype(np.float64)
+    assert (np.abs(got[rows] - ref64) <= _f32_bound(a[rows], b)).all()
