@@ -17,7 +17,15 @@ CPU baseline: the reference's own compiled backend/cpu/src/Ops.cpp matmul
 dequantizing the weight (python/kansai/quantize.py:115-122) -- on one core,
 over a time-bounded slab of rows of the same workload.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--only gemm,quant,f32,copy]
+
+Profiling (the summaries under profiles/ are made this way):
+    rocprofv3 --kernel-trace --stats -d OUT/trace -o run --output-format csv -- python3 bench.py --no-cpu
+    rocprofv3 --pmc FETCH_SIZE -d OUT/fetch -o run --output-format csv -- python3 bench.py --only gemm,quant,copy --steps 3 --warmup 1 --no-cpu
+    rocprofv3 --pmc WRITE_SIZE -d OUT/write -o run --output-format csv -- python3 bench.py --only gemm,quant,copy --steps 3 --warmup 1 --no-cpu
+    python3 bench.py --summarize OUT
+"copy" runs a 1 GiB device-to-device copy: the calibration that turns the
+FETCH_SIZE / WRITE_SIZE readings of the other kernels into HBM bytes.
 """
 
 from __future__ import annotations
@@ -68,6 +76,10 @@ def measured_traffic(kernel_key):
             return json.load(f).get(kernel_key, {}).get("bytes_per_launch")
     except (OSError, ValueError):
         return None
+
+
+def _r(x, nd):
+    return None if x != x else round(x, nd)
 
 
 def bench_gemm(H, D, steps, warmup):
@@ -121,6 +133,94 @@ def bench_f32(H, D, steps, warmup):
     return ms, 2.0 * n ** 3 / (ms * 1e-3) / 1e12
 
 
+COPY_BYTES = 1 << 30
+
+
+def bench_copy(steps, warmup):
+    """1 GiB device-to-device copy (the library's copy16_kernel): the known-size
+    reference for FETCH_SIZE / WRITE_SIZE calibration."""
+    from kansai_amd import _native as Nn
+    from kansai_amd.device import DeviceTensor as D
+    src = D([COPY_BYTES], "int8")
+    dst = D([COPY_BYTES], "int8")
+    ms = time_kernel(lambda: Nn.call("kh_memcpy_d2d", dst.ptr, src.ptr, COPY_BYTES), steps, warmup)
+    return ms, 2.0 * COPY_BYTES / (ms * 1e-3) / 1e9
+
+
+# Kernel-name fragments (rocprofv3 Kernel_Name) of the kernels each bench line measures.
+KERNELS = {
+    "gemm_i8_8192": "gemm_i8_tiled_kernel",
+    "quant_rows_16384": "quant_rows_reg_kernel<4, 16>",
+    "dequant_rows_16384": "dequant_vec_kernel",
+    "fp32_matmul_4096": "gemm_f32_kernel",
+    "copy_1GiB": "copy16_kernel",
+}
+ALGO_BYTES = {"gemm_i8_8192": 2 * 8192 * 8192 + 4 * 8192 * 8192, "quant_rows_16384": 5 * 16384 * 16384,
+              "dequant_rows_16384": 5 * 16384 * 16384, "copy_1GiB": 2 * COPY_BYTES,
+              "fp32_matmul_4096": 3 * 4 * 4096 * 4096}
+
+
+def _read_csv(path):
+    import csv
+    with open(path) as f:
+        return list(csv.DictReader(f))
+
+
+def _find(root, suffix):
+    for dirpath, _, files in os.walk(root):
+        for f in files:
+            if f.endswith(suffix):
+                return os.path.join(dirpath, f)
+    return None
+
+
+def summarize(root):
+    """Turns rocprofv3 CSV output under root/{trace,fetch,write} into the
+    text summaries in profiles/ and profiles/traffic.json."""
+    out_dir = os.path.join(ROOT, "profiles")
+    os.makedirs(out_dir, exist_ok=True)
+    lines = []
+    stats = _find(os.path.join(root, "trace"), "kernel_stats.csv")
+    if stats:
+        rows = _read_csv(stats)
+        lines.append("| kernel | calls | avg us | min us | max us | % time |")
+        lines.append("|---|---|---|---|---|---|")
+        for r in rows:
+            lines.append(f"| {r['Name'][:90]} | {r['Calls']} | {float(r['AverageNs'])/1e3:.2f} | "
+                         f"{float(r['MinNs'])/1e3:.2f} | {float(r['MaxNs'])/1e3:.2f} | {float(r['Percentage']):.1f} |")
+    traffic = {}
+    per = {}
+    for which in ("fetch", "write"):
+        cc = _find(os.path.join(root, which), "counter_collection.csv")
+        if not cc:
+            continue
+        for r in _read_csv(cc):
+            for key, frag in KERNELS.items():
+                if frag in r["Kernel_Name"]:
+                    per.setdefault(key, {}).setdefault(r["Counter_Name"], {}).setdefault(r["Dispatch_Id"], 0.0)
+                    per[key][r["Counter_Name"]][r["Dispatch_Id"]] += float(r["Counter_Value"])
+    def avg(key, ctr):
+        d = per.get(key, {}).get(ctr, {})
+        return sum(d.values()) / len(d) if d else None
+    cf, cw = avg("copy_1GiB", "FETCH_SIZE"), avg("copy_1GiB", "WRITE_SIZE")
+    if cf and cw:
+        ff, wf = COPY_BYTES / (cf * 1024), COPY_BYTES / (cw * 1024)
+        traffic["_calibration"] = {"copy_bytes": COPY_BYTES, "FETCH_SIZE_KiB": cf, "WRITE_SIZE_KiB": cw,
+                                   "fetch_factor": ff, "write_factor": wf}
+        for key in KERNELS:
+            f, w = avg(key, "FETCH_SIZE"), avg(key, "WRITE_SIZE")
+            if f is None or w is None or key == "copy_1GiB":
+                continue
+            b = f * 1024 * ff + w * 1024 * wf
+            traffic[key] = {"FETCH_SIZE_KiB": f, "WRITE_SIZE_KiB": w, "bytes_per_launch": b,
+                            "algorithmic_bytes": ALGO_BYTES.get(key), "ratio": b / ALGO_BYTES[key]}
+    with open(os.path.join(out_dir, "traffic.json"), "w") as fjs:
+        json.dump(traffic, fjs, indent=1, sort_keys=True)
+    print("\n".join(lines))
+    print(json.dumps(traffic, indent=1))
+    return lines, traffic
+
+
 def cpu_baseline(budget_s=12.0):
     """The reference's compiled fp32 i-k-j matmul (oracle/_ref, built from
     backend/cpu/src/Ops.cpp) on dequantized operands of the C3a workload,
@@ -159,7 +259,13 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only", default="gemm,quant,f32", help="comma list of gemm,quant,f32,copy")
+    ap.add_argument("--summarize", metavar="DIR", help="summarize rocprofv3 CSV output and exit")
     args = ap.parse_args()
+    if args.summarize:
+        summarize(args.summarize)
+        return
+    only = set(args.only.split(","))
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only: the int8 path has no multi-GPU leg "
                                    "(rows/columns would shard with zero exchange); run with --gpus 1"}))
@@ -173,21 +279,29 @@ def main():
     info = Nn.device_info()
     log(f"device {info}")
 
-    log("int8 GEMM 8192^3 ...")
-    g_ms, g_tops, keep = bench_gemm(H, D, args.steps, args.warmup)
-    log(f"int8 GEMM: {g_ms:.4f} ms/step, {g_tops:.1f} TOPS")
-    del keep
-    Nn.call("kh_pool_trim")
-    log("quantize/dequantize C2 ...")
-    q_ms, d_ms, qd_bytes = bench_quant_dequant(H, D, args.steps, args.warmup)
-    q_gbs = qd_bytes / (q_ms * 1e-3) / 1e9
-    d_gbs = qd_bytes / (d_ms * 1e-3) / 1e9
-    log(f"quantize {q_ms:.4f} ms ({q_gbs:.0f} GB/s), dequantize {d_ms:.4f} ms ({d_gbs:.0f} GB/s)")
-    Nn.call("kh_pool_trim")
-    log("fp32 matmul 4096^3 ...")
-    f_ms, f_tflops = bench_f32(H, D, max(5, args.steps // 2), max(2, args.warmup // 2))
-    log(f"fp32 matmul: {f_ms:.4f} ms, {f_tflops:.1f} TFLOP/s")
-    Nn.call("kh_pool_trim")
+    g_ms = g_tops = q_ms = d_ms = q_gbs = d_gbs = f_ms = f_tflops = float("nan")
+    if "gemm" in only:
+        log("int8 GEMM 8192^3 ...")
+        g_ms, g_tops, keep = bench_gemm(H, D, args.steps, args.warmup)
+        log(f"int8 GEMM: {g_ms:.4f} ms/step, {g_tops:.1f} TOPS")
+        del keep
+        Nn.call("kh_pool_trim")
+    if "quant" in only:
+        log("quantize/dequantize C2 ...")
+        q_ms, d_ms, qd_bytes = bench_quant_dequant(H, D, args.steps, args.warmup)
+        q_gbs = qd_bytes / (q_ms * 1e-3) / 1e9
+        d_gbs = qd_bytes / (d_ms * 1e-3) / 1e9
+        log(f"quantize {q_ms:.4f} ms ({q_gbs:.0f} GB/s), dequantize {d_ms:.4f} ms ({d_gbs:.0f} GB/s)")
+        Nn.call("kh_pool_trim")
+    if "f32" in only:
+        log("fp32 matmul 4096^3 ...")
+        f_ms, f_tflops = bench_f32(H, D, max(5, args.steps // 2), max(2, args.warmup // 2))
+        log(f"fp32 matmul: {f_ms:.4f} ms, {f_tflops:.1f} TFLOP/s")
+        Nn.call("kh_pool_trim")
+    if "copy" in only:
+        c_ms, c_gbs = bench_copy(args.steps, args.warmup)
+        log(f"1 GiB d2d copy: {c_ms:.4f} ms, {c_gbs:.0f} GB/s")
+        Nn.call("kh_pool_trim")
 
     cpu = None
     if not args.no_cpu:
@@ -230,7 +344,7 @@ def main():
         "cpu_baseline": cpu,
         "device": info,
     }
-    print(json.dumps(result))
+    print(json.dumps(result).replace("NaN", "null"))
 
 
 if __name__ == "__main__":

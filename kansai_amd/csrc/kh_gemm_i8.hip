@@ -52,6 +52,26 @@ __device__ __forceinline__ void epilogue_store(const Epilogue& ep, int64_t i, in
     }
 }
 
+// Stores one 32x32 MFMA result block (register r of lane l holds row
+// 8*(r/4) + 4*(l/32) + r%4, column l%32, relative to (i0, j)).  The column's
+// scale and bias are read once per block.
+__device__ __forceinline__ void store_block32(const Epilogue& ep, int64_t i0, int64_t j, int64_t N, const i32x16& v) {
+    const double sbj = ep.sb ? ep.sb[ep.sb_per_col ? j : 0] : 0.0;
+    const float bj = ep.bias ? ep.bias[j] : 0.0f;
+    const double sa0 = (ep.sa && !ep.sa_per_row) ? ep.sa[0] * sbj : 0.0;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int64_t i = i0 + 8 * (r >> 2) + (r & 3);
+        if (ep.acc) ep.acc[i * N + j] = v[r];
+        if (ep.out) {
+            const double s = ep.sa_per_row ? ep.sa[i] * sbj : sa0;
+            float y = (float)((double)v[r] * s);
+            if (ep.bias) y = y + bj;
+            ep.out[i * N + j] = y;
+        }
+    }
+}
+
 template <int BM, int BN, int BK, int WM, int WN>
 struct GemmCfg {
     static constexpr int kThreads = WM * WN * 64;
@@ -191,6 +211,228 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_i8_kernel(const int8_t* __r
         }
 }
 
+// ---------------------------------------------------------------------------
+// Full-tile kernel (M % BM == 0, N % BN == 0, K % BK == 0, 16-byte aligned
+// operands): no bounds tests in the main loop.
+//
+// * Global loads are raw buffer loads: one VGPR offset per chunk, the k
+//   advance in an SGPR.
+// * LDS rows are BK = 128 bytes (8 chunks of 16 B) with no padding; chunk c
+//   of row r is stored at chunk slot c ^ swz(r), an XOR swizzle under which
+//   the MFMA fragment reads (32 consecutive rows, one chunk) and the
+//   row-contiguous fragment writes are both free of bank conflicts.
+// * MFMA fragments are double-buffered in registers across the four 32-k
+//   substeps of a BK step, so LDS latency hides behind the previous
+//   substep's MFMAs.
+// * Workgroups are launched on a 1-D grid; hardware deals consecutive
+//   workgroup ids round-robin to the 8 XCDs, so the id is remapped to give
+//   each XCD a contiguous band of tiles, walked in groups of kGroupM tile rows
+//   so that concurrently resident tiles share A and B panels in that XCD's L2.
+// ---------------------------------------------------------------------------
+constexpr int kXcds = 8;
+constexpr int kBufferFlags = 0x00020000;  // dword 3 of a raw gfx9 buffer resource
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kBufferFlags);
+}
+
+__device__ __forceinline__ int lds_swz(int r) { return ((r >> 1) ^ (r << 2)) & 7; }
+
+// Workgroup id -> (tile row, tile col).
+__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int group_m, int& tm, int& tn) {
+    const int total = tiles_m * tiles_n;
+    int t = bid;
+    if (total % kXcds == 0) t = (bid % kXcds) * (total / kXcds) + bid / kXcds;
+    const int per_group = group_m * tiles_n;
+    const int g = t / per_group;
+    const int first_m = g * group_m;
+    const int gm = min(tiles_m - first_m, group_m);
+    const int in_g = t - g * per_group;
+    tm = first_m + in_g % gm;
+    tn = in_g / gm;
+}
+
+// Swizzle for BK-byte LDS rows (BK / 16 chunks): conflict-free for 8- and
+// 16-lane groups reading one chunk of consecutive rows.
+template <int BK>
+__device__ __forceinline__ int tile_swz(int r) {
+    if (BK == 128) return ((r >> 1) ^ (r << 2)) & 7;
+    return ((r >> 1) ^ (r >> 3)) & 3;
+}
+
+// Scheduling hint: interleave `n` (1 MFMA, 1 LDS read) pairs.
+#define KH_SCHED_MFMA_DS(n)                                   \
+    do {                                                      \
+        _Pragma("unroll") for (int _i = 0; _i < (n); ++_i) {  \
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); \
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); \
+        }                                                     \
+    } while (0)
+
+// HINT: interleave LDS reads between MFMAs with scheduling barriers.
+// PRIO: raise the wave's issue priority while it issues an MFMA cluster, so
+// the SIMD's other wave does its memory work in the gaps.
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int HINT, int PRIO>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_i8_tiled_kernel(const int8_t* __restrict__ A,
+                                                                     const int8_t* __restrict__ B, int M, int N,
+                                                                     int K, int group_m, Epilogue ep) {
+    constexpr int kCh = BK / 16;  // 16-byte chunks per LDS row
+    constexpr int kSub = BK / 32;  // MFMA k-substeps per stage
+    constexpr int kThreads = WM * WN * 64;
+    constexpr int kWaveM = BM / WM, kWaveN = BN / WN;
+    constexpr int kTM = kWaveM / 32, kTN = kWaveN / 32;
+    constexpr int kAChunks = BM * kCh / kThreads;
+    constexpr int kBChunks = BN * kCh / kThreads;
+    constexpr int kLdsA = BM * BK, kLdsB = BN * BK, kStage = kLdsA + kLdsB;
+    static_assert(kAChunks >= 1 && kBChunks >= 1, "tile too small for the block");
+    static_assert(STAGES >= 2, "at least two LDS stages");
+    __shared__ __attribute__((aligned(16))) int8_t lds[STAGES * kStage];
+
+    int tm, tn;
+    tile_of(blockIdx.x, M / BM, N / BN, group_m, tm, tn);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(A + (int64_t)tm * BM * K, (uint32_t)BM * (uint32_t)K);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(B + (int64_t)tn * BN * K, (uint32_t)BN * (uint32_t)K);
+
+    int a_goff[kAChunks], a_loff[kAChunks], b_goff[kBChunks], b_loff[kBChunks];
+#pragma unroll
+    for (int c = 0; c < kAChunks; ++c) {
+        const int idx = tid + c * kThreads, r = idx / kCh, kc = idx % kCh;
+        a_goff[c] = r * K + kc * 16;
+        a_loff[c] = r * BK + ((kc ^ tile_swz<BK>(r)) << 4);
+    }
+#pragma unroll
+    for (int c = 0; c < kBChunks; ++c) {
+        const int idx = tid + c * kThreads, r = idx / kCh, kc = idx % kCh;
+        b_goff[c] = r * K + kc * 16;
+        b_loff[c] = kLdsA + r * BK + ((kc ^ tile_swz<BK>(r)) << 4);
+    }
+    i32x4 sa_[kAChunks], sb_[kBChunks];
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int c = 0; c < kAChunks; ++c) sa_[c] = __builtin_amdgcn_raw_buffer_load_b128(ra, a_goff[c], k0, 0);
+#pragma unroll
+        for (int c = 0; c < kBChunks; ++c) sb_[c] = __builtin_amdgcn_raw_buffer_load_b128(rb, b_goff[c], k0, 0);
+    };
+    auto lstore = [&](int stage) {
+        int8_t* base = lds + stage * kStage;
+#pragma unroll
+        for (int c = 0; c < kAChunks; ++c) *reinterpret_cast<i32x4*>(base + a_loff[c]) = sa_[c];
+#pragma unroll
+        for (int c = 0; c < kBChunks; ++c) *reinterpret_cast<i32x4*>(base + b_loff[c]) = sb_[c];
+    };
+
+    const int fr = lane & 31, fh = lane >> 5;
+    // LDS byte offsets (within a stage) of this lane's fragment rows.
+    int a_row[kTM], b_row[kTN];
+#pragma unroll
+    for (int a = 0; a < kTM; ++a) a_row[a] = wm * kWaveM + a * 32 + fr;
+#pragma unroll
+    for (int b = 0; b < kTN; ++b) b_row[b] = wn * kWaveN + b * 32 + fr;
+    auto read_frags = [&](int stage, int sub, i32x4* fa, i32x4* fb) {
+        const int8_t* base = lds + stage * kStage;
+#pragma unroll
+        for (int a = 0; a < kTM; ++a) {
+            const int r = a_row[a];
+            fa[a] = *reinterpret_cast<const i32x4*>(base + r * BK + (((2 * sub + fh) ^ tile_swz<BK>(r)) << 4));
+        }
+#pragma unroll
+        for (int b = 0; b < kTN; ++b) {
+            const int r = b_row[b];
+            fb[b] = *reinterpret_cast<const i32x4*>(base + kLdsA + r * BK + (((2 * sub + fh) ^ tile_swz<BK>(r)) << 4));
+        }
+    };
+
+    i32x16 acc[kTM][kTN];
+#pragma unroll
+    for (int a = 0; a < kTM; ++a)
+#pragma unroll
+        for (int b = 0; b < kTN; ++b) acc[a][b] = i32x16{0};
+
+    const int nk = K / BK;
+    // Prologue: stages 0 .. STAGES-2 into LDS, k-step STAGES-1 into registers.
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s) {
+        if (s < nk) {
+            gload(s * BK);
+            lstore(s);
+        }
+    }
+    if (STAGES - 1 < nk) gload((STAGES - 1) * BK);
+    __syncthreads();
+
+    i32x4 fa[2][kTM], fb[2][kTN];
+    read_frags(0, 0, fa[0], fb[0]);
+    for (int kt = 0; kt < nk; ++kt) {
+        const int stage = kt % STAGES;
+        const int next_stage = (kt + 1) % STAGES;
+#pragma unroll
+        for (int sub = 0; sub < kSub; ++sub) {
+            const int cur = sub & 1;
+            // Prefetch the next substep's fragments -- from the next stage
+            // after the last substep (visible since the previous barrier).
+            if (sub + 1 < kSub)
+                read_frags(stage, sub + 1, fa[cur ^ 1], fb[cur ^ 1]);
+            else if (kt + 1 < nk && STAGES > 2)
+                read_frags(next_stage, 0, fa[cur ^ 1], fb[cur ^ 1]);
+            if (PRIO) __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+            for (int a = 0; a < kTM; ++a)
+#pragma unroll
+                for (int b = 0; b < kTN; ++b)
+                    acc[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[cur][a], fb[cur][b], acc[a][b], 0, 0, 0);
+            if (HINT) KH_SCHED_MFMA_DS(kTM + kTN);
+            if (PRIO) __builtin_amdgcn_s_setprio(0);
+        }
+        // Registers hold k-step kt + STAGES - 1: store it into the stage that
+        // was read during k-step kt - 1 (every wave passed the last barrier).
+        if (kt + STAGES - 1 < nk) {
+            lstore((kt + STAGES - 1) % STAGES);
+            if (kt + STAGES < nk) gload((kt + STAGES) * BK);
+        }
+        __syncthreads();
+        if (STAGES == 2 && kt + 1 < nk) read_frags(next_stage, 0, fa[kSub & 1], fb[kSub & 1]);
+    }
+
+    // With 128x128 wave tiles the accumulators fill all 256 AGPRs; keep them
+    // there until each block is stored (otherwise every block is copied to
+    // VGPRs at once on loop exit).
+    if (kTM * kTN * 16 > 128) {
+#pragma unroll
+        for (int a = 0; a < kTM; ++a)
+#pragma unroll
+            for (int b = 0; b < kTN; ++b) asm volatile("" : "+a"(acc[a][b]));
+    }
+    const int64_t row_base = (int64_t)tm * BM + wm * kWaveM + 4 * fh;
+    const int64_t col_base = (int64_t)tn * BN + wn * kWaveN + fr;
+#pragma unroll
+    for (int a = 0; a < kTM; ++a)
+#pragma unroll
+        for (int b = 0; b < kTN; ++b) {
+            store_block32(ep, row_base + a * 32, col_base + b * 32, N, acc[a][b]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int STAGES, int HINT, int PRIO>
+int launch_tiled(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
+                 const Epilogue& ep, int group_m) {
+    const unsigned tiles = (unsigned)((M / BM) * (N / BN));
+    gemm_i8_tiled_kernel<BM, BN, BK, WM, WN, STAGES, HINT, PRIO>
+        <<<tiles, WM * WN * 64, 0, d->stream>>>(A, B, (int)M, (int)N, (int)K, group_m, ep);
+    return kh::launch_status("gemm_i8_tiled");
+}
+
+// True when the full-tile kernel applies to this shape.
+template <int BM, int BN, int BK>
+bool tiled_fits(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K) {
+    return M % BM == 0 && N % BN == 0 && K % BK == 0 && K > 0 && kh::aligned(A, 16) && kh::aligned(B, 16) &&
+           (int64_t)BM * K <= 0xFFFFFFFFLL && (int64_t)BN * K <= 0xFFFFFFFFLL && M <= 0x7FFFFFFF && N <= 0x7FFFFFFF &&
+           (M / BM) * (N / BN) <= 0x7FFFFFFF;
+}
+
 template <int BM, int BN, int BK, int WM, int WN>
 int launch_gemm(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K, const Epilogue& ep,
                 bool vec16) {
@@ -217,6 +459,8 @@ int kh_gemm_i8(const int8_t* a, const int8_t* b_packed, int64_t M, int64_t N, in
     KH_REQUIRE(!out || (sa && sb), "kh_gemm_i8: scales required when out is given");
     KH_DEVICE_OR_RETURN(d);
     Epilogue ep{sa, sb, bias, out, acc_out, sa_per_row, sb_per_col};
+    if (tiled_fits<256, 256, 128>(a, b_packed, M, N, K))
+        return launch_tiled<256, 256, 128, 2, 4, 2, 1, 0>(d, a, b_packed, M, N, K, ep, 8);
     const bool vec16 = (K % 16 == 0) && kh::aligned(a, 16) && kh::aligned(b_packed, 16);
     if (M >= 2048 && N >= 2048)
         return launch_gemm<256, 256, 64, 2, 4>(d, a, b_packed, M, N, K, ep, vec16);

@@ -316,13 +316,6 @@ int kh_memcpy_d2h(void* host_dst, const void* src, size_t bytes) {
     return hip_status(hipStreamSynchronize(d->stream), "hipStreamSynchronize");
 }
 
-int kh_memcpy_d2d(void* dst, const void* src, size_t bytes) {
-    if (bytes == 0) return KH_OK;
-    KH_REQUIRE(dst && src, "kh_memcpy_d2d: null pointer");
-    KH_DEVICE_OR_RETURN(d);
-    return hip_status(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, d->stream), "hipMemcpyAsync(D2D)");
-}
-
 // ---- events -------------------------------------------------------------------
 
 int kh_event_create(void** event) {

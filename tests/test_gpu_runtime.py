@@ -1,0 +1,67 @@
+"""GPU checks of the runtime half of the C ABI: device copies, the caching
+pool (core/src/StoragePool.cpp:5-24's role, for device memory) and events."""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def rt():
+    from kansai_amd import _native as N
+    from kansai_amd.device import DeviceTensor
+    assert N.available(), "no gfx950 device"
+    return N, DeviceTensor
+
+
+@pytest.mark.parametrize("nbytes,offset", [(16, 0), (4096, 0), (1 << 20, 0), (1000, 0), (4096, 3), (33, 1)])
+def test_memcpy_d2d(rt, nbytes, offset):
+    N, D = rt
+    gen = np.random.Generator(np.random.PCG64(nbytes + offset))
+    host = gen.integers(0, 256, nbytes + offset, dtype=np.uint8).view(np.int8)
+    src = D.from_host(host)
+    dst = D([nbytes + offset], "int8")
+    N.call("kh_memcpy_d2d", ctypes.c_void_p(dst.addr + offset), ctypes.c_void_p(src.addr + offset), nbytes)
+    got = dst.numpy()
+    np.testing.assert_array_equal(got[offset:], host[offset:])
+
+
+def test_pool_reuses_blocks(rt):
+    N, D = rt
+    N.call("kh_pool_trim")
+    before = N.pool_stats()["driver_allocs"]
+    for _ in range(5):
+        t = D([3, 1000], "float32")
+        t.release()
+    after = N.pool_stats()
+    assert after["driver_allocs"] - before == 1
+    assert after["cached"] >= 12000
+
+
+def test_free_of_foreign_pointer_is_an_error(rt):
+    N, D = rt
+    t = D([64], "int8")
+    with pytest.raises(RuntimeError):
+        N.call("kh_free", ctypes.c_void_p(t.addr + 16))
+
+
+def test_events_time_work(rt):
+    N, D = rt
+    e0, e1 = N.Event(), N.Event()
+    a = D([1 << 24], "int8")
+    b = D([1 << 24], "int8")
+    e0.record()
+    N.call("kh_memcpy_d2d", b.ptr, a.ptr, 1 << 24)
+    e1.record()
+    assert e0.elapsed_ms(e1) > 0.0
+
+
+def test_invalid_arguments_raise(rt):
+    N, D = rt
+    with pytest.raises(RuntimeError):
+        N.call("kh_quantize_rows", None, -1, 4, None, None)
+    with pytest.raises(RuntimeError):
+        N.call("kh_gemm_i8", None, None, 4, 4, 4, None, 0, None, 0, None, None, None)
