@@ -1,0 +1,469 @@
+"""KIR on the HIP backend: the graph schema, a tracer for the int8 path, the
+memory planner, and `run_hip`, the interpreter that dispatches a graph to the
+gfx950 kernels.
+
+The schema is the reference's (python/kansai/kir.py:40-75): single-output SSA
+`Node`s (id, op, inputs, shape, dtype, attrs) kept in execution order in a
+`Graph` with `inputs` (placeholder ids in argument order) and `output`.
+`run_hip` is duck-typed over that schema, so it also runs graphs built by the
+reference's own `kir.trace`.  It mirrors `run_metal`'s contract
+(kir.py:1586-1836): `run_hip(graph, *args)` returns the output value, raises
+RuntimeError when the device is missing, KeyError for an op it has no kernel
+for.  There is no CPU fallback for any op.
+
+New node kinds for the int8 path (the reference quantizes outside the graph
+at trace time, kir.py:129-136):
+
+  quantize      fp32 -> int8 codes + binary64 scales (attrs: granularity
+                "tensor" | "row"), value: QTensor
+  int8_matmul   QTensor [M,K] x packed-weight QTensor [K,N] -> int32 [M,N]
+  dequantize    QTensor -> fp32 (quantize.py:73-77), or an int8_matmul
+                accumulator -> fp32 (acc * sa * sb)
+  int8_linear   fusion of int8_matmul -> dequantize [-> add(bias)] into one
+                GEMM with the dequantize + bias epilogue
+  matmul_bias   fusion of fp32 matmul -> add(bias) (bias in the GEMM store)
+  fused_bias_relu  add(bias) -> relu (the reference's pattern, kir.py:581-600)
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Any
+
+import numpy as np
+
+from . import _native as N
+from . import hip as H
+from .device import DeviceTensor, as_host_array
+
+
+# ---------------------------------------------------------------------------
+# Graph / Node (kir.py:40-75)
+# ---------------------------------------------------------------------------
+
+@dataclass
+class Node:
+    id: int
+    op: str
+    inputs: list
+    shape: list
+    dtype: str = "float32"
+    attrs: dict = field(default_factory=dict)
+
+    def __repr__(self):
+        ins = ", ".join(f"%{i}" for i in self.inputs)
+        extra = {k: v for k, v in self.attrs.items() if k not in ("value", "_dev")}
+        return f"%{self.id} = {self.op}({ins})  : {self.dtype}{self.shape}" + (f"  {extra}" if extra else "")
+
+
+class Graph:
+    def __init__(self):
+        self.nodes: list = []
+        self.inputs: list = []
+        self.output = None
+
+    def add(self, op: str, inputs: list, shape: list, dtype: str = "float32", **attrs) -> int:
+        nid = len(self.nodes)
+        self.nodes.append(Node(nid, op, list(inputs), list(shape), dtype, dict(attrs)))
+        return nid
+
+    def placeholder(self, shape: list, dtype: str = "float32") -> int:
+        nid = self.add("placeholder", [], shape, dtype)
+        self.inputs.append(nid)
+        return nid
+
+    def __repr__(self):
+        return "\n".join([repr(n) for n in self.nodes] + [f"return %{self.output}"])
+
+
+# ---------------------------------------------------------------------------
+# Tracing (kir.py:115-407, the subset on the int8 / Linear path)
+# ---------------------------------------------------------------------------
+
+def _broadcast(a: list, b: list, what: str) -> list:
+    """Right-aligned NumPy broadcasting (kir.py:85-112's rule)."""
+    rank = max(len(a), len(b))
+    a2 = [1] * (rank - len(a)) + list(a)
+    b2 = [1] * (rank - len(b)) + list(b)
+    out = []
+    for x, y in zip(a2, b2):
+        if x != y and x != 1 and y != 1:
+            raise ValueError(f"{what}: shapes are not broadcast-compatible ({a} vs {b})")
+        out.append(max(x, y))
+    return out
+
+
+class TraceValue:
+    """A traced value: graph, node id, shape, dtype; no storage."""
+
+    __slots__ = ("graph", "node_id", "shape", "dtype")
+
+    def __init__(self, graph: Graph, node_id: int, shape: list, dtype: str = "float32"):
+        self.graph, self.node_id, self.shape, self.dtype = graph, node_id, list(shape), dtype
+
+    def _coerce(self, other) -> "TraceValue":
+        if isinstance(other, TraceValue):
+            return other
+        from .quantize import QTensor
+        if isinstance(other, QTensor):
+            nid = self.graph.add("constant", [], other.shape, "int8", value=other)
+            return TraceValue(self.graph, nid, other.shape, "int8")
+        shape = list(getattr(other, "shape", np.shape(other)))
+        nid = self.graph.add("constant", [], shape, value=other)
+        return TraceValue(self.graph, nid, shape)
+
+    def _emit(self, op, inputs, shape, dtype="float32", **attrs):
+        nid = self.graph.add(op, [t.node_id for t in inputs], shape, dtype, **attrs)
+        return TraceValue(self.graph, nid, shape, dtype)
+
+    def add(self, other):
+        other = self._coerce(other)
+        return self._emit("add", [self, other], _broadcast(self.shape, other.shape, "add"))
+
+    def relu(self):
+        return self._emit("relu", [self], self.shape)
+
+    def matmul(self, other):
+        other = self._coerce(other)
+        if len(self.shape) != 2 or len(other.shape) != 2:
+            raise ValueError(f"matmul: the HIP path traces 2-D operands, got {self.shape} vs {other.shape}")
+        if self.shape[1] != other.shape[0]:
+            raise ValueError(f"matmul: incompatible shapes {self.shape} vs {other.shape}")
+        return self._emit("matmul", [self, other], [self.shape[0], other.shape[1]])
+
+    def quantize(self, granularity: str = "tensor"):
+        if granularity not in ("tensor", "row"):
+            raise ValueError(f"quantize: granularity must be 'tensor' or 'row', got {granularity!r}")
+        if granularity == "row" and len(self.shape) != 2:
+            raise ValueError("quantize: per-row granularity needs a 2-D value")
+        return self._emit("quantize", [self], self.shape, "int8", granularity=granularity)
+
+    def int8_matmul(self, other):
+        other = self._coerce(other)
+        if self.dtype != "int8" or other.dtype != "int8":
+            raise ValueError("int8_matmul: both operands must be quantized (int8)")
+        if len(self.shape) != 2 or len(other.shape) != 2 or self.shape[1] != other.shape[0]:
+            raise ValueError(f"int8_matmul: incompatible shapes {self.shape} vs {other.shape}")
+        return self._emit("int8_matmul", [self, other], [self.shape[0], other.shape[1]], "int32")
+
+    def dequantize(self):
+        if self.dtype not in ("int8", "int32"):
+            raise ValueError("dequantize: operand is not quantized")
+        return self._emit("dequantize", [self], self.shape, "float32")
+
+
+def trace(fn, *example_inputs) -> Graph:
+    """Records fn applied to placeholders shaped like example_inputs
+    (kir.py:393-407)."""
+    g = Graph()
+    args = []
+    for x in example_inputs:
+        shape = list(getattr(x, "shape", np.shape(x)))
+        args.append(TraceValue(g, g.placeholder(shape), shape))
+    g.output = fn(*args).node_id
+    return g
+
+
+# ---------------------------------------------------------------------------
+# Fusion pass
+# ---------------------------------------------------------------------------
+
+def _users(graph) -> dict:
+    users = {n.id: [] for n in graph.nodes}
+    for n in graph.nodes:
+        for i in n.inputs:
+            users[i].append(n.id)
+    return users
+
+
+def _is_bias(graph, by_id, x_id, b_id) -> bool:
+    xs, bs = by_id[x_id].shape, by_id[b_id].shape
+    return len(xs) == 2 and len(bs) == 1 and xs[1] == bs[0]
+
+
+def quant_fusion(graph) -> Graph:
+    """Fuses, where the intermediate has no other user:
+      int8_matmul -> dequantize [-> add(bias)]  =>  int8_linear
+      matmul -> add(bias)                        =>  matmul_bias
+      add(bias) -> relu                          =>  fused_bias_relu
+    The fused node takes the place of the last node of its pattern (every
+    operand, e.g. a bias constant traced after the matmul, precedes it).
+    Returns a new Graph; node order is preserved, ids are renumbered."""
+    by_id = {n.id: n for n in graph.nodes}
+    users = _users(graph)
+
+    def only_user(nid):
+        u = users[nid]
+        return u[0] if len(u) == 1 and nid != graph.output else None
+
+    # Phase 1: find patterns.  fused[last] = (op, [operand ids]); absorbed
+    # nodes are dropped.
+    fused, absorbed = {}, set()
+    for n in graph.nodes:
+        if n.id in absorbed:
+            continue
+        if n.op == "int8_matmul":
+            dq = only_user(n.id)
+            if dq is not None and by_id[dq].op == "dequantize":
+                last, ins = dq, list(n.inputs)
+                ad = only_user(dq)
+                if ad is not None and by_id[ad].op == "add":
+                    a_in = by_id[ad].inputs
+                    if a_in[0] == dq and _is_bias(graph, by_id, dq, a_in[1]):
+                        last, ins = ad, ins + [a_in[1]]
+                absorbed.update({n.id, dq, last} - {last})
+                fused[last] = ("int8_linear", ins)
+                continue
+        if n.op == "matmul":
+            ad = only_user(n.id)
+            if ad is not None and by_id[ad].op == "add":
+                a_in = by_id[ad].inputs
+                if a_in[0] == n.id and _is_bias(graph, by_id, n.id, a_in[1]):
+                    absorbed.add(n.id)
+                    fused[ad] = ("matmul_bias", list(n.inputs) + [a_in[1]])
+                    continue
+        if n.op == "add" and n.id not in fused and len(n.inputs) == 2 and _is_bias(graph, by_id, *n.inputs):
+            r = only_user(n.id)
+            if r is not None and by_id[r].op == "relu":
+                absorbed.add(n.id)
+                fused[r] = ("fused_bias_relu", list(n.inputs))
+
+    # Phase 2: emit in order.
+    out, remap = Graph(), {}
+    for n in graph.nodes:
+        if n.id in absorbed:
+            continue
+        if n.id in fused:
+            op, ins = fused[n.id]
+            nid = out.add(op, [remap[i] for i in ins], n.shape, "float32")
+        else:
+            nid = out.add(n.op, [remap[i] for i in n.inputs], n.shape, n.dtype, **n.attrs)
+        remap[n.id] = nid
+    out.inputs = [remap[i] for i in graph.inputs]
+    out.output = remap[graph.output]
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Memory planning (kir.py:884-954)
+# ---------------------------------------------------------------------------
+
+@dataclass
+class MemoryPlan:
+    last_use: dict
+    slot_of: dict
+    num_slots: int
+    num_computed_nodes: int
+
+
+def plan_memory(graph) -> MemoryPlan:
+    """Liveness (index of each value's last reader; the output lives to the
+    end) and a greedy slot assignment in node order, reusing the most
+    recently freed slot; placeholders and constants own no slot.  The same
+    algorithm as the reference's plan_memory (kir.py:892-954)."""
+    n = len(graph.nodes)
+    last_use = {}
+    for idx, node in enumerate(graph.nodes):
+        for i in node.inputs:
+            last_use[i] = idx
+    if graph.output is not None:
+        last_use[graph.output] = n
+    slot_of, free, busy_until, next_slot = {}, [], {}, 0
+    for idx, node in enumerate(graph.nodes):
+        for sid, until in busy_until.items():
+            if until <= idx and sid not in free:
+                free.append(sid)
+        if node.op in ("placeholder", "constant"):
+            continue
+        if free:
+            sid = free.pop()
+        else:
+            sid, next_slot = next_slot, next_slot + 1
+        slot_of[node.id] = sid
+        busy_until[sid] = last_use.get(node.id, idx)
+    return MemoryPlan(last_use, slot_of, next_slot, len(slot_of))
+
+
+class DevicePool:
+    """Handle on the library's hipMalloc-backed caching pool: the role of
+    core.StoragePool (core/include/kansai/StoragePool.hpp:15-26) for device
+    memory.  Every DeviceTensor draws from it; run_hip_planned returns each
+    intermediate to it right after the value's last use."""
+
+    def stats(self) -> dict:
+        return N.pool_stats()
+
+    def num_allocated(self) -> int:
+        return N.pool_stats()["driver_allocs"]
+
+    def trim(self):
+        N.call("kh_pool_trim")
+
+
+# ---------------------------------------------------------------------------
+# Interpreter
+# ---------------------------------------------------------------------------
+
+@dataclass
+class _Acc:
+    """Value of an unfused int8_matmul: int32 accumulators + operand scales."""
+    acc: DeviceTensor
+    sa: DeviceTensor
+    sb: DeviceTensor
+
+
+def _constant(node):
+    from .quantize import QTensor
+    v = node.attrs["value"]
+    if isinstance(v, (QTensor, DeviceTensor)):
+        return v
+    cached = node.attrs.get("_dev")
+    if cached is None or cached[0] is not v:
+        cached = (v, DeviceTensor.from_host(as_host_array(v, "float32")))
+        node.attrs["_dev"] = cached  # weights stay resident across calls
+    return cached[1]
+
+
+def _dequantize(v):
+    from .quantize import QTensor
+    if isinstance(v, _Acc):
+        return H.dequantize_acc(v.acc, v.sa, v.sb)
+    if isinstance(v, QTensor):
+        return v.dequantize()
+    raise TypeError(f"dequantize: unsupported operand {type(v).__name__}")
+
+
+def _add(a, b):
+    if list(a.shape) == list(b.shape):
+        return H.add(a, b)
+    if len(a.shape) == 2 and len(b.shape) == 1 and a.shape[1] == b.shape[0]:
+        return H.add_bias(a, b)
+    raise NotImplementedError(f"run_hip: add with broadcast {a.shape} + {b.shape} has no HIP kernel")
+
+
+def _quantize_node(x, node):
+    from .quantize import QTensor
+    if node.attrs.get("granularity", "tensor") == "row":
+        q, s = H.quantize_rows(x)
+        return QTensor(q, s, list(x.shape), "row", packed=False)
+    q, s = H.quantize_tensor(x)
+    return QTensor(q, s, list(x.shape), "tensor", packed=False)
+
+
+def _int8_operands(qa, qb, what):
+    from .quantize import QTensor
+    if not (isinstance(qa, QTensor) and isinstance(qb, QTensor)):
+        raise TypeError(f"{what}: operands must be quantized")
+    if qa.packed or not qb.packed:
+        raise TypeError(f"{what}: expects quantized activations [M,K] and a packed weight [K,N]")
+    return qa.codes.reshape(qa.shape), qb.codes, qa.scales, qb.scales
+
+
+def _exec(node, vals):
+    op = node.op
+    ins = [vals[i] for i in node.inputs]
+    if op == "matmul":
+        return H.matmul(*ins)
+    if op == "matmul_bias":
+        return H.matmul(ins[0], ins[1], ins[2])
+    if op == "add":
+        return _add(*ins)
+    if op == "relu":
+        return H.relu(ins[0])
+    if op == "fused_bias_relu":
+        return H.add_bias(ins[0], ins[1], relu=True)
+    if op == "quantize":
+        return _quantize_node(ins[0], node)
+    if op == "dequantize":
+        return _dequantize(ins[0])
+    if op == "int8_matmul":
+        a, b, sa, sb = _int8_operands(ins[0], ins[1], "int8_matmul")
+        _, acc = H.gemm_i8(a, b, want_out=False, want_acc=True)
+        return _Acc(acc, sa, sb)
+    if op == "int8_linear":
+        a, b, sa, sb = _int8_operands(ins[0], ins[1], "int8_linear")
+        out, _ = H.gemm_i8(a, b, sa, sb, ins[2] if len(ins) > 2 else None)
+        return out
+    if op == "tuple":
+        return tuple(ins)
+    raise KeyError(op)
+
+
+def _release(v):
+    from .quantize import QTensor
+    if isinstance(v, DeviceTensor):
+        v.release()
+    elif isinstance(v, _Acc):
+        v.acc.release()
+    elif isinstance(v, QTensor) and v.owned:
+        v.codes.release()
+        v.scales.release()
+
+
+def _to_host(v):
+    if isinstance(v, DeviceTensor):
+        return v.numpy()
+    if isinstance(v, tuple):
+        return tuple(_to_host(x) for x in v)
+    return v
+
+
+def _run(graph, args, plan, to_host):
+    if not N.available():
+        raise RuntimeError("run_hip: no gfx950 (MI355X) device available on this system")
+    by_id = {n.id: n for n in graph.nodes}
+    vals = {}
+    for nid, a in zip(graph.inputs, args):
+        vals[nid] = a if isinstance(a, DeviceTensor) else DeviceTensor.from_host(as_host_array(a, "float32"))
+    external = set(graph.inputs)
+    for idx, node in enumerate(graph.nodes):
+        if node.op == "placeholder":
+            continue
+        if node.op == "constant":
+            vals[node.id] = _constant(node)
+            continue
+        vals[node.id] = _exec(node, vals)
+        if plan is not None:
+            for i in node.inputs:
+                src = by_id[i]
+                if src.op in ("placeholder", "constant") or i in external:
+                    continue
+                if plan.last_use.get(i) == idx and i in vals:
+                    _release(vals.pop(i))
+    out = vals[graph.output]
+    N.synchronize()  # reports a non-finite quantizer input as ValueError
+    return _to_host(out) if to_host else out
+
+
+def run_hip(graph, *args, to_host: bool = True):
+    """Runs `graph` on the GPU.  Host inputs (numpy arrays, or anything with
+    .tolist() and .shape such as the reference's Tensor) are uploaded;
+    DeviceTensors are used in place.  Returns the output as a numpy array
+    (or a DeviceTensor with to_host=False)."""
+    return _run(graph, args, None, to_host)
+
+
+def run_hip_planned(graph, plan: MemoryPlan, pool: DevicePool | None, *args, to_host: bool = True):
+    """run_planned's contract (kir.py:957-1068) on the device: every
+    intermediate is returned to the device pool right after its last use, so
+    repeated runs of the graph reuse the same device buffers and never call
+    hipMalloc after the first run.  Placeholders and constants are never
+    released; the output's ownership passes to the caller."""
+    return _run(graph, args, plan, to_host)
+
+
+def jit(fn):
+    """Traces fn on first call per input-shape key, fuses, and replays the
+    graph through run_hip (kir.py:536-555's cache, on the HIP backend)."""
+    cache: dict = {}
+
+    def wrapped(*args):
+        key = tuple(tuple(getattr(a, "shape", np.shape(a))) for a in args)
+        g = cache.get(key)
+        if g is None:
+            g = quant_fusion(trace(fn, *args))
+            cache[key] = g
+        return run_hip(g, *args)
+
+    wrapped.trace = lambda *args: trace(fn, *args)
+    return wrapped

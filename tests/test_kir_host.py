@@ -1,0 +1,105 @@
+"""Host logic of the KIR layer (no GPU): tracing the int8 path, the fusion
+pass and the memory planner (python/kansai/kir.py:884-954's algorithm)."""
+
+import numpy as np
+import pytest
+
+from kansai_amd import kir
+
+
+def _linear_int8(x, w_q, bias, gran="tensor"):
+    return x.quantize(gran).int8_matmul(w_q).dequantize().add(bias)
+
+
+def test_trace_int8_linear_and_fuse():
+    bias = np.zeros(8, np.float32)
+
+    def fn(x, w):
+        return _linear_int8(x, w.quantize("tensor"), bias)
+
+    g = kir.trace(fn, np.zeros((4, 16), np.float32), np.zeros((16, 8), np.float32))
+    ops = [n.op for n in g.nodes]
+    assert ops == ["placeholder", "placeholder", "quantize", "quantize", "int8_matmul", "dequantize", "constant",
+                   "add"]
+    assert g.nodes[4].dtype == "int32" and g.nodes[4].shape == [4, 8]
+    f = kir.quant_fusion(g)
+    fops = [n.op for n in f.nodes]
+    assert "int8_linear" in fops and "int8_matmul" not in fops and "dequantize" not in fops
+    lin = [n for n in f.nodes if n.op == "int8_linear"][0]
+    assert len(lin.inputs) == 3 and f.output == lin.id
+    assert f.inputs == [0, 1]
+
+
+def test_fusion_keeps_shared_intermediates():
+    """An intermediate read twice must not be fused away."""
+    def fn(x, w):
+        acc = x.quantize().int8_matmul(w.quantize())
+        d = acc.dequantize()
+        return d.add(d)
+
+    g = kir.trace(fn, np.zeros((4, 16), np.float32), np.zeros((16, 8), np.float32))
+    f = kir.quant_fusion(g)
+    ops = [n.op for n in f.nodes]
+    assert "int8_linear" in ops  # int8_matmul -> dequantize fused; the add reads it twice
+    assert ops[-1] == "add"
+    assert f.nodes[-1].inputs[0] == f.nodes[-1].inputs[1]
+
+
+def test_matmul_bias_and_bias_relu_fusion():
+    b1 = np.zeros(8, np.float32)
+    w1 = np.zeros((16, 8), np.float32)
+
+    def fn(x):
+        return x.matmul(w1).add(b1).relu()
+
+    g = kir.trace(fn, np.zeros((4, 16), np.float32))
+    f = kir.quant_fusion(g)
+    assert [n.op for n in f.nodes if n.op not in ("placeholder", "constant")] == ["matmul_bias", "relu"]
+
+
+def test_trace_shape_errors():
+    with pytest.raises(ValueError):
+        kir.trace(lambda x: x.matmul(np.zeros((3, 2), np.float32)), np.zeros((4, 5), np.float32))
+    with pytest.raises(ValueError):
+        kir.trace(lambda x: x.int8_matmul(x), np.zeros((4, 4), np.float32))
+    with pytest.raises(ValueError):
+        kir.trace(lambda x: x.quantize("col"), np.zeros((4, 4), np.float32))
+
+
+def test_plan_memory_chain_reuses_slots():
+    """A 6-deep chain of computed nodes: each op's input dies at that op, so
+    (as in the reference's planner, which releases inputs after the op runs)
+    the whole chain fits in one slot."""
+    g = kir.Graph()
+    x = g.placeholder([4, 4])
+    cur = x
+    for _ in range(6):
+        cur = g.add("relu", [cur], [4, 4])
+    g.output = cur
+    plan = kir.plan_memory(g)
+    assert plan.num_computed_nodes == 6
+    assert plan.num_slots == 1
+    assert plan.last_use[g.output] == len(g.nodes)
+    assert x not in plan.slot_of
+
+
+def test_plan_memory_matches_liveness_brute_force():
+    """Slots never overlap in time: brute-force interval check on a random DAG."""
+    rng = np.random.default_rng(0)
+    for trial in range(20):
+        g = kir.Graph()
+        ids = [g.placeholder([2, 2])]
+        ids.append(g.add("constant", [], [2, 2]))
+        for _ in range(15):
+            k = int(rng.integers(1, 3))
+            ins = [int(v) for v in rng.choice(ids, size=k)]
+            ids.append(g.add("add" if k == 2 else "relu", ins, [2, 2]))
+        g.output = ids[-1]
+        plan = kir.plan_memory(g)
+        live = {}
+        for nid, sid in plan.slot_of.items():
+            live.setdefault(sid, []).append((nid, plan.last_use.get(nid, nid)))
+        for sid, iv in live.items():
+            iv.sort()
+            for (a0, a1), (b0, b1) in zip(iv, iv[1:]):
+                assert a1 <= b0, f"slot {sid} reused while live (trial {trial})"
