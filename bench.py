@@ -133,6 +133,54 @@ def bench_f32(H, D, steps, warmup):
     return ms, 2.0 * n ** 3 / (ms * 1e-3) / 1e12
 
 
+def bench_skinny(steps):
+    """Config C5: kh_linear_i8 (per-token quantize of fp32 x, int8 GEMM,
+    per-output-channel weight scales, fused epilogue) for M in {1, 8, 32},
+    (K, N) in {(4096, 4096), (4096, 11008)}.  Weight copies are rotated so
+    more than 512 MB of distinct weights pass through HBM (beyond the 256 MB
+    Infinity Cache).  Each launch pair is bracketed by its own HIP events, so
+    host launch gaps are excluded."""
+    from kansai_amd import _native as Nn
+    from kansai_amd.device import DeviceTensor as D
+    gen = np.random.Generator(np.random.PCG64(5))
+    rows = []
+    for K, N in ((4096, 4096), (4096, 11008)):
+        copies = max(2, -(-(512 << 20) // (N * K)))
+        ws = [D([N, K], "int8") for _ in range(copies)]
+        w0 = gen.integers(-127, 128, (N, K), dtype=np.int8)
+        for w in ws:
+            Nn.call("kh_memcpy_h2d", w.ptr, w0.ctypes.data, N * K)
+        sw = D.from_host(gen.uniform(1e-3, 1e-2, N))
+        bias = D.from_host(np.zeros(N, np.float32))
+        for M in (1, 8, 32):
+            x = D.from_host(gen.standard_normal((M, K), dtype=np.float32))
+            q = D([M, K], "int8")
+            sx = D([M], "float64")
+            out = D([M, N], "float32")
+            call = lambda w: Nn.call("kh_linear_i8", x.ptr, M, K, w.ptr, N, sw.ptr, 1, bias.ptr, q.ptr, sx.ptr,  # noqa: E731
+                                     out.ptr)
+            for i in range(3):
+                call(ws[i % copies])
+            Nn.synchronize()
+            evs = [(Nn.Event(), Nn.Event()) for _ in range(steps)]
+            for i, (e0, e1) in enumerate(evs):
+                e0.record()
+                call(ws[i % copies])
+                e1.record()
+            Nn.synchronize()
+            us = sum(e0.elapsed_ms(e1) for e0, e1 in evs) / steps * 1e3
+            nbytes = N * K + 8 * N + 4 * M * K + 2 * M * K + 4 * M * N
+            gbs = nbytes / (us * 1e-6) / 1e9
+            rows.append({"M": M, "K": K, "N": N, "us": round(us, 2), "GB/s": round(gbs, 1),
+                         "TOPS": round(2.0 * M * N * K / (us * 1e-6) / 1e12, 2),
+                         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                                      "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}})
+            log(f"skinny M={M} K={K} N={N}: {us:.2f} us, {gbs:.0f} GB/s")
+        del ws
+        Nn.call("kh_pool_trim")
+    return rows
+
+
 COPY_BYTES = 1 << 30
 
 
@@ -259,7 +307,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", default="gemm,quant,f32", help="comma list of gemm,quant,f32,copy")
+    ap.add_argument("--only", default="gemm,quant,f32,skinny", help="comma list of gemm,quant,f32,skinny,copy")
     ap.add_argument("--summarize", metavar="DIR", help="summarize rocprofv3 CSV output and exit")
     args = ap.parse_args()
     if args.summarize:
@@ -298,6 +346,10 @@ def main():
         f_ms, f_tflops = bench_f32(H, D, max(5, args.steps // 2), max(2, args.warmup // 2))
         log(f"fp32 matmul: {f_ms:.4f} ms, {f_tflops:.1f} TFLOP/s")
         Nn.call("kh_pool_trim")
+    skinny = None
+    if "skinny" in only:
+        log("skinny decode GEMMs C5 ...")
+        skinny = bench_skinny(max(20, args.steps))
     if "copy" in only:
         c_ms, c_gbs = bench_copy(args.steps, args.warmup)
         log(f"1 GiB d2d copy: {c_ms:.4f} ms, {c_gbs:.0f} GB/s")
@@ -341,6 +393,8 @@ def main():
                         "roofline": {"bound": "mfma", "achieved": round(f_tflops, 2), "peak": PEAK_FP32_TFLOPS,
                                      "unit": "TFLOP/s", "frac": round(f_tflops / PEAK_FP32_TFLOPS, 4),
                                      "traffic": None}},
+        "skinny_decode": {"workload": "C5 kh_linear_i8: per-token quantize + int8 GEMM, per-channel weights",
+                          "bytes": "N*K + 8N + 4MK + 2MK + 4MN", "rows": skinny},
         "cpu_baseline": cpu,
         "device": info,
     }

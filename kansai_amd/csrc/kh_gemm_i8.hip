@@ -416,6 +416,96 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_i8_tiled_kernel(const int8_
         }
 }
 
+// ---------------------------------------------------------------------------
+// Skinny GEMM for decode-style shapes (M <= 32): weight streaming.
+//
+// A workgroup owns 16 output columns for all M rows; its SKW waves split K,
+// each streaming its slice of those 16 packed weight rows (16 B per lane per
+// 64-k step) through v_mfma_i32_16x16x64_i8 with up to two 16-row tiles of
+// activations.  Rows >= M read zeros: their buffer offsets fall past the
+// activation resource, whose loads return 0.  The waves' partial int32
+// accumulators are summed through LDS (integer sums are exact in any order)
+// and the first wave applies the epilogue.  Bound: HBM bytes of the weight,
+// N*K, plus the activations (L2 resident) and the output.
+// ---------------------------------------------------------------------------
+typedef int i32x4v __attribute__((ext_vector_type(4)));
+constexpr int kSkinnyWaves = 8;
+
+template <int MT>
+__global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_i8_skinny_kernel(const int8_t* __restrict__ A,
+                                                                           const int8_t* __restrict__ B, int M,
+                                                                           int N, int K, Epilogue ep) {
+    __shared__ i32x4v red[kSkinnyWaves][MT][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n0 = blockIdx.x * 16;
+    const int col = n0 + (lane & 15);
+    const int kg = (lane >> 4) * 16;
+    const int kper = K / kSkinnyWaves;
+    const int k_begin = wave * kper;
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, (uint32_t)M * (uint32_t)K);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(B, (uint32_t)N * (uint32_t)K);
+    const int b_off = min(col, N - 1) * K + kg;
+    int a_off[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) a_off[t] = (t * 16 + (lane & 15)) * K + kg;
+
+    i32x4v acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = i32x4v{0, 0, 0, 0};
+#pragma unroll 8
+    for (int k = k_begin; k < k_begin + kper; k += 64) {
+        const i32x4v b = __builtin_amdgcn_raw_buffer_load_b128(rb, b_off, k, 0);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            const i32x4v a = __builtin_amdgcn_raw_buffer_load_b128(ra, a_off[t], k, 0);
+            acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc[t], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < MT; ++t) red[wave][t][lane] = acc[t];
+    __syncthreads();
+    if (wave != 0) return;
+    // 16x16 MFMA result layout: register r of lane l holds row 4*(l/16) + r,
+    // column l%16.
+    const int64_t j = col;
+    if (j >= N) return;
+    const double sbj = ep.sb ? ep.sb[ep.sb_per_col ? j : 0] : 0.0;
+    const float bj = ep.bias ? ep.bias[j] : 0.0f;
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+        i32x4v sum = red[0][t][lane];
+#pragma unroll
+        for (int w = 1; w < kSkinnyWaves; ++w) sum += red[w][t][lane];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t i = t * 16 + 4 * (lane >> 4) + r;
+            if (i >= M) continue;
+            if (ep.acc) ep.acc[i * N + j] = sum[r];
+            if (ep.out) {
+                const double s = ep.sa[ep.sa_per_row ? i : 0] * sbj;
+                float y = (float)((double)sum[r] * s);
+                if (ep.bias) y = y + bj;
+                ep.out[i * N + j] = y;
+            }
+        }
+    }
+}
+
+bool skinny_fits(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K) {
+    return M >= 1 && M <= 32 && K > 0 && K % (64 * kSkinnyWaves) == 0 && kh::aligned(A, 16) &&
+           kh::aligned(B, 16) && M * K <= 0xFFFFFFFFLL && N * K <= 0xFFFFFFFFLL && N <= 0x7FFFFFFF;
+}
+
+int launch_skinny(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
+                  const Epilogue& ep) {
+    const unsigned blocks = (unsigned)((N + 15) / 16);
+    if (M <= 16)
+        gemm_i8_skinny_kernel<1><<<blocks, kSkinnyWaves * 64, 0, d->stream>>>(A, B, (int)M, (int)N, (int)K, ep);
+    else
+        gemm_i8_skinny_kernel<2><<<blocks, kSkinnyWaves * 64, 0, d->stream>>>(A, B, (int)M, (int)N, (int)K, ep);
+    return kh::launch_status("gemm_i8_skinny");
+}
+
 template <int BM, int BN, int BK, int WM, int WN, int STAGES, int HINT, int PRIO>
 int launch_tiled(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
                  const Epilogue& ep, int group_m) {
@@ -459,6 +549,7 @@ int kh_gemm_i8(const int8_t* a, const int8_t* b_packed, int64_t M, int64_t N, in
     KH_REQUIRE(!out || (sa && sb), "kh_gemm_i8: scales required when out is given");
     KH_DEVICE_OR_RETURN(d);
     Epilogue ep{sa, sb, bias, out, acc_out, sa_per_row, sb_per_col};
+    if (skinny_fits(a, b_packed, M, N, K)) return launch_skinny(d, a, b_packed, M, N, K, ep);
     if (tiled_fits<256, 256, 128>(a, b_packed, M, N, K))
         return launch_tiled<256, 256, 128, 2, 4, 2, 1, 0>(d, a, b_packed, M, N, K, ep, 8);
     const bool vec16 = (K % 16 == 0) && kh::aligned(a, 16) && kh::aligned(b_packed, 16);

@@ -46,6 +46,7 @@ SHAPES = [
     (256, 1536, 384), (256, 384, 1536),
     (129, 257, 80), (300, 200, 48), (2048, 2048, 512), (2304, 2176, 1024),
     (33, 40, 130), (100, 50, 77), (5, 7, 3),  # K % 16 != 0: byte-gather path
+    (2, 100, 512), (17, 4096, 4096), (31, 64, 1024), (16, 16, 512), (5, 11008, 4096), (32, 40, 512),  # skinny
 ]
 
 
@@ -107,6 +108,28 @@ def test_gemm_i8_c3a_full_size(hip):
     cols = gen.choice(N, size=64, replace=False)
     eacc_c = (a.astype(np.int64)[::97] @ bt[cols].astype(np.int64).T).astype(np.int32)
     np.testing.assert_array_equal(acc[::97][:, cols], eacc_c)
+
+
+@pytest.mark.parametrize("M", [1, 3, 8, 16, 17, 32])
+def test_skinny_per_token_and_per_channel(hip, M):
+    """Config C5 shapes through kh_linear_i8: per-token activations, per-output-
+    channel weights with 0.5% outlier columns x20, K=4096, N=11008."""
+    H, D = hip
+    K, N = 4096, 11008
+    gen = np.random.Generator(np.random.PCG64(100 + M))
+    x = gen.standard_normal((M, K), dtype=np.float32)
+    w = gen.standard_normal((K, N), dtype=np.float32) * np.float32(0.02)
+    cols = gen.choice(N, size=N // 200, replace=False)
+    w[:, cols] *= np.float32(20.0)
+    bias = gen.standard_normal(N).astype(np.float32)
+    wd = D.from_host(w)
+    qw, sw = H.quantize_cols_packed(wd)
+    out = H.linear_i8(D.from_host(x), qw, sw, D.from_host(bias)).numpy()
+    eqw, esw = O.ko_quantize_cols_packed(w)
+    np.testing.assert_array_equal(qw.numpy(), eqw)
+    qx, sx = O.ko_quantize_rows(x)
+    expect = O.ko_epilogue(O.ko_gemm_i8(qx, eqw), sx, esw, bias)
+    np.testing.assert_array_equal(bits32(out), bits32(expect))
 
 
 def test_linear_i8_per_token(hip):
