@@ -191,6 +191,30 @@ int kh_add_bias(const float* x, const float* bias, float* out, int64_t batch, in
  * kan::cpu::relu_fwd (backend/cpu/src/Ops.cpp:197-199). */
 int kh_relu(const float* x, float* out, int64_t n);
 
+/* ---- fp32 pieces of a decoder block (config C4) -------------------------- */
+
+/* out[r, :] = tok[ids[r], :] + pos[r % T, :] -- nn.Embedding lookups summed
+ * (python/kansai/nn.py:624-646; examples/tinyshakespeare/
+ * train_shakespeare_large.py:72-75).  ids: int32 [rows]; tok [V, D];
+ * pos [T, D].  An id outside [0, V) is reported by kh_synchronize
+ * (KH_ERR_INVALID_ARG). */
+int kh_embedding(const int32_t* ids, int64_t rows, int T, const float* tok, int V, const float* pos, int D,
+                 float* out);
+
+/* LayerNorm over the last axis (nn.py:308-331): biased variance,
+ * (x - mean) / sqrt(var + eps) * weight + bias.  D <= 1024. */
+int kh_layernorm(const float* x, int64_t rows, int D, const float* weight, const float* bias, float eps, float* out);
+
+/* Exact-erf GELU (backend/cpu/src/Ops.cpp:250-256). */
+int kh_gelu(const float* x, float* out, int64_t n);
+
+/* Causal multi-head self-attention core of nn.MultiHeadAttention.forward
+ * (nn.py:381-427) with the additive causal mask of
+ * train_shakespeare_large.py:69-70: per head softmax(Q K^T / sqrt(dk) +
+ * mask) V.  qkv: [B*T, 3*H*dk], the fused Q|K|V projection (head h of Q at
+ * columns h*dk..); out: [B*T, H*dk] with heads merged in place.  dk == 64. */
+int kh_causal_attention(const float* qkv, int B, int T, int H, int dk, float* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -72,6 +72,10 @@ _SIGNATURES = {
     "kh_add": [_vp, _vp, _vp, _i64],
     "kh_add_bias": [_vp, _vp, _vp, _i64, _i64, _int],
     "kh_relu": [_vp, _vp, _i64],
+    "kh_embedding": [_vp, _i64, _int, _vp, _int, _vp, _int, _vp],
+    "kh_layernorm": [_vp, _i64, _int, _vp, _vp, ctypes.c_float, _vp],
+    "kh_gelu": [_vp, _vp, _i64],
+    "kh_causal_attention": [_vp, _int, _int, _int, _int, _vp],
 }
 _RESTYPES = {"kh_last_error": ctypes.c_char_p}
 

@@ -1,0 +1,131 @@
+"""Config C4: the quantized decoder-only char-LM forward on the HIP backend.
+
+The architecture is the reference's BigGPT
+(examples/tinyshakespeare/train_shakespeare_large.py:61-79) built from its
+nn modules (python/kansai/nn.py): token + learned position embedding,
+N pre-LN TransformerBlocks (nn.py:430-478: x + attn(LN1 x), then
+x + fc2(GELU(fc1(LN2 x)))) under one causal mask, a final LayerNorm and the
+vocabulary head.  MultiHeadAttention (nn.py:334-427) has no projection bias;
+the FFN Linears and the head do.
+
+Every Linear is int8 here: weights quantized once per output channel
+(packed [out, in]), activations quantized per tensor on the fly, int32
+accumulation, dequantize + bias in the GEMM epilogue.  Q, K and V share one
+GEMM (their weights concatenated to [D, 3D]; with per-channel weight scales
+this is the same arithmetic as three GEMMs).  Softmax, LayerNorm, GELU and
+the residual adds are fp32.  The forward is traced once into a KIR graph,
+fused, and replayed with run_hip_planned.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+from . import kir
+from .device import DeviceTensor
+from .quantize import QTensor
+
+
+class CharLMWeights:
+    """fp32 parameters of the model, host side (numpy), seeded."""
+
+    def __init__(self, vocab=65, d_model=384, heads=6, layers=6, d_ff=1536, seq=256, seed=0, std=0.02,
+                 bias_std=0.0):
+        g = np.random.Generator(np.random.PCG64(seed))
+        f32 = np.float32
+        self.vocab, self.d_model, self.heads, self.layers, self.d_ff, self.seq = vocab, d_model, heads, layers, d_ff, seq
+        # nn.Embedding: std 1/sqrt(embed_dim) (nn.py:637-641)
+        self.tok = (g.standard_normal((vocab, d_model)) / math.sqrt(d_model)).astype(f32)
+        self.pos = (g.standard_normal((seq, d_model)) / math.sqrt(d_model)).astype(f32)
+
+        def lin(i, o):
+            return (g.standard_normal((i, o)) * std).astype(f32)
+
+        def bias(o):
+            return (g.standard_normal(o) * bias_std).astype(f32) if bias_std else np.zeros(o, f32)
+
+        self.blocks = []
+        for _ in range(layers):
+            self.blocks.append(dict(
+                ln1_w=np.ones(d_model, f32), ln1_b=np.zeros(d_model, f32),
+                w_q=lin(d_model, d_model), w_k=lin(d_model, d_model), w_v=lin(d_model, d_model),
+                w_o=lin(d_model, d_model),
+                ln2_w=np.ones(d_model, f32), ln2_b=np.zeros(d_model, f32),
+                fc1_w=lin(d_model, d_ff), fc1_b=bias(d_ff), fc2_w=lin(d_ff, d_model), fc2_b=bias(d_model)))
+        self.lnf_w, self.lnf_b = np.ones(d_model, f32), np.zeros(d_model, f32)
+        self.head_w, self.head_b = lin(d_model, vocab), bias(vocab)
+
+
+class CharLM:
+    """Device-resident int8 model; `forward(ids)` returns fp32 logits
+    [batch * seq, vocab] (numpy by default)."""
+
+    def __init__(self, w: CharLMWeights):
+        self.w = w
+        up = DeviceTensor.from_host
+        self.tok, self.pos = up(w.tok), up(w.pos)
+        self.blocks = []
+        for b in w.blocks:
+            self.blocks.append(dict(
+                ln1_w=up(b["ln1_w"]), ln1_b=up(b["ln1_b"]),
+                w_qkv=QTensor.from_weight(np.concatenate([b["w_q"], b["w_k"], b["w_v"]], axis=1), "col"),
+                w_o=QTensor.from_weight(b["w_o"], "col"),
+                ln2_w=up(b["ln2_w"]), ln2_b=up(b["ln2_b"]),
+                fc1=QTensor.from_weight(b["fc1_w"], "col"), fc1_b=up(b["fc1_b"]),
+                fc2=QTensor.from_weight(b["fc2_w"], "col"), fc2_b=up(b["fc2_b"])))
+        self.lnf_w, self.lnf_b = up(w.lnf_w), up(w.lnf_b)
+        self.head, self.head_b = QTensor.from_weight(w.head_w, "col"), up(w.head_b)
+        self._graphs = {}
+
+    def _fn(self, batch, seq):
+        def linear(x, qw, b=None):
+            y = x.quantize("tensor").int8_matmul(qw).dequantize()
+            return y.add(b) if b is not None else y
+
+        def fn(ids):
+            x = ids.embedding(self.tok, self.pos)
+            for p in self.blocks:
+                h = x.layer_norm(p["ln1_w"], p["ln1_b"])
+                a = linear(h, p["w_qkv"]).causal_attention(batch, seq, self.w.heads)
+                x = x.add(linear(a, p["w_o"]))
+                h = x.layer_norm(p["ln2_w"], p["ln2_b"])
+                x = x.add(linear(linear(h, p["fc1"], p["fc1_b"]).gelu(), p["fc2"], p["fc2_b"]))
+            x = x.layer_norm(self.lnf_w, self.lnf_b)
+            return linear(x, self.head, self.head_b)
+
+        return fn
+
+    def graph(self, batch, seq):
+        key = (batch, seq)
+        if key not in self._graphs:
+            g = kir.quant_fusion(kir.trace(self._fn(batch, seq), np.zeros((batch, seq), np.int32)))
+            self._graphs[key] = (g, kir.plan_memory(g))
+        return self._graphs[key]
+
+    def forward(self, ids, to_host: bool = True):
+        ids = np.asarray(ids, np.int32) if not isinstance(ids, DeviceTensor) else ids
+        batch, seq = ids.shape
+        if seq > self.w.seq:
+            raise ValueError(f"sequence length {seq} exceeds the position table ({self.w.seq})")
+        g, plan = self.graph(batch, seq)
+        return kir.run_hip_planned(g, plan, None, ids, to_host=to_host)
+
+    __call__ = forward
+
+
+def int8_linear_ops(w: CharLMWeights, batch: int, seq: int) -> float:
+    """Integer ops (2*M*N*K) of the model's int8 Linear layers per forward."""
+    m = batch * seq
+    d, f = w.d_model, w.d_ff
+    per_block = 2 * m * d * (3 * d) + 2 * m * d * d + 2 * m * d * f + 2 * m * f * d
+    return w.layers * per_block + 2 * m * d * w.vocab
+
+
+def attention_flops(w: CharLMWeights, batch: int, seq: int) -> float:
+    """fp32 flops of QK^T and PV per forward, counted as full squares
+    (2 * 2 * batch * heads * seq^2 * dk per layer; the causal kernel skips the
+    masked half)."""
+    dk = w.d_model // w.heads
+    return w.layers * 2 * 2 * batch * w.heads * seq * seq * dk

@@ -26,6 +26,7 @@ int launch_status(const char* kernel);
 // Bits of the device fault word (set by kernels with a vector atomic OR,
 // read and cleared by kh_synchronize).
 constexpr unsigned kFaultNonFinite = 1u;
+constexpr unsigned kFaultBadIndex = 2u;
 
 struct Device {
     int id = -1;

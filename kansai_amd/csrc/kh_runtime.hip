@@ -208,6 +208,8 @@ int kh_synchronize(void) {
         if (rc) return rc;
         if (fault & kh::kFaultNonFinite)
             return fail(KH_ERR_NONFINITE, "cannot quantize a non-finite value (NaN or inf)");
+        if (fault & kh::kFaultBadIndex)
+            return fail(KH_ERR_INVALID_ARG, "embedding: token id out of range");
     }
     return KH_OK;
 }

@@ -23,6 +23,12 @@ at trace time, kir.py:129-136):
                 GEMM with the dequantize + bias epilogue
   matmul_bias   fusion of fp32 matmul -> add(bias) (bias in the GEMM store)
   fused_bias_relu  add(bias) -> relu (the reference's pattern, kir.py:581-600)
+
+and, for a decoder block (config C4), fused forms of what the reference
+composes from generic ops (nn.py:308-478): embedding (token + position
+lookup on int32 ids), layer_norm, gelu, causal_attention (the per-head
+softmax(Q K^T / sqrt(d_k) + causal mask) V core of MultiHeadAttention on a
+fused Q|K|V projection, heads merged in place).
 """
 
 from __future__ import annotations
@@ -151,15 +157,53 @@ class TraceValue:
             raise ValueError("dequantize: operand is not quantized")
         return self._emit("dequantize", [self], self.shape, "float32")
 
+    # -- decoder-block pieces (config C4) -----------------------------------
+    def embedding(self, tok, pos):
+        """self: int32 ids [B, T]; tok [V, D]; pos [T, D] -> [B*T, D]."""
+        if self.dtype != "int32" or len(self.shape) != 2:
+            raise ValueError("embedding: expects int32 token ids [batch, seq]")
+        tok, pos = self._coerce(tok), self._coerce(pos)
+        if pos.shape[0] < self.shape[1] or tok.shape[1] != pos.shape[1]:
+            raise ValueError(f"embedding: tables {tok.shape} / {pos.shape} do not fit ids {self.shape}")
+        return self._emit("embedding", [self, tok, pos], [self.shape[0] * self.shape[1], tok.shape[1]],
+                          seq=self.shape[1])
+
+    def layer_norm(self, weight, bias, eps: float = 1e-5):
+        weight, bias = self._coerce(weight), self._coerce(bias)
+        if len(self.shape) != 2 or weight.shape != [self.shape[1]] or bias.shape != [self.shape[1]]:
+            raise ValueError("layer_norm: expects [rows, D] with weight and bias of shape [D]")
+        return self._emit("layer_norm", [self, weight, bias], self.shape, eps=float(eps))
+
+    def gelu(self):
+        return self._emit("gelu", [self], self.shape)
+
+    def causal_attention(self, batch: int, seq: int, heads: int):
+        """self: fused Q|K|V projection [batch*seq, 3*D] -> [batch*seq, D]."""
+        if len(self.shape) != 2 or self.shape[0] != batch * seq or self.shape[1] % (3 * heads):
+            raise ValueError(f"causal_attention: {self.shape} is not [batch*seq, 3*D] for {heads} heads")
+        return self._emit("causal_attention", [self], [self.shape[0], self.shape[1] // 3], batch=batch, seq=seq,
+                          heads=heads)
+
+
+def _example_dtype(x) -> str:
+    dt = getattr(x, "dtype", None)
+    if isinstance(dt, str):
+        return dt
+    if dt is not None and np.issubdtype(np.dtype(dt), np.integer):
+        return "int32"
+    return "float32"
+
 
 def trace(fn, *example_inputs) -> Graph:
     """Records fn applied to placeholders shaped like example_inputs
-    (kir.py:393-407)."""
+    (kir.py:393-407).  Integer examples (token ids) become int32
+    placeholders."""
     g = Graph()
     args = []
     for x in example_inputs:
         shape = list(getattr(x, "shape", np.shape(x)))
-        args.append(TraceValue(g, g.placeholder(shape), shape))
+        dt = _example_dtype(x)
+        args.append(TraceValue(g, g.placeholder(shape, dt), shape, dt))
     g.output = fn(*args).node_id
     return g
 
@@ -384,6 +428,28 @@ def _exec(node, vals):
         a, b, sa, sb = _int8_operands(ins[0], ins[1], "int8_linear")
         out, _ = H.gemm_i8(a, b, sa, sb, ins[2] if len(ins) > 2 else None)
         return out
+    if op == "embedding":
+        ids, tok, pos = ins
+        rows, D = node.shape
+        out = DeviceTensor([rows, D], "float32")
+        N.call("kh_embedding", ids.ptr, rows, node.attrs["seq"], tok.ptr, tok.shape[0], pos.ptr, D, out.ptr)
+        return out
+    if op == "layer_norm":
+        x, w, b = ins
+        out = DeviceTensor(x.shape, "float32")
+        N.call("kh_layernorm", x.ptr, x.shape[0], x.shape[1], w.ptr, b.ptr, node.attrs.get("eps", 1e-5), out.ptr)
+        return out
+    if op == "gelu":
+        out = DeviceTensor(ins[0].shape, "float32")
+        N.call("kh_gelu", ins[0].ptr, out.ptr, ins[0].numel())
+        return out
+    if op == "causal_attention":
+        qkv = ins[0]
+        heads = node.attrs["heads"]
+        out = DeviceTensor(node.shape, "float32")
+        N.call("kh_causal_attention", qkv.ptr, node.attrs["batch"], node.attrs["seq"], heads,
+               node.shape[1] // heads, out.ptr)
+        return out
     if op == "tuple":
         return tuple(ins)
     raise KeyError(op)
@@ -414,7 +480,8 @@ def _run(graph, args, plan, to_host):
     by_id = {n.id: n for n in graph.nodes}
     vals = {}
     for nid, a in zip(graph.inputs, args):
-        vals[nid] = a if isinstance(a, DeviceTensor) else DeviceTensor.from_host(as_host_array(a, "float32"))
+        dt = by_id[nid].dtype if by_id[nid].dtype in ("float32", "int32") else "float32"
+        vals[nid] = a if isinstance(a, DeviceTensor) else DeviceTensor.from_host(as_host_array(a, dt))
     external = set(graph.inputs)
     for idx, node in enumerate(graph.nodes):
         if node.op == "placeholder":

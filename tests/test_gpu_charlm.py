@@ -1,0 +1,124 @@
+"""GPU parity for config C4 (the int8 char-LM forward): each fp32 kernel
+against numpy, then the whole model against the CPU restatement
+(oracle/charlm_ref.py, whose int8 steps are the C oracle's)."""
+
+import numpy as np
+import pytest
+from scipy.special import erf
+
+from oracle import charlm_ref as R
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def G():
+    from kansai_amd import _native as N
+    from kansai_amd.device import DeviceTensor as D
+    assert N.available(), "no gfx950 device"
+    return N, D
+
+
+@pytest.mark.parametrize("rows,d", [(1, 384), (37, 384), (256, 64), (5, 1000), (8, 1024)])
+def test_layernorm(G, rows, d):
+    N, D = G
+    gen = np.random.Generator(np.random.PCG64(rows * 31 + d))
+    x = (gen.standard_normal((rows, d)) * 3 + 1).astype(np.float32)
+    w = gen.standard_normal(d).astype(np.float32)
+    b = gen.standard_normal(d).astype(np.float32)
+    out = D([rows, d])
+    xd, wd, bd = D.from_host(x), D.from_host(w), D.from_host(b)  # keep the buffers alive across the call
+    N.call("kh_layernorm", xd.ptr, rows, d, wd.ptr, bd.ptr, 1e-5, out.ptr)
+    x64 = x.astype(np.float64)
+    m = x64.mean(-1, keepdims=True)
+    ref = (x64 - m) / np.sqrt(((x64 - m) ** 2).mean(-1, keepdims=True) + 1e-5) * w + b
+    assert np.abs(out.numpy() - ref).max() < 2e-5 * (1 + np.abs(ref).max())
+
+
+def test_gelu(G):
+    N, D = G
+    x = np.linspace(-8, 8, 100_001, dtype=np.float32)
+    out = D([x.size])
+    xd = D.from_host(x)
+    N.call("kh_gelu", xd.ptr, out.ptr, x.size)
+    x64 = x.astype(np.float64)
+    ref = x64 * 0.5 * (1 + erf(x64 / np.sqrt(2)))
+    assert np.abs(out.numpy() - ref).max() < 4e-6 * max(1.0, np.abs(ref).max())
+
+
+def test_embedding_exact_and_bad_id(G):
+    N, D = G
+    gen = np.random.Generator(np.random.PCG64(3))
+    tok = gen.standard_normal((65, 48)).astype(np.float32)
+    pos = gen.standard_normal((20, 48)).astype(np.float32)
+    ids = gen.integers(0, 65, (3, 20)).astype(np.int32)
+    out = D([60, 48])
+    idd, td, pd = D.from_host(ids), D.from_host(tok), D.from_host(pos)
+    N.call("kh_embedding", idd.ptr, 60, 20, td.ptr, 65, pd.ptr, 48, out.ptr)
+    ref = tok[ids.reshape(-1)] + np.tile(pos, (3, 1))
+    np.testing.assert_array_equal(out.numpy().view(np.uint32), ref.astype(np.float32).view(np.uint32))
+    ids[1, 4] = 65
+    idd = D.from_host(ids)
+    N.call("kh_embedding", idd.ptr, 60, 20, td.ptr, 65, pd.ptr, 48, out.ptr)
+    with pytest.raises(RuntimeError):
+        N.synchronize()
+    N.synchronize()
+
+
+@pytest.mark.parametrize("batch,seq,heads", [(2, 1, 2), (2, 5, 3), (1, 64, 2), (2, 100, 2), (2, 256, 6)])
+def test_causal_attention(G, batch, seq, heads):
+    N, D = G
+    gen = np.random.Generator(np.random.PCG64(batch * 1000 + seq * 10 + heads))
+    dm = heads * 64
+    qkv = (gen.standard_normal((batch * seq, 3 * dm)) * 1.5).astype(np.float32)
+    out = D([batch * seq, dm])
+    qd = D.from_host(qkv)
+    N.call("kh_causal_attention", qd.ptr, batch, seq, heads, 64, out.ptr)
+    ref = R.causal_attention(qkv.astype(np.float64), batch, seq, heads)
+    assert np.abs(out.numpy() - ref).max() < 2e-5
+
+
+@pytest.mark.parametrize("seq", [64, 100])
+def test_small_model_matches_restatement(G, seq):
+    """Two layers of the C4 architecture (d 384, 6 heads, FFN 1536, vocab 65)
+    with nonzero biases.  The int8 steps are exact on both sides; fp32
+    rounding in LayerNorm / softmax / GELU can move an activation across a
+    quantization boundary, which changes a logit by at most a few
+    quantization steps, so the bound is 5e-3 absolute against logits of
+    magnitude ~1."""
+    from kansai_amd.charlm import CharLM, CharLMWeights
+    w = CharLMWeights(layers=2, seq=128, seed=1, bias_std=0.02)
+    ids = np.random.Generator(np.random.PCG64(2)).integers(0, 65, (2, seq)).astype(np.int32)
+    model = CharLM(w)
+    y = model(ids)
+    ref = R.forward(w, ids)
+    assert y.shape == (2 * seq, 65)
+    err = np.abs(y - ref)
+    assert err.max() < 5e-3, err.max()
+    assert err.mean() < 1e-4, err.mean()
+    # and the int8 model stays near the fp32 one (quantization error)
+    fp = R.forward(w, ids, quantized=False)
+    assert np.abs(y - fp).max() < 0.1 * np.abs(fp).max()
+    # repeated forwards through the memory plan are identical
+    np.testing.assert_array_equal(model(ids).view(np.uint32), y.view(np.uint32))
+
+
+def test_full_c4_forward_runs(G):
+    """Config C4 at full size: vocab 65, d 384, 6 heads, 6 layers, FFN 1536,
+    seq 256, batch 64.  Per-tensor activation scales span the whole batch, so
+    the int8 restatement cannot be sliced to a quick size; exactness of the
+    int8 arithmetic is established by test_small_model_matches_restatement,
+    and the full-size check is determinism plus the quantization-error bound
+    against the fp32 model: max and mean deviation within 10% of the logits'
+    max and mean magnitude (per-tensor activation quantization over 6
+    layers; the reference holds its quantized XOR model to 0.1 absolute)."""
+    from kansai_amd.charlm import CharLM, CharLMWeights
+    w = CharLMWeights(seed=0)
+    ids = np.random.Generator(np.random.PCG64(9)).integers(0, 65, (64, 256)).astype(np.int32)
+    model = CharLM(w)
+    y = model(ids)
+    assert y.shape == (64 * 256, 65) and np.isfinite(y).all()
+    fp = R.forward(w, ids, quantized=False)
+    assert np.abs(y - fp).max() < 0.1 * np.abs(fp).max()
+    assert np.abs(y - fp).mean() < 0.1 * np.abs(fp).mean()
+    np.testing.assert_array_equal(model(ids).view(np.uint32), y.view(np.uint32))
