@@ -181,6 +181,24 @@ def bench_skinny(steps):
     return rows
 
 
+def bench_c4(steps, warmup):
+    """Config C4: the int8 char-LM forward (vocab 65, d 384, 6 heads, 6 layers,
+    FFN 1536, seq 256, batch 64; int8 per-channel weights ~N(0, 0.02),
+    per-tensor dynamic activation scales, fp32 softmax / LayerNorm / GELU).
+    Token ids and weights resident on the device; logits stay on the device."""
+    from kansai_amd.charlm import CharLM, CharLMWeights, attention_flops, int8_linear_ops
+    from kansai_amd.device import DeviceTensor as D
+    w = CharLMWeights(seed=0)
+    model = CharLM(w)
+    ids = D.from_host(np.random.Generator(np.random.PCG64(9)).integers(0, 65, (64, 256)).astype(np.int32))
+    ms = time_kernel(lambda: model.forward(ids, to_host=False), steps, warmup)
+    ops = int8_linear_ops(w, 64, 256)
+    return {"workload": "C4 int8 char-LM forward, batch 64 x seq 256 (16384 tokens), 6 layers, d 384",
+            "ms_per_forward": round(ms, 4), "tokens_per_s": round(64 * 256 / (ms * 1e-3), 1),
+            "int8_linear_ops": ops, "int8_linear_TOPS_over_forward": round(ops / (ms * 1e-3) / 1e12, 2),
+            "attention_fp32_flops_full_square": attention_flops(w, 64, 256)}
+
+
 COPY_BYTES = 1 << 30
 
 
@@ -307,7 +325,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", default="gemm,quant,f32,skinny", help="comma list of gemm,quant,f32,skinny,copy")
+    ap.add_argument("--only", default="gemm,quant,f32,skinny,c4", help="comma list of gemm,quant,f32,skinny,c4,copy")
     ap.add_argument("--summarize", metavar="DIR", help="summarize rocprofv3 CSV output and exit")
     args = ap.parse_args()
     if args.summarize:
@@ -350,6 +368,12 @@ def main():
     if "skinny" in only:
         log("skinny decode GEMMs C5 ...")
         skinny = bench_skinny(max(20, args.steps))
+    c4 = None
+    if "c4" in only:
+        log("C4 int8 char-LM forward ...")
+        c4 = bench_c4(max(5, args.steps // 4), 2)
+        log(f"C4 forward: {c4['ms_per_forward']:.3f} ms ({c4['tokens_per_s']:.0f} tokens/s)")
+        Nn.call("kh_pool_trim")
     if "copy" in only:
         c_ms, c_gbs = bench_copy(args.steps, args.warmup)
         log(f"1 GiB d2d copy: {c_ms:.4f} ms, {c_gbs:.0f} GB/s")
@@ -395,6 +419,7 @@ def main():
                                      "traffic": None}},
         "skinny_decode": {"workload": "C5 kh_linear_i8: per-token quantize + int8 GEMM, per-channel weights",
                           "bytes": "N*K + 8N + 4MK + 2MK + 4MN", "rows": skinny},
+        "c4_forward": c4,
         "cpu_baseline": cpu,
         "device": info,
     }

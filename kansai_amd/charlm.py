@@ -104,13 +104,13 @@ class CharLM:
             self._graphs[key] = (g, kir.plan_memory(g))
         return self._graphs[key]
 
-    def forward(self, ids, to_host: bool = True):
+    def forward(self, ids, to_host: bool = True, observe=None):
         ids = np.asarray(ids, np.int32) if not isinstance(ids, DeviceTensor) else ids
         batch, seq = ids.shape
         if seq > self.w.seq:
             raise ValueError(f"sequence length {seq} exceeds the position table ({self.w.seq})")
         g, plan = self.graph(batch, seq)
-        return kir.run_hip_planned(g, plan, None, ids, to_host=to_host)
+        return kir.run_hip_planned(g, plan, None, ids, to_host=to_host, observe=observe)
 
     __call__ = forward
 

@@ -106,98 +106,105 @@ __global__ __launch_bounds__(256) void gelu_kernel(const float* __restrict__ x, 
 // qkv: [B*T, 3*D] row-major, the fused Q|K|V projection output (head h of Q
 // at columns h*dk .. h*dk+dk-1, K at D + h*dk, V at 2D + h*dk).  out: [B*T, D],
 // head h written to its own columns (heads are merged in place).
-// A workgroup of 256 threads owns 64 queries of one (batch, head): 4 threads
-// per query, each covering every 4th key of a 64-key tile held in LDS.
-// dk = 64 (static).
+// One thread per query: the query row and its output accumulator live in
+// registers; K and V rows are staged in LDS 64 keys at a time and every lane
+// of a wave reads the same K/V row (an LDS broadcast), so each 16-byte LDS
+// read feeds four FMAs per lane.  The softmax is rescaled once per chunk of
+// 16 keys.  A workgroup owns kQ queries of one (batch, head).  dk = 64.
 // ---------------------------------------------------------------------------
 constexpr int kDk = 64;
-constexpr int kQ = 64;   // queries per workgroup
+constexpr int kQ = 128;  // queries (threads) per workgroup
 constexpr int kKT = 64;  // keys per LDS tile
+constexpr int kChunk = 16;
 
-__global__ __launch_bounds__(256) void attention_kernel(const float* __restrict__ qkv, int B, int T, int H,
-                                                        float scale, float* __restrict__ out) {
-    __shared__ float ks[kKT][kDk + 1];
-    __shared__ float vs[kKT][kDk + 1];
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(kQ) void attention_kernel(const float* __restrict__ qkv, int B, int T, int H,
+                                                       float scale, float* __restrict__ out) {
+    __shared__ __attribute__((aligned(16))) float ks[kKT][kDk];
+    __shared__ __attribute__((aligned(16))) float vs[kKT][kDk];
     const int D = H * kDk;
-    const int qb = blockIdx.x;   // query block
-    const int h = blockIdx.y;
-    const int b = blockIdx.z;
+    const int qb = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x;
-    const int ql = tid >> 2;     // query within block
-    const int part = tid & 3;    // which quarter of each key tile
-    const int q = qb * kQ + ql;  // query position
+    const int q = qb * kQ + tid;
     const bool qvalid = q < T;
     const int64_t row0 = (int64_t)b * T;
 
-    float qv[kDk];
+    float qv[kDk], o[kDk];
     {
-        const float* qr = qkv + (row0 + (qvalid ? q : 0)) * 3 * D + h * kDk;
+        const f32x4v* qr = reinterpret_cast<const f32x4v*>(qkv + (row0 + (qvalid ? q : 0)) * 3 * D + h * kDk);
 #pragma unroll
-        for (int d = 0; d < kDk; ++d) qv[d] = qvalid ? qr[d] * scale : 0.0f;
+        for (int d4 = 0; d4 < kDk / 4; ++d4) {
+            const f32x4v v = qr[d4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) qv[4 * d4 + e] = qvalid ? v[e] * scale : 0.0f;
+        }
     }
-    float o[kDk];
 #pragma unroll
     for (int d = 0; d < kDk; ++d) o[d] = 0.0f;
     float m = -3.0e38f, l = 0.0f;
 
-    const int q_last = min(T, (qb + 1) * kQ) - 1;  // last query of the block
+    const int q_last = min(T, (qb + 1) * kQ) - 1;
     for (int k0 = 0; k0 <= q_last; k0 += kKT) {
         __syncthreads();
-        // Load K and V tiles: 64 keys x 64 dims each, 256 threads.
-        for (int e = tid; e < kKT * kDk; e += 256) {
-            const int kk = e / kDk, d = e % kDk;
+        for (int e = tid; e < kKT * kDk / 4; e += kQ) {
+            const int kk = e / (kDk / 4), d4 = e % (kDk / 4);
             const int key = k0 + kk;
             const bool ok = key < T;
             const float* kr = qkv + (row0 + (ok ? key : 0)) * 3 * D;
-            ks[kk][d] = ok ? kr[D + h * kDk + d] : 0.0f;
-            vs[kk][d] = ok ? kr[2 * D + h * kDk + d] : 0.0f;
+            const f32x4v zero = {0.f, 0.f, 0.f, 0.f};
+            reinterpret_cast<f32x4v*>(ks[kk])[d4] = ok ? reinterpret_cast<const f32x4v*>(kr + D + h * kDk)[d4] : zero;
+            reinterpret_cast<f32x4v*>(vs[kk])[d4] = ok ? reinterpret_cast<const f32x4v*>(kr + 2 * D + h * kDk)[d4] : zero;
         }
         __syncthreads();
-        if (!qvalid) continue;
-        // Scores for this thread's 16 keys (keys k0 + part + 4*j).
-        float s[kKT / 4];
-        float tmax = -3.0e38f;
+        if (!qvalid || q < k0) continue;
+        const int n_keys = min(kKT, q - k0 + 1);  // keys <= q in this tile
+        for (int c0 = 0; c0 < n_keys; c0 += kChunk) {
+            float s[kChunk];
+            float cmax = -3.0e38f;
 #pragma unroll
-        for (int j = 0; j < kKT / 4; ++j) {
-            const int kk = part + 4 * j;
-            const int key = k0 + kk;
-            float acc = 0.0f;
+            for (int j = 0; j < kChunk; ++j) {
+                const f32x4v* kr = reinterpret_cast<const f32x4v*>(ks[c0 + j]);
+                float acc = 0.0f;
 #pragma unroll
-            for (int d = 0; d < kDk; ++d) acc += qv[d] * ks[kk][d];
-            s[j] = (key <= q) ? acc : -3.0e38f;
-            tmax = fmaxf(tmax, s[j]);
+                for (int d4 = 0; d4 < kDk / 4; ++d4) {
+                    const f32x4v kv = kr[d4];
+                    acc += qv[4 * d4] * kv[0];
+                    acc += qv[4 * d4 + 1] * kv[1];
+                    acc += qv[4 * d4 + 2] * kv[2];
+                    acc += qv[4 * d4 + 3] * kv[3];
+                }
+                s[j] = (c0 + j < n_keys) ? acc : -3.0e38f;
+                cmax = fmaxf(cmax, s[j]);
+            }
+            const float m_new = fmaxf(m, cmax);
+            const float corr = __expf(m - m_new);
+            l *= corr;
+#pragma unroll
+            for (int d = 0; d < kDk; ++d) o[d] *= corr;
+#pragma unroll
+            for (int j = 0; j < kChunk; ++j) {
+                const float p = (c0 + j < n_keys) ? __expf(s[j] - m_new) : 0.0f;
+                l += p;
+                const f32x4v* vr = reinterpret_cast<const f32x4v*>(vs[c0 + j]);
+#pragma unroll
+                for (int d4 = 0; d4 < kDk / 4; ++d4) {
+                    const f32x4v vv = vr[d4];
+                    o[4 * d4] += p * vv[0];
+                    o[4 * d4 + 1] += p * vv[1];
+                    o[4 * d4 + 2] += p * vv[2];
+                    o[4 * d4 + 3] += p * vv[3];
+                }
+            }
+            m = m_new;
         }
-        // Row max across the 4 threads of this query (adjacent lanes).
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 1, 64));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 2, 64));
-        const float m_new = fmaxf(m, tmax);
-        const float corr = __expf(m - m_new);
-        float psum = 0.0f;
-#pragma unroll
-        for (int d = 0; d < kDk; ++d) o[d] *= corr;
-#pragma unroll
-        for (int j = 0; j < kKT / 4; ++j) {
-            const int kk = part + 4 * j;
-            const float p = (k0 + kk <= q) ? __expf(s[j] - m_new) : 0.0f;
-            psum += p;
-#pragma unroll
-            for (int d = 0; d < kDk; ++d) o[d] += p * vs[kk][d];
-        }
-        l = l * corr + psum;
-        m = m_new;
     }
     if (!qvalid) return;
-    // Combine the 4 partial (m is shared; l and o are partial sums).
-    l += __shfl_xor(l, 1, 64);
-    l += __shfl_xor(l, 2, 64);
-    float* orow = out + (row0 + q) * D + h * kDk;
+    const float inv = 1.0f / l;
+    f32x4v* orow = reinterpret_cast<f32x4v*>(out + (row0 + q) * D + h * kDk);
 #pragma unroll
-    for (int d = 0; d < kDk; ++d) {
-        float v = o[d];
-        v += __shfl_xor(v, 1, 64);
-        v += __shfl_xor(v, 2, 64);
-        if (part == (d & 3)) orow[d] = v / l;
-    }
+    for (int d4 = 0; d4 < kDk / 4; ++d4)
+        orow[d4] = f32x4v{o[4 * d4] * inv, o[4 * d4 + 1] * inv, o[4 * d4 + 2] * inv, o[4 * d4 + 3] * inv};
 }
 
 }  // namespace
@@ -242,11 +249,12 @@ int kh_causal_attention(const float* qkv, int B, int T, int H, int dk, float* ou
     KH_REQUIRE(B <= 65535 && H <= 65535, "kh_causal_attention: too many batches or heads");
     KH_REQUIRE(qkv && out, "kh_causal_attention: null pointer");
     KH_DEVICE_OR_RETURN(d);
+    KH_REQUIRE(kh::aligned(qkv, 16) && kh::aligned(out, 16), "kh_causal_attention: 16-byte aligned buffers required");
     dim3 grid((unsigned)((T + kQ - 1) / kQ), (unsigned)H, (unsigned)B);
     // 1/sqrt(d_k) as the reference forms it: a binary64 Python float narrowed
     // to binary32 by from_flat (nn.py:413).
     const float scale = (float)(1.0 / 8.0);
-    attention_kernel<<<grid, 256, 0, d->stream>>>(qkv, B, T, H, scale, out);
+    attention_kernel<<<grid, kQ, 0, d->stream>>>(qkv, B, T, H, scale, out);
     return kh::launch_status("attention");
 }
 

@@ -474,7 +474,7 @@ def _to_host(v):
     return v
 
 
-def _run(graph, args, plan, to_host):
+def _run(graph, args, plan, to_host, observe=None):
     if not N.available():
         raise RuntimeError("run_hip: no gfx950 (MI355X) device available on this system")
     by_id = {n.id: n for n in graph.nodes}
@@ -488,8 +488,12 @@ def _run(graph, args, plan, to_host):
             continue
         if node.op == "constant":
             vals[node.id] = _constant(node)
+            if observe is not None:
+                observe(node, vals[node.id])
             continue
         vals[node.id] = _exec(node, vals)
+        if observe is not None:
+            observe(node, vals[node.id])
         if plan is not None:
             for i in node.inputs:
                 src = by_id[i]
@@ -502,21 +506,27 @@ def _run(graph, args, plan, to_host):
     return _to_host(out) if to_host else out
 
 
-def run_hip(graph, *args, to_host: bool = True):
+def run_hip(graph, *args, to_host: bool = True, observe=None):
     """Runs `graph` on the GPU.  Host inputs (numpy arrays, or anything with
     .tolist() and .shape such as the reference's Tensor) are uploaded;
     DeviceTensors are used in place.  Returns the output as a numpy array
-    (or a DeviceTensor with to_host=False)."""
-    return _run(graph, args, None, to_host)
+    (or a DeviceTensor with to_host=False).
+
+    observe(node, value), if given, is called after every constant and every
+    executed node with its device value (DeviceTensor, QTensor or the
+    accumulator holder), before any release: per-node inspection, like the
+    reference's trace printing of node results."""
+    return _run(graph, args, None, to_host, observe)
 
 
-def run_hip_planned(graph, plan: MemoryPlan, pool: DevicePool | None, *args, to_host: bool = True):
+def run_hip_planned(graph, plan: MemoryPlan, pool: DevicePool | None, *args, to_host: bool = True, observe=None):
     """run_planned's contract (kir.py:957-1068) on the device: every
     intermediate is returned to the device pool right after its last use, so
     repeated runs of the graph reuse the same device buffers and never call
     hipMalloc after the first run.  Placeholders and constants are never
-    released; the output's ownership passes to the caller."""
-    return _run(graph, args, plan, to_host)
+    released; the output's ownership passes to the caller.  `observe` is
+    run_hip's per-node hook."""
+    return _run(graph, args, plan, to_host, observe)
 
 
 def jit(fn):

@@ -78,24 +78,86 @@ def test_causal_attention(G, batch, seq, heads):
     assert np.abs(out.numpy() - ref).max() < 2e-5
 
 
+def _host(v):
+    """Host copy of a node value: arrays, or (codes, scales) for a QTensor
+    (packed codes in their [out, in] storage order)."""
+    from kansai_amd.quantize import QTensor
+    if isinstance(v, QTensor):
+        c = v.codes.numpy()
+        c = c.reshape(v.shape[::-1] if v.packed else v.shape)
+        return c, v.scales.numpy()
+    return v.numpy()
+
+
+def _check_node(node, got, ins):
+    """One graph node against the restatement fed with the GPU's own inputs:
+    bit-exact for embedding, add, quantize and the int8 Linear; the fp32
+    kernels within their own unit tests' bounds."""
+    from oracle import oracle as O
+    op = node.op
+    if op == "embedding":
+        ids, tok, pos = ins
+        seq = node.attrs["seq"]
+        ref = (tok[ids.reshape(-1)] + np.tile(pos[:seq], (ids.size // seq, 1))).astype(np.float32)
+        np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+    elif op == "add":
+        a, b = ins
+        np.testing.assert_array_equal(got.view(np.uint32), (a + b).astype(np.float32).view(np.uint32))
+    elif op == "quantize":
+        q, s = O.ko_quantize_tensor(ins[0])
+        np.testing.assert_array_equal(got[0], q.reshape(got[0].shape))
+        assert got[1][0] == s
+    elif op == "int8_linear":
+        (qa, sa), (qw, sw) = ins[0], ins[1]
+        bias = ins[2] if len(ins) > 2 else None
+        ref = O.ko_epilogue(O.ko_gemm_i8(qa, qw), sa, sw, bias)
+        np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+    elif op == "layer_norm":
+        x, w, b = ins
+        ref = R.layer_norm(x.astype(np.float64), w, b, node.attrs.get("eps", 1e-5))
+        assert np.abs(got - ref).max() < 2e-5 * max(1.0, np.abs(ref).max())
+    elif op == "gelu":
+        x = ins[0].astype(np.float64)
+        ref = x * 0.5 * (1 + erf(x / np.sqrt(2)))
+        assert np.abs(got - ref).max() < 4e-6 * max(1.0, np.abs(ref).max())
+    elif op == "causal_attention":
+        ref = R.causal_attention(ins[0].astype(np.float64), node.attrs["batch"], node.attrs["seq"],
+                                 node.attrs["heads"])
+        assert np.abs(got - ref).max() < 2e-5
+    else:
+        raise AssertionError(f"unchecked node kind {op}")
+
+
 @pytest.mark.parametrize("seq", [64, 100])
 def test_small_model_matches_restatement(G, seq):
     """Two layers of the C4 architecture (d 384, 6 heads, FFN 1536, vocab 65)
-    with nonzero biases.  The int8 steps are exact on both sides; fp32
-    rounding in LayerNorm / softmax / GELU can move an activation across a
-    quantization boundary, which changes a logit by at most a few
-    quantization steps, so the bound is 5e-3 absolute against logits of
-    magnitude ~1."""
+    with nonzero biases, checked node by node: every node's GPU output
+    against the restatement of that node applied to the GPU's own inputs.
+
+    End to end the int8 model is discontinuous: one activation tensor's
+    per-tensor scale is set by its largest element, and a one-ulp change of
+    the attention output (below any fp32 kernel's rounding bound) re-rounds
+    enough codes downstream to move logits by 2.5e-2 at seq 100.  So the
+    whole-model comparison is against the fp32 model, at the quantization
+    error's scale, and exactness is asserted per node."""
     from kansai_amd.charlm import CharLM, CharLMWeights
     w = CharLMWeights(layers=2, seq=128, seed=1, bias_std=0.02)
     ids = np.random.Generator(np.random.PCG64(2)).integers(0, 65, (2, seq)).astype(np.int32)
     model = CharLM(w)
-    y = model(ids)
-    ref = R.forward(w, ids)
+    seen = {}
+    y = model(ids, observe=lambda node, v: seen.__setitem__(node.id, (node, _host(v))))
     assert y.shape == (2 * seq, 65)
-    err = np.abs(y - ref)
-    assert err.max() < 5e-3, err.max()
-    assert err.mean() < 1e-4, err.mean()
+    g, _ = model.graph(2, seq)
+    by_id = {n.id: n for n in g.nodes}
+    checked = set()
+    for nid, (node, got) in seen.items():
+        if node.op == "constant":
+            continue
+        ins = [ids if by_id[i].op == "placeholder" else seen[i][1] for i in node.inputs]
+        _check_node(node, got, ins)
+        checked.add(node.op)
+    assert checked == {"embedding", "layer_norm", "quantize", "int8_linear", "causal_attention", "add", "gelu"}
+    np.testing.assert_array_equal(seen[g.output][1].view(np.uint32), y.view(np.uint32))
     # and the int8 model stays near the fp32 one (quantization error)
     fp = R.forward(w, ids, quantized=False)
     assert np.abs(y - fp).max() < 0.1 * np.abs(fp).max()
