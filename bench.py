@@ -55,7 +55,7 @@ def log(msg):
 def time_kernel(fn, steps, warmup):
     """Average ms per call of fn() over `steps` back-to-back calls, HIP events
     on the library stream, synchronized before and after."""
-    from kansai_amd import _native as N
+    from kansaiml_amd import _native as N
     for _ in range(warmup):
         fn()
     N.synchronize()
@@ -89,7 +89,7 @@ def bench_gemm(H, D, steps, warmup):
     b = D.from_host(gen.integers(-127, 128, (N, K), dtype=np.int8))
     sa = D.from_host(np.array([0.01]))
     sb = D.from_host(np.array([0.02]))
-    from kansai_amd import _native as Nn
+    from kansaiml_amd import _native as Nn
     out = D([M, N], "float32")
     args = (a.ptr, b.ptr, M, N, K, sa.ptr, 0, sb.ptr, 0, None, out.ptr, None)
     fn = lambda: Nn.call("kh_gemm_i8", *args)  # noqa: E731
@@ -108,7 +108,7 @@ def bench_quant_dequant(H, D, steps, warmup):
     x.reshape(-1)[idx] = np.where(gen.random(n_out) < 0.5, -50.0, 50.0).astype(np.float32)
     xd = D.from_host(x)
     del x
-    from kansai_amd import _native as Nn
+    from kansaiml_amd import _native as Nn
     q = D([rows, cols], "int8")
     s = D([rows], "float64")
     out = D([rows, cols], "float32")
@@ -127,7 +127,7 @@ def bench_f32(H, D, steps, warmup):
     a = D.from_host(gen.standard_normal((n, n), dtype=np.float32))
     b = D.from_host(gen.standard_normal((n, n), dtype=np.float32))
     out = D([n, n], "float32")
-    from kansai_amd import _native as Nn
+    from kansaiml_amd import _native as Nn
     fn = lambda: Nn.call("kh_matmul_f32", a.ptr, b.ptr, out.ptr, n, n, n, None)  # noqa: E731
     ms = time_kernel(fn, steps, warmup)
     return ms, 2.0 * n ** 3 / (ms * 1e-3) / 1e12
@@ -140,8 +140,8 @@ def bench_skinny(steps):
     more than 512 MB of distinct weights pass through HBM (beyond the 256 MB
     Infinity Cache).  Each launch pair is bracketed by its own HIP events, so
     host launch gaps are excluded."""
-    from kansai_amd import _native as Nn
-    from kansai_amd.device import DeviceTensor as D
+    from kansaiml_amd import _native as Nn
+    from kansaiml_amd.device import DeviceTensor as D
     gen = np.random.Generator(np.random.PCG64(5))
     rows = []
     for K, N in ((4096, 4096), (4096, 11008)):
@@ -186,8 +186,8 @@ def bench_c4(steps, warmup):
     FFN 1536, seq 256, batch 64; int8 per-channel weights ~N(0, 0.02),
     per-tensor dynamic activation scales, fp32 softmax / LayerNorm / GELU).
     Token ids and weights resident on the device; logits stay on the device."""
-    from kansai_amd.charlm import CharLM, CharLMWeights, attention_flops, int8_linear_ops
-    from kansai_amd.device import DeviceTensor as D
+    from kansaiml_amd.charlm import CharLM, CharLMWeights, attention_flops, int8_linear_ops
+    from kansaiml_amd.device import DeviceTensor as D
     w = CharLMWeights(seed=0)
     model = CharLM(w)
     ids = D.from_host(np.random.Generator(np.random.PCG64(9)).integers(0, 65, (64, 256)).astype(np.int32))
@@ -205,8 +205,8 @@ COPY_BYTES = 1 << 30
 def bench_copy(steps, warmup):
     """1 GiB device-to-device copy (the library's copy16_kernel): the known-size
     reference for FETCH_SIZE / WRITE_SIZE calibration."""
-    from kansai_amd import _native as Nn
-    from kansai_amd.device import DeviceTensor as D
+    from kansaiml_amd import _native as Nn
+    from kansaiml_amd.device import DeviceTensor as D
     src = D([COPY_BYTES], "int8")
     dst = D([COPY_BYTES], "int8")
     ms = time_kernel(lambda: Nn.call("kh_memcpy_d2d", dst.ptr, src.ptr, COPY_BYTES), steps, warmup)
@@ -337,9 +337,9 @@ def main():
                                    "(rows/columns would shard with zero exchange); run with --gpus 1"}))
         sys.exit(2)
 
-    from kansai_amd import _native as Nn
-    from kansai_amd import hip as H
-    from kansai_amd.device import DeviceTensor as D
+    from kansaiml_amd import _native as Nn
+    from kansaiml_amd import hip as H
+    from kansaiml_amd.device import DeviceTensor as D
     if not H.available():
         raise SystemExit("bench: no gfx950 GPU visible")
     info = Nn.device_info()

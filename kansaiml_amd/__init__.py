@@ -1,4 +1,4 @@
-"""kansai_amd -- an MI355X (gfx950) HIP backend for Kansai's int8
+"""kansaiml_amd -- an MI355X (gfx950) HIP backend for Kansai's int8
 quantize -> int8 matmul -> dequantize path and its fp32 matmul.
 
 Modules:
@@ -7,7 +7,7 @@ Modules:
   hip       tensor-level ops (shape checks + kernel calls)
   quantize  the reference's quantize.py API on the GPU
   kir       the KIR graph schema, tracer, memory planner and run_hip
-  build     compiles kansai_amd/csrc/*.hip for gfx950
+  build     compiles kansaiml_amd/csrc/*.hip for gfx950
 
 Importing the package does not touch the GPU.
 """

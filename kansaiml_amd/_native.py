@@ -98,7 +98,7 @@ def load_library(path: str = LIB_PATH):
     with _lock:
         if _lib is None:
             if not os.path.exists(path):
-                raise HipUnavailable(f"{path} is missing: build it with `python -m kansai_amd.build`")
+                raise HipUnavailable(f"{path} is missing: build it with `python -m kansaiml_amd.build`")
             lib = ctypes.CDLL(path)
             for name, args in _SIGNATURES.items():
                 fn = getattr(lib, name)

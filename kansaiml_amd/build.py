@@ -1,10 +1,10 @@
-"""Builds the gfx950 HIP backend: kansai_amd/csrc/*.hip -> kansai_amd/lib/libkansai_hip.so.
+"""Builds the gfx950 HIP backend: kansaiml_amd/csrc/*.hip -> kansaiml_amd/lib/libkansai_hip.so.
 
 hipcc cross-compiles for gfx950 without a GPU.  Objects go to _build/ (not
 committed); the shared library is written in-tree so it travels with the
 source tree to the GPU box.
 
-    python -m kansai_amd.build [-v]
+    python -m kansaiml_amd.build [-v]
 """
 
 from __future__ import annotations

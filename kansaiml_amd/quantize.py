@@ -17,7 +17,7 @@ QTensor here lives on the device (int8 codes + binary64 scales) and may be
 per-tensor, per-row (per token) or per-column (per output channel, stored
 packed [out, in] for the GEMM); QLinear(linear, mode="int8") quantizes its
 input dynamically and runs the int8 GEMM with a fused dequantize + bias
-epilogue.  Traced through kansai_amd.kir, QLinear emits quantize /
+epilogue.  Traced through kansaiml_amd.kir, QLinear emits quantize /
 int8_matmul / dequantize nodes.
 """
 

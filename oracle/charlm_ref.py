@@ -66,7 +66,7 @@ def linear(x, w, b=None, quantized=True):
 
 
 def forward(w, ids, quantized=True):
-    """w: kansai_amd.charlm.CharLMWeights (plain numpy arrays); ids [B, T]."""
+    """w: kansaiml_amd.charlm.CharLMWeights (plain numpy arrays); ids [B, T]."""
     ids = np.asarray(ids)
     batch, seq = ids.shape
     x = (w.tok[ids.reshape(-1)] + np.tile(w.pos[:seq], (batch, 1))).astype(f32)

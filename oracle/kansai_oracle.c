@@ -2,7 +2,7 @@
  * kansai_oracle.c -- CPU restatement of the reference's int8 quantize ->
  * int8 matmul -> dequantize path and of its fp32 matmul + bias.
  *
- * TEST INFRASTRUCTURE ONLY.  Nothing in the product (kansai_amd/) links,
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product (kansaiml_amd/) links,
  * loads or calls this file; only tests/, __graft_entry__.smoke() and
  * bench.py's cpu_baseline leg use it, as the checker.
  *

@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and
 bench.py's cpu_baseline leg import this module, as the checker; the
-product package (kansai_amd/) never imports it and has no CPU fallback.
+product package (kansaiml_amd/) never imports it and has no CPU fallback.
 
 Three layers, each citing the reference it follows:
 

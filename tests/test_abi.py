@@ -10,7 +10,7 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "kansai_hip.h")
-LIB = os.path.join(ROOT, "kansai_amd", "lib", "libkansai_hip.so")
+LIB = os.path.join(ROOT, "kansaiml_amd", "lib", "libkansai_hip.so")
 
 
 def declared():
@@ -35,22 +35,22 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_binding_covers_header():
-    from kansai_amd import _native
+    from kansaiml_amd import _native
     assert set(_native.exported_symbols()) == declared()
 
 
 @pytest.mark.skipif(not os.path.exists(LIB), reason="library not built")
 def test_library_loads_and_resolves_symbols():
-    from kansai_amd import _native
+    from kansaiml_amd import _native
     lib = _native.load_library()
     for name in _native.exported_symbols():
         assert getattr(lib, name) is not None
 
 
 def test_product_package_never_imports_oracle():
-    """The product path has no CPU fallback: nothing under kansai_amd/
+    """The product path has no CPU fallback: nothing under kansaiml_amd/
     imports, loads or names the oracle."""
-    pkg = os.path.join(ROOT, "kansai_amd")
+    pkg = os.path.join(ROOT, "kansaiml_amd")
     for dirpath, _, files in os.walk(pkg):
         for f in files:
             if f.endswith((".py", ".hip", ".h", ".cpp")):

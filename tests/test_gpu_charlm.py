@@ -13,8 +13,8 @@ pytestmark = pytest.mark.gpu
 
 @pytest.fixture(scope="module")
 def G():
-    from kansai_amd import _native as N
-    from kansai_amd.device import DeviceTensor as D
+    from kansaiml_amd import _native as N
+    from kansaiml_amd.device import DeviceTensor as D
     assert N.available(), "no gfx950 device"
     return N, D
 
@@ -81,7 +81,7 @@ def test_causal_attention(G, batch, seq, heads):
 def _host(v):
     """Host copy of a node value: arrays, or (codes, scales) for a QTensor
     (packed codes in their [out, in] storage order)."""
-    from kansai_amd.quantize import QTensor
+    from kansaiml_amd.quantize import QTensor
     if isinstance(v, QTensor):
         c = v.codes.numpy()
         c = c.reshape(v.shape[::-1] if v.packed else v.shape)
@@ -140,7 +140,7 @@ def test_small_model_matches_restatement(G, seq):
     enough codes downstream to move logits by 2.5e-2 at seq 100.  So the
     whole-model comparison is against the fp32 model, at the quantization
     error's scale, and exactness is asserted per node."""
-    from kansai_amd.charlm import CharLM, CharLMWeights
+    from kansaiml_amd.charlm import CharLM, CharLMWeights
     w = CharLMWeights(layers=2, seq=128, seed=1, bias_std=0.02)
     ids = np.random.Generator(np.random.PCG64(2)).integers(0, 65, (2, seq)).astype(np.int32)
     model = CharLM(w)
@@ -174,7 +174,7 @@ def test_full_c4_forward_runs(G):
     against the fp32 model: max and mean deviation within 10% of the logits'
     max and mean magnitude (per-tensor activation quantization over 6
     layers; the reference holds its quantized XOR model to 0.1 absolute)."""
-    from kansai_amd.charlm import CharLM, CharLMWeights
+    from kansaiml_amd.charlm import CharLM, CharLMWeights
     w = CharLMWeights(seed=0)
     ids = np.random.Generator(np.random.PCG64(9)).integers(0, 65, (64, 256)).astype(np.int32)
     model = CharLM(w)

@@ -13,8 +13,8 @@ pytestmark = pytest.mark.gpu
 
 @pytest.fixture(scope="module")
 def hip():
-    from kansai_amd import hip as H
-    from kansai_amd.device import DeviceTensor
+    from kansaiml_amd import hip as H
+    from kansaiml_amd.device import DeviceTensor
     assert H.available(), "no gfx950 device"
     return H, DeviceTensor
 

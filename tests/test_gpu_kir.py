@@ -18,8 +18,8 @@ pytestmark = pytest.mark.gpu
 
 @pytest.fixture(scope="module")
 def K():
-    from kansai_amd import kir, quantize
-    from kansai_amd import _native as N
+    from kansaiml_amd import kir, quantize
+    from kansaiml_amd import _native as N
     assert N.available(), "no gfx950 device"
     return kir, quantize, N
 

@@ -17,8 +17,8 @@ PER_TENSOR = ["ref_test_quantize_1000", "zero_maps_to_zero", "ties_scale_one", "
 
 @pytest.fixture(scope="module")
 def hip():
-    from kansai_amd import hip as H
-    from kansai_amd.device import DeviceTensor
+    from kansaiml_amd import hip as H
+    from kansaiml_amd.device import DeviceTensor
     assert H.available(), "no gfx950 device"
     return H, DeviceTensor
 
@@ -159,7 +159,7 @@ def test_tiny_and_subnormal_rows(hip):
 @pytest.mark.parametrize("bad", [np.nan, np.inf, -np.inf])
 def test_nonfinite_raises_value_error(hip, bad):
     H, D = hip
-    from kansai_amd import _native as N
+    from kansaiml_amd import _native as N
     x = np.ones((3, 8), np.float32)
     x[1, 5] = bad
     xd = D.from_host(x)

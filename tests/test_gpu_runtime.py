@@ -11,8 +11,8 @@ pytestmark = pytest.mark.gpu
 
 @pytest.fixture(scope="module")
 def rt():
-    from kansai_amd import _native as N
-    from kansai_amd.device import DeviceTensor
+    from kansaiml_amd import _native as N
+    from kansaiml_amd.device import DeviceTensor
     assert N.available(), "no gfx950 device"
     return N, DeviceTensor
 

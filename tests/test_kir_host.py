@@ -4,7 +4,7 @@ pass and the memory planner (python/kansai/kir.py:884-954's algorithm)."""
 import numpy as np
 import pytest
 
-from kansai_amd import kir
+from kansaiml_amd import kir
 
 
 def _linear_int8(x, w_q, bias, gran="tensor"):
