@@ -212,22 +212,34 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_i8_kernel(const int8_t* __r
 }
 
 // ---------------------------------------------------------------------------
-// Full-tile kernel (M % BM == 0, N % BN == 0, K % BK == 0, 16-byte aligned
-// operands): no bounds tests in the main loop.
+// Full-tile kernel (M % 256 == 0, N % 256 == 0, K % 64 == 0, 16-byte aligned
+// operands), scheduled for the MI355X power envelope: with random int8
+// operands the shader clock settles near 1.3-1.6 GHz under MFMA load, so the
+// kernel's job is to keep the MFMA pipe issuing at that clock.
 //
-// * Global loads are raw buffer loads: one VGPR offset per chunk, the k
-//   advance in an SGPR.
-// * LDS rows are BK = 128 bytes (8 chunks of 16 B) with no padding; chunk c
-//   of row r is stored at chunk slot c ^ swz(r), an XOR swizzle under which
-//   the MFMA fragment reads (32 consecutive rows, one chunk) and the
-//   row-contiguous fragment writes are both free of bank conflicts.
-// * MFMA fragments are double-buffered in registers across the four 32-k
-//   substeps of a BK step, so LDS latency hides behind the previous
-//   substep's MFMAs.
-// * Workgroups are launched on a 1-D grid; hardware deals consecutive
-//   workgroup ids round-robin to the 8 XCDs, so the id is remapped to give
-//   each XCD a contiguous band of tiles, walked in groups of kGroupM tile rows
-//   so that concurrently resident tiles share A and B panels in that XCD's L2.
+// * 256x256 workgroup tile, 8 waves as 2 (M) x 4 (N); each wave owns 128x64
+//   outputs as 4x2 blocks of v_mfma_i32_32x32x32_i8 (128 int32 accumulators).
+// * K is staged 64 bytes at a time in a ring of NS LDS stages (32 KB each).
+//   Operands move global -> LDS by LDS-DMA (buffer_load_dwordx4 ... lds):
+//   no VGPR staging and no ds_write.  Lane l of one instruction lands at
+//   M0 + 16*l, so the XOR swizzle is applied on the global side: LDS slot
+//   (row r, chunk c') holds global chunk c' ^ swz(r), swz(r) = (r >> 2) & 3,
+//   under which the MFMA fragment reads (16 consecutive rows, one chunk per
+//   lane) hit 64 distinct banks.
+// * Ping-pong: waves 0-3 (group 0, one per SIMD) and waves 4-7 (group 1) run
+//   the same sequence -- memory phase (fragment reads for K-step k, LDS-DMA
+//   for step k + NS - 1), barrier, compute phase (16 MFMAs), barrier -- with
+//   group 1 one barrier behind, so on every SIMD one wave's MFMAs cover the
+//   other wave's memory phase.  Every wave executes 2 * nk + 2 barriers.
+// * Before the barrier that ends its memory phase for step k a wave waits
+//   for its own LDS-DMA of stage k + 1 (vmcnt counts the later stages still
+//   allowed in flight) and for its fragment reads (lgkmcnt 0), so the
+//   barrier publishes stage k + 1 and retires every read of stage k - 1,
+//   whose slot the next memory phase refills.
+// * Workgroups are launched on a 1-D grid; hardware deals consecutive ids
+//   round-robin to the 8 XCDs, so the id is remapped to give each XCD a
+//   contiguous band of tiles, walked in groups of `group_m` tile rows so that
+//   concurrently resident tiles share A and B panels in that XCD's L2.
 // ---------------------------------------------------------------------------
 constexpr int kXcds = 8;
 constexpr int kBufferFlags = 0x00020000;  // dword 3 of a raw gfx9 buffer resource
@@ -235,8 +247,6 @@ constexpr int kBufferFlags = 0x00020000;  // dword 3 of a raw gfx9 buffer resour
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kBufferFlags);
 }
-
-__device__ __forceinline__ int lds_swz(int r) { return ((r >> 1) ^ (r << 2)) & 7; }
 
 // Workgroup id -> (tile row, tile col).
 __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int group_m, int& tm, int& tn) {
@@ -252,96 +262,100 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int g
     tn = in_g / gm;
 }
 
-// Swizzle for BK-byte LDS rows (BK / 16 chunks): conflict-free for 8- and
-// 16-lane groups reading one chunk of consecutive rows.
-template <int BK>
-__device__ __forceinline__ int tile_swz(int r) {
-    if (BK == 128) return ((r >> 1) ^ (r << 2)) & 7;
-    return ((r >> 1) ^ (r >> 3)) & 3;
+// s_waitcnt immediate (gfx9 encoding): wait until at most `vm` vector-memory
+// and `lgkm` LDS operations of this wave are outstanding; exports not waited.
+__host__ __device__ constexpr int wait_imm(int vm, int lgkm) {
+    return (vm & 15) | (7 << 4) | ((lgkm & 15) << 8) | (((vm >> 4) & 3) << 14);
 }
 
-// Scheduling hint: interleave `n` (1 MFMA, 1 LDS read) pairs.
-#define KH_SCHED_MFMA_DS(n)                                   \
-    do {                                                      \
-        _Pragma("unroll") for (int _i = 0; _i < (n); ++_i) {  \
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); \
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); \
-        }                                                     \
-    } while (0)
+// Waits until this wave has at most `stages` x `per_stage` LDS-DMA loads in
+// flight (stages in 0..3; uniform branch on a wave-uniform value).
+template <int per_stage>
+__device__ __forceinline__ void wait_loads_beyond(int stages) {
+    if (stages >= 3) __builtin_amdgcn_s_waitcnt(wait_imm(3 * per_stage, 15));
+    else if (stages == 2) __builtin_amdgcn_s_waitcnt(wait_imm(2 * per_stage, 15));
+    else if (stages == 1) __builtin_amdgcn_s_waitcnt(wait_imm(per_stage, 15));
+    else __builtin_amdgcn_s_waitcnt(wait_imm(0, 15));
+}
 
-// HINT: interleave LDS reads between MFMAs with scheduling barriers.
-// PRIO: raise the wave's issue priority while it issues an MFMA cluster, so
-// the SIMD's other wave does its memory work in the gaps.
-template <int BM, int BN, int BK, int WM, int WN, int STAGES, int HINT, int PRIO>
-__global__ __launch_bounds__(WM * WN * 64) void gemm_i8_tiled_kernel(const int8_t* __restrict__ A,
-                                                                     const int8_t* __restrict__ B, int M, int N,
-                                                                     int K, int group_m, Epilogue ep) {
-    constexpr int kCh = BK / 16;  // 16-byte chunks per LDS row
-    constexpr int kSub = BK / 32;  // MFMA k-substeps per stage
-    constexpr int kThreads = WM * WN * 64;
+// LDS-DMA of 16 bytes per lane: lane l's bytes land at dst + 16 * l (dst is
+// wave-uniform; it goes to M0).
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, void* dst, int voff, int soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, soff, 0, 0);
+}
+
+template <int NS>
+__global__ __launch_bounds__(512) void gemm_i8_pingpong_kernel(const int8_t* __restrict__ A,
+                                                               const int8_t* __restrict__ B, int M, int N, int K,
+                                                               int group_m, Epilogue ep) {
+    constexpr int BM = 256, BN = 256, BK = 64, WM = 2, WN = 4, kWaves = WM * WN;
     constexpr int kWaveM = BM / WM, kWaveN = BN / WN;
     constexpr int kTM = kWaveM / 32, kTN = kWaveN / 32;
-    constexpr int kAChunks = BM * kCh / kThreads;
-    constexpr int kBChunks = BN * kCh / kThreads;
-    constexpr int kLdsA = BM * BK, kLdsB = BN * BK, kStage = kLdsA + kLdsB;
-    static_assert(kAChunks >= 1 && kBChunks >= 1, "tile too small for the block");
-    static_assert(STAGES >= 2, "at least two LDS stages");
-    __shared__ __attribute__((aligned(16))) int8_t lds[STAGES * kStage];
+    constexpr int kLdsA = BM * BK, kStage = (BM + BN) * BK;
+    constexpr int kAInst = BM / 16 / kWaves, kBInst = BN / 16 / kWaves;  // 1 KB = 16 rows per instruction
+    constexpr int kLoads = kAInst + kBInst;  // LDS-DMA instructions per wave per stage
+    constexpr int D = NS - 1;                // prefetch distance in stages
+    static_assert(NS >= 3 && NS <= 5, "wait_loads_beyond covers up to 3 stages ahead");
+    __shared__ __attribute__((aligned(1024))) int8_t lds[NS * kStage];
 
     int tm, tn;
     tile_of(blockIdx.x, M / BM, N / BN, group_m, tm, tn);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;
+    const int group = wm;  // waves 0-3 and 4-7: one of each per SIMD
 
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(A + (int64_t)tm * BM * K, (uint32_t)BM * (uint32_t)K);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(B + (int64_t)tn * BN * K, (uint32_t)BN * (uint32_t)K);
+    auto swz = [](int r) { return (r >> 2) & 3; };
 
-    int a_goff[kAChunks], a_loff[kAChunks], b_goff[kBChunks], b_loff[kBChunks];
+    // LDS-DMA sources: instruction i of this wave fills rows
+    // (wave * kXInst + i) * 16 + l / 4, slot chunk l % 4.
+    const int lr = lane >> 2, lc = lane & 3;
+    int a_voff[kAInst], b_voff[kBInst];
 #pragma unroll
-    for (int c = 0; c < kAChunks; ++c) {
-        const int idx = tid + c * kThreads, r = idx / kCh, kc = idx % kCh;
-        a_goff[c] = r * K + kc * 16;
-        a_loff[c] = r * BK + ((kc ^ tile_swz<BK>(r)) << 4);
+    for (int i = 0; i < kAInst; ++i) {
+        const int r = (wave * kAInst + i) * 16 + lr;
+        a_voff[i] = r * K + ((lc ^ swz(r)) << 4);
     }
 #pragma unroll
-    for (int c = 0; c < kBChunks; ++c) {
-        const int idx = tid + c * kThreads, r = idx / kCh, kc = idx % kCh;
-        b_goff[c] = r * K + kc * 16;
-        b_loff[c] = kLdsA + r * BK + ((kc ^ tile_swz<BK>(r)) << 4);
+    for (int i = 0; i < kBInst; ++i) {
+        const int r = (wave * kBInst + i) * 16 + lr;
+        b_voff[i] = r * K + ((lc ^ swz(r)) << 4);
     }
-    i32x4 sa_[kAChunks], sb_[kBChunks];
-    auto gload = [&](int k0) {
+    auto issue_stage = [&](int kt) {
+        int8_t* base = lds + (kt % NS) * kStage;
+        const int k0 = kt * BK;
 #pragma unroll
-        for (int c = 0; c < kAChunks; ++c) sa_[c] = __builtin_amdgcn_raw_buffer_load_b128(ra, a_goff[c], k0, 0);
+        for (int i = 0; i < kAInst; ++i) lds_dma16(ra, base + (wave * kAInst + i) * 1024, a_voff[i], k0);
 #pragma unroll
-        for (int c = 0; c < kBChunks; ++c) sb_[c] = __builtin_amdgcn_raw_buffer_load_b128(rb, b_goff[c], k0, 0);
-    };
-    auto lstore = [&](int stage) {
-        int8_t* base = lds + stage * kStage;
-#pragma unroll
-        for (int c = 0; c < kAChunks; ++c) *reinterpret_cast<i32x4*>(base + a_loff[c]) = sa_[c];
-#pragma unroll
-        for (int c = 0; c < kBChunks; ++c) *reinterpret_cast<i32x4*>(base + b_loff[c]) = sb_[c];
+        for (int i = 0; i < kBInst; ++i) lds_dma16(rb, base + kLdsA + (wave * kBInst + i) * 1024, b_voff[i], k0);
     };
 
+    // Fragment of 32x32 block row/col r for 32-k substep s: lane l reads
+    // 16 bytes of row r + l % 32 at chunk 2s + l / 32, i.e. LDS byte
+    // r * 64 + (((l / 32) ^ swz) << 4), with bit 5 flipped for s = 1.
     const int fr = lane & 31, fh = lane >> 5;
-    // LDS byte offsets (within a stage) of this lane's fragment rows.
-    int a_row[kTM], b_row[kTN];
+    int a_off[kTM], b_off[kTN];
 #pragma unroll
-    for (int a = 0; a < kTM; ++a) a_row[a] = wm * kWaveM + a * 32 + fr;
+    for (int a = 0; a < kTM; ++a) {
+        const int r = wm * kWaveM + a * 32 + fr;
+        a_off[a] = r * BK + ((fh ^ swz(r)) << 4);
+    }
 #pragma unroll
-    for (int b = 0; b < kTN; ++b) b_row[b] = wn * kWaveN + b * 32 + fr;
-    auto read_frags = [&](int stage, int sub, i32x4* fa, i32x4* fb) {
-        const int8_t* base = lds + stage * kStage;
+    for (int b = 0; b < kTN; ++b) {
+        const int r = wn * kWaveN + b * 32 + fr;
+        b_off[b] = kLdsA + r * BK + ((fh ^ swz(r)) << 4);
+    }
+    i32x4 fa[2][kTM], fb[2][kTN];
+    auto read_stage = [&](int kt) {
+        const int8_t* base = lds + (kt % NS) * kStage;
 #pragma unroll
-        for (int a = 0; a < kTM; ++a) {
-            const int r = a_row[a];
-            fa[a] = *reinterpret_cast<const i32x4*>(base + r * BK + (((2 * sub + fh) ^ tile_swz<BK>(r)) << 4));
-        }
+        for (int s = 0; s < 2; ++s) {
 #pragma unroll
-        for (int b = 0; b < kTN; ++b) {
-            const int r = b_row[b];
-            fb[b] = *reinterpret_cast<const i32x4*>(base + kLdsA + r * BK + (((2 * sub + fh) ^ tile_swz<BK>(r)) << 4));
+            for (int a = 0; a < kTM; ++a) fa[s][a] = *reinterpret_cast<const i32x4*>(base + (a_off[a] ^ (s << 5)));
+#pragma unroll
+            for (int b = 0; b < kTN; ++b) fb[s][b] = *reinterpret_cast<const i32x4*>(base + (b_off[b] ^ (s << 5)));
         }
     };
 
@@ -352,59 +366,36 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_i8_tiled_kernel(const int8_
         for (int b = 0; b < kTN; ++b) acc[a][b] = i32x16{0};
 
     const int nk = K / BK;
-    // Prologue: stages 0 .. STAGES-2 into LDS, k-step STAGES-1 into registers.
 #pragma unroll
-    for (int s = 0; s < STAGES - 1; ++s) {
-        if (s < nk) {
-            gload(s * BK);
-            lstore(s);
-        }
-    }
-    if (STAGES - 1 < nk) gload((STAGES - 1) * BK);
-    __syncthreads();
-
-    i32x4 fa[2][kTM], fb[2][kTN];
-    read_frags(0, 0, fa[0], fb[0]);
-    for (int kt = 0; kt < nk; ++kt) {
-        const int stage = kt % STAGES;
-        const int next_stage = (kt + 1) % STAGES;
+    for (int s = 0; s < D; ++s)
+        if (s < nk) issue_stage(s);
+    wait_loads_beyond<kLoads>(min(D - 1, nk - 1));  // stage 0 landed
+    __builtin_amdgcn_s_barrier();
+    if (group == 1) __builtin_amdgcn_s_barrier();  // stagger: group 1 runs one phase behind
+    __builtin_amdgcn_sched_barrier(0);
+    for (int k = 0; k < nk; ++k) {
+        // memory phase
+        read_stage(k);
+        if (k + D < nk) issue_stage(k + D);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(wait_imm(63, 0));          // fragments in registers
+        wait_loads_beyond<kLoads>(min(D - 1, nk - 2 - k));  // stage k + 1 landed
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        // compute phase
 #pragma unroll
-        for (int sub = 0; sub < kSub; ++sub) {
-            const int cur = sub & 1;
-            // Prefetch the next substep's fragments -- from the next stage
-            // after the last substep (visible since the previous barrier).
-            if (sub + 1 < kSub)
-                read_frags(stage, sub + 1, fa[cur ^ 1], fb[cur ^ 1]);
-            else if (kt + 1 < nk && STAGES > 2)
-                read_frags(next_stage, 0, fa[cur ^ 1], fb[cur ^ 1]);
-            if (PRIO) __builtin_amdgcn_s_setprio(1);
+        for (int s = 0; s < 2; ++s)
 #pragma unroll
             for (int a = 0; a < kTM; ++a)
 #pragma unroll
                 for (int b = 0; b < kTN; ++b)
-                    acc[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[cur][a], fb[cur][b], acc[a][b], 0, 0, 0);
-            if (HINT) KH_SCHED_MFMA_DS(kTM + kTN);
-            if (PRIO) __builtin_amdgcn_s_setprio(0);
-        }
-        // Registers hold k-step kt + STAGES - 1: store it into the stage that
-        // was read during k-step kt - 1 (every wave passed the last barrier).
-        if (kt + STAGES - 1 < nk) {
-            lstore((kt + STAGES - 1) % STAGES);
-            if (kt + STAGES < nk) gload((kt + STAGES) * BK);
-        }
-        __syncthreads();
-        if (STAGES == 2 && kt + 1 < nk) read_frags(next_stage, 0, fa[kSub & 1], fb[kSub & 1]);
+                    acc[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[s][a], fb[s][b], acc[a][b], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
     }
+    if (group == 0) __builtin_amdgcn_s_barrier();  // both groups end on 2 * nk + 2 barriers
 
-    // With 128x128 wave tiles the accumulators fill all 256 AGPRs; keep them
-    // there until each block is stored (otherwise every block is copied to
-    // VGPRs at once on loop exit).
-    if (kTM * kTN * 16 > 128) {
-#pragma unroll
-        for (int a = 0; a < kTM; ++a)
-#pragma unroll
-            for (int b = 0; b < kTN; ++b) asm volatile("" : "+a"(acc[a][b]));
-    }
     const int64_t row_base = (int64_t)tm * BM + wm * kWaveM + 4 * fh;
     const int64_t col_base = (int64_t)tn * BN + wn * kWaveN + fr;
 #pragma unroll
@@ -506,21 +497,17 @@ int launch_skinny(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, in
     return kh::launch_status("gemm_i8_skinny");
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int STAGES, int HINT, int PRIO>
-int launch_tiled(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
-                 const Epilogue& ep, int group_m) {
-    const unsigned tiles = (unsigned)((M / BM) * (N / BN));
-    gemm_i8_tiled_kernel<BM, BN, BK, WM, WN, STAGES, HINT, PRIO>
-        <<<tiles, WM * WN * 64, 0, d->stream>>>(A, B, (int)M, (int)N, (int)K, group_m, ep);
-    return kh::launch_status("gemm_i8_tiled");
+int launch_pingpong(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
+                    const Epilogue& ep) {
+    const unsigned tiles = (unsigned)((M / 256) * (N / 256));
+    gemm_i8_pingpong_kernel<4><<<tiles, 512, 0, d->stream>>>(A, B, (int)M, (int)N, (int)K, 8, ep);
+    return kh::launch_status("gemm_i8_pingpong");
 }
 
 // True when the full-tile kernel applies to this shape.
-template <int BM, int BN, int BK>
-bool tiled_fits(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K) {
-    return M % BM == 0 && N % BN == 0 && K % BK == 0 && K > 0 && kh::aligned(A, 16) && kh::aligned(B, 16) &&
-           (int64_t)BM * K <= 0xFFFFFFFFLL && (int64_t)BN * K <= 0xFFFFFFFFLL && M <= 0x7FFFFFFF && N <= 0x7FFFFFFF &&
-           (M / BM) * (N / BN) <= 0x7FFFFFFF;
+bool pingpong_fits(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K) {
+    return M % 256 == 0 && N % 256 == 0 && K % 64 == 0 && K > 0 && kh::aligned(A, 16) && kh::aligned(B, 16) &&
+           256 * K <= 0x7FFFFFFFLL && M <= 0x7FFFFFFF && N <= 0x7FFFFFFF && (M / 256) * (N / 256) <= 0x7FFFFFFF;
 }
 
 template <int BM, int BN, int BK, int WM, int WN>
@@ -550,8 +537,7 @@ int kh_gemm_i8(const int8_t* a, const int8_t* b_packed, int64_t M, int64_t N, in
     KH_DEVICE_OR_RETURN(d);
     Epilogue ep{sa, sb, bias, out, acc_out, sa_per_row, sb_per_col};
     if (skinny_fits(a, b_packed, M, N, K)) return launch_skinny(d, a, b_packed, M, N, K, ep);
-    if (tiled_fits<256, 256, 128>(a, b_packed, M, N, K))
-        return launch_tiled<256, 256, 128, 2, 4, 2, 1, 0>(d, a, b_packed, M, N, K, ep, 8);
+    if (pingpong_fits(a, b_packed, M, N, K)) return launch_pingpong(d, a, b_packed, M, N, K, ep);
     const bool vec16 = (K % 16 == 0) && kh::aligned(a, 16) && kh::aligned(b_packed, 16);
     if (M >= 2048 && N >= 2048)
         return launch_gemm<256, 256, 64, 2, 4>(d, a, b_packed, M, N, K, ep, vec16);

@@ -47,6 +47,7 @@ SHAPES = [
     (129, 257, 80), (300, 200, 48), (2048, 2048, 512), (2304, 2176, 1024),
     (33, 40, 130), (100, 50, 77), (5, 7, 3),  # K % 16 != 0: byte-gather path
     (2, 100, 512), (17, 4096, 4096), (31, 64, 1024), (16, 16, 512), (5, 11008, 4096), (32, 40, 512),  # skinny
+    (512, 768, 64), (768, 512, 192), (1024, 256, 4160),  # full-tile kernel: K % 64 == 0, K % 128 != 0
 ]
 
 
@@ -79,12 +80,13 @@ def test_gemm_i8_per_tensor_scales_and_no_bias(hip):
     np.testing.assert_array_equal(bits32(out), bits32(O.ko_epilogue(eacc, [0.01], [0.02], None)))
 
 
-def test_gemm_i8_extreme_values(hip):
+@pytest.mark.parametrize("M,N", [(64, 128), (256, 256)])  # general and full-tile kernels
+def test_gemm_i8_extreme_values(hip, M, N):
     """All -127: the largest accumulator magnitude, 127*127*K."""
     H, D = hip
     K = 8192
-    a = np.full((64, K), -127, np.int8)
-    bt = np.full((128, K), -127, np.int8)
+    a = np.full((M, K), -127, np.int8)
+    bt = np.full((N, K), -127, np.int8)
     a[1] = 127
     _, acc = run_gemm(H, D, a, bt, [1.0], [1.0], None)
     assert (acc[0] == 127 * 127 * K).all() and (acc[1] == -127 * 127 * K).all()
