@@ -160,6 +160,7 @@ __device__ __forceinline__ unsigned pack4(f32x4 v, const Scale& sc) {
 // stores beyond it are dropped, so the row edge needs no per-access test,
 // and each access needs one VGPR offset (the per-step offset is an SGPR).
 constexpr int kBufferFlags = 0x00020000;  // dword 3 of a raw gfx9 buffer resource (32-bit data)
+constexpr int kCacheNontemporal = 2;      // buffer instruction cache-policy operand: nt
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* base, int64_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kBufferFlags);
@@ -179,11 +180,14 @@ __global__ __launch_bounds__(256) void quant_rows_reg_kernel(const float* __rest
     // An inactive slot (past the last row) gets an empty resource: loads read 0.
     const __amdgpu_buffer_rsrc_t xr = row_rsrc(x + (active ? row : 0) * cols, active ? cols * 4 : 0);
 
+    // Each value is read once: nontemporal loads (the row is not read again
+    // unless a group takes the exact path); the codes are stored normally.
     f32x4 v[VPT];
     AbsMax am;
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
-        v[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, lt * 16, i * ROW_THREADS * 16, 0));
+        v[i] = __builtin_bit_cast(
+            f32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, lt * 16, i * ROW_THREADS * 16, kCacheNontemporal));
         am.add4(v[i]);
     }
     unsigned mb = wave_max(am.bits());
@@ -203,20 +207,24 @@ __global__ __launch_bounds__(256) void quant_rows_reg_kernel(const float* __rest
         if (sc.bad) flag_nonfinite(fault);
     }
     // Fast path for every element, stored as it is produced; the registers
-    // holding the row die group by group.  Threads with an undecided element
-    // (about one wave in five) then redo their groups from memory.
+    // holding the row die group by group.  A group of four holding an
+    // undecided element (|d| within kTieEps of a half; about one per 30k
+    // elements) is then redone from memory by the exact path and stored again.
     const __amdgpu_buffer_rsrc_t qr = row_rsrc(q + row * cols, cols);
-    bool ok = sc.fast;
+    unsigned redo = sc.fast ? 0u : (VPT >= 32 ? ~0u : ((1u << VPT) - 1u));
 #pragma unroll
-    for (int i = 0; i < VPT; ++i)
-        __builtin_amdgcn_raw_buffer_store_b32(pack4_fast(v[i], sc.rf, ok), qr, lt * 4, i * ROW_THREADS * 4, 0);
-    if (!ok) {
-#pragma unroll 1
-        for (int i = 0; i < VPT; ++i) {
-            const f32x4 vv = __builtin_bit_cast(
-                f32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, lt * 16, i * ROW_THREADS * 16, 0));
-            __builtin_amdgcn_raw_buffer_store_b32(pack4(vv, sc), qr, lt * 4, i * ROW_THREADS * 4, 0);
-        }
+    for (int i = 0; i < VPT; ++i) {
+        bool ok = true;
+        const unsigned w = pack4_fast(v[i], sc.rf, ok);
+        if (!ok) redo |= 1u << i;
+        __builtin_amdgcn_raw_buffer_store_b32(w, qr, lt * 4, i * ROW_THREADS * 4, 0);
+    }
+    while (redo) {
+        const int i = __builtin_ctz(redo);
+        redo &= redo - 1;
+        const f32x4 vv =
+            __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, lt * 16, i * ROW_THREADS * 16, 0));
+        __builtin_amdgcn_raw_buffer_store_b32(pack4(vv, sc), qr, lt * 4, i * ROW_THREADS * 4, 0);
     }
 }
 
@@ -425,6 +433,8 @@ __device__ __forceinline__ f32x4 deq4(unsigned w, double s) {
 // one row (per-row scale uniform over the block; per-tensor: rows == 1).
 // Each lane reads 4 codes (one u32) and writes one 16-byte float4 per step,
 // so every load and store instruction covers a contiguous span of the wave.
+// Codes load through the cache normally; the fp32 output is written with
+// nontemporal stores (measured fastest of the four load/store policy pairs).
 // Requires cols % 4 == 0, q 4-byte and out 16-byte aligned.
 constexpr int kDeqSteps = 4;
 constexpr int kDeqPerBlock = 256 * 4 * kDeqSteps;
@@ -441,7 +451,7 @@ __global__ __launch_bounds__(256) void dequant_vec_kernel(const int8_t* __restri
 #pragma unroll
     for (int step = 0; step < kDeqSteps; ++step) {
         const int64_t i = base + step * 256;
-        if (i < c4) __builtin_nontemporal_store(deq4(__builtin_nontemporal_load(qr + i), s), orow + i);
+        if (i < c4) __builtin_nontemporal_store(deq4(qr[i], s), orow + i);
     }
 }
 
