@@ -23,6 +23,7 @@
 #include <hip/hip_runtime.h>
 
 #include "kh_common.h"
+#include "kh_quant_math.h"
 
 #pragma clang fp contract(off)
 
@@ -521,6 +522,157 @@ int launch_gemm(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, int6
     return kh::launch_status("gemm_i8");
 }
 
+// ---------------------------------------------------------------------------
+// Decode Linear for one or two tokens (kh_linear_i8 with M <= 2): the per-token
+// quantize of the fp32 activations is fused into the weight-streaming GEMM,
+// so a decode step is one launch instead of two dependent ones.
+//
+// A workgroup (8 waves) owns 16 output columns for all M rows; wave w covers
+// k in [w * K/8, (w+1) * K/8) as S = K/512 steps of v_mfma_i32_16x16x64_i8.
+// Each workgroup reads the activations first (M x K fp32, L2-resident after
+// the first workgroup touches them), then issues all its weight loads, so
+// the in-order vmcnt wait for the activations does not wait for the weights;
+// while the weights stream in it reduces each row's absmax (wave shuffles and
+// an LDS table), quantizes the row with the reference's arithmetic into LDS
+// codes (workgroup 0 also writes the codes and scales to q_out / sx_out, the
+// outputs kh_linear_i8 documents), then multiplies.  Groups with an
+// undecided element take the exact path out of line, from memory.
+// ---------------------------------------------------------------------------
+template <int S, int MAXM>
+__global__ __launch_bounds__(512) void linear_i8_decode_kernel(const float* __restrict__ x, int M,
+                                                               const int8_t* __restrict__ B, int N,
+                                                               const double* __restrict__ sb, int sb_per_col,
+                                                               const float* __restrict__ bias,
+                                                               float* __restrict__ out, int8_t* __restrict__ q_out,
+                                                               double* __restrict__ sx_out,
+                                                               unsigned* __restrict__ fault) {
+    using namespace kh::quant;
+    constexpr int W = 8, T = W * 64;
+    constexpr int K = 512 * S;
+    constexpr int XH = K / 4 / T;  // float4 of each row per thread
+    constexpr int kRow = K + 16;   // padded LDS code row: 16 rows at one k hit distinct banks
+    static_assert(XH >= 1 && MAXM * XH <= 32, "shape");
+    __shared__ __attribute__((aligned(16))) int8_t codes[MAXM * kRow];
+    __shared__ unsigned rmax[W][MAXM];
+    __shared__ i32x4 red[W][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)M * (uint32_t)K * 4u);
+    f32x4 xv[MAXM][XH];
+#pragma unroll
+    for (int m = 0; m < MAXM; ++m)
+#pragma unroll
+        for (int h = 0; h < XH; ++h)
+            xv[m][h] = __builtin_bit_cast(
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (m * K + (threadIdx.x + h * T) * 4) * 4, 0, 0));
+
+    const int cl = lane & 15, g = lane >> 4;
+    const int kb = wave * (S * 64) + g * 16;
+    const int col = blockIdx.x * 16 + cl;
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(B, (uint32_t)N * (uint32_t)K);
+    i32x4 b[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) b[s] = __builtin_amdgcn_raw_buffer_load_b128(rb, min(col, N - 1) * K + kb, s * 64, 0);
+
+#pragma unroll
+    for (int m = 0; m < MAXM; ++m) {
+        AbsMax am;
+#pragma unroll
+        for (int h = 0; h < XH; ++h) am.add4(xv[m][h]);
+        const unsigned mb = wave_max(am.bits());
+        if (lane == 0) rmax[wave][m] = mb;
+    }
+    __builtin_amdgcn_s_waitcnt(wait_imm(63, 0));
+    __builtin_amdgcn_s_barrier();
+
+    unsigned redo = 0;
+#pragma unroll
+    for (int m = 0; m < MAXM; ++m) {
+        if (m >= M) break;
+        unsigned mb = rmax[0][m];
+#pragma unroll
+        for (int w = 1; w < W; ++w) mb = max(mb, rmax[w][m]);
+        const Scale sc = make_scale(mb);
+        if (blockIdx.x == 0 && threadIdx.x == 0) {
+            sx_out[m] = sc.s;
+            if (sc.bad) flag_nonfinite(fault);
+        }
+#pragma unroll
+        for (int h = 0; h < XH; ++h) {
+            const int e4 = threadIdx.x + h * T;
+            bool ok = sc.fast;
+            const unsigned w4 = pack4_fast(xv[m][h], sc.rf, ok);
+            if (!ok) redo |= 1u << (m * XH + h);
+            *reinterpret_cast<unsigned*>(codes + m * kRow + e4 * 4) = w4;
+            if (blockIdx.x == 0) *reinterpret_cast<unsigned*>(q_out + (int64_t)m * K + e4 * 4) = w4;
+        }
+    }
+    while (redo) {
+        const int bit = __builtin_ctz(redo);
+        redo &= redo - 1;
+        const int m = bit / XH, h = bit % XH;
+        unsigned mb = rmax[0][m];
+        for (int w = 1; w < W; ++w) mb = max(mb, rmax[w][m]);
+        const Scale sc = make_scale(mb);
+        const int e4 = threadIdx.x + h * T;
+        const f32x4 vv =
+            __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (m * K + e4 * 4) * 4, 0, 0));
+        const unsigned w4 = pack4(vv, sc);
+        *reinterpret_cast<unsigned*>(codes + m * kRow + e4 * 4) = w4;
+        if (blockIdx.x == 0) *reinterpret_cast<unsigned*>(q_out + (int64_t)m * K + e4 * 4) = w4;
+    }
+    __builtin_amdgcn_s_waitcnt(wait_imm(63, 0));
+    __builtin_amdgcn_s_barrier();
+
+    i32x4 acc = {0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        const i32x4 af = (cl < M) ? *reinterpret_cast<const i32x4*>(codes + cl * kRow + kb + s * 64) : i32x4{0, 0, 0, 0};
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, b[s], acc, 0, 0, 0);
+    }
+    red[wave][lane] = acc;
+    __syncthreads();
+    if (wave != 0 || col >= N) return;
+    i32x4 sum = red[0][lane];
+#pragma unroll
+    for (int w = 1; w < W; ++w) sum += red[w][lane];
+    // 16x16 MFMA result layout: register r of lane l holds row 4 * (l / 16) + r, column l % 16.
+    const double sbj = sb[sb_per_col ? col : 0];
+    const float bj = bias ? bias[col] : 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int i = 4 * g + r;
+        if (i >= M) continue;
+        unsigned mb = rmax[0][i];
+#pragma unroll
+        for (int w = 1; w < W; ++w) mb = max(mb, rmax[w][i]);
+        float y = (float)((double)sum[r] * (make_scale(mb).s * sbj));
+        if (bias) y = y + bj;
+        out[(int64_t)i * N + col] = y;
+    }
+}
+
+template <int S>
+int launch_decode(kh::Device* d, const float* x, int64_t M, const int8_t* B, int64_t N, const double* sb,
+                  int sb_per_col, const float* bias, float* out, int8_t* q, double* sx) {
+    const unsigned blocks = (unsigned)((N + 15) / 16);
+    if (M == 1)
+        linear_i8_decode_kernel<S, 1><<<blocks, 512, 0, d->stream>>>(x, (int)M, B, (int)N, sb, sb_per_col, bias, out, q,
+                                                                      sx, d->fault);
+    else
+        linear_i8_decode_kernel<S, 2><<<blocks, 512, 0, d->stream>>>(x, (int)M, B, (int)N, sb, sb_per_col, bias, out, q,
+                                                                      sx, d->fault);
+    return kh::launch_status("linear_i8_decode");
+}
+
+// True when the fused decode kernel covers this call.
+bool decode_fits(const float* x, int64_t M, int64_t K, const int8_t* B, int64_t N, const int8_t* q) {
+    return M >= 1 && M <= 2 && (K == 2048 || K == 4096 || K == 8192) && N >= 1 &&
+           N * K <= 0xFFFFFFFFLL && (N + 15) / 16 <= 0x7FFFFFFFLL && kh::aligned(x, 16) && kh::aligned(B, 16) &&
+           kh::aligned(q, 4);
+}
+
 }  // namespace
 
 extern "C" {
@@ -547,6 +699,15 @@ int kh_gemm_i8(const int8_t* a, const int8_t* b_packed, int64_t M, int64_t N, in
 int kh_linear_i8(const float* x, int64_t M, int64_t K, const int8_t* b_packed, int64_t N, const double* sb,
                  int sb_per_col, const float* bias, int8_t* q_scratch, double* sx_scratch, float* out) {
     KH_REQUIRE(out, "kh_linear_i8: null out");
+    if (M >= 1 && N >= 1 && x && b_packed && sb && q_scratch && sx_scratch &&
+        decode_fits(x, M, K, b_packed, N, q_scratch)) {
+        KH_DEVICE_OR_RETURN(d);
+        switch (K) {
+            case 2048: return launch_decode<4>(d, x, M, b_packed, N, sb, sb_per_col, bias, out, q_scratch, sx_scratch);
+            case 4096: return launch_decode<8>(d, x, M, b_packed, N, sb, sb_per_col, bias, out, q_scratch, sx_scratch);
+            default: return launch_decode<16>(d, x, M, b_packed, N, sb, sb_per_col, bias, out, q_scratch, sx_scratch);
+        }
+    }
     int rc = kh_quantize_rows(x, M, K, q_scratch, sx_scratch);
     if (rc) return rc;
     return kh_gemm_i8(q_scratch, b_packed, M, N, K, sx_scratch, 1, sb, sb_per_col, bias, out, nullptr);

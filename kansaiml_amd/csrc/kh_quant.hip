@@ -31,125 +31,11 @@
 
 #pragma clang fp contract(off)
 
+#include "kh_quant_math.h"
+
+using namespace kh::quant;
+
 namespace {
-
-// Native clang vectors (the nontemporal builtins reject HIP's struct vectors).
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-
-constexpr float kTieEps = 1.0f / 32768.0f;
-// |v * rf - k| <= kFastHalf  <=>  v * rf is at least kTieEps from a half-integer.
-constexpr float kFastHalf = 0.5f - kTieEps;
-constexpr unsigned kFastMinBits = 0x1F800000u;  // 2^-64
-// 1.5 * 2^23: for |x| < 2^22, fl32(x + kMagic) = kMagic + rint(x) (binary32
-// spacing is 1 there; kMagic is even so ties go to the even integer), and the
-// low byte of its bit pattern is rint(x) as a two's-complement int8.
-constexpr float kMagic = 12582912.0f;
-
-__device__ __forceinline__ unsigned abs_bits(float v) { return __float_as_uint(v) & 0x7FFFFFFFu; }
-
-// Running absmax over raw bit patterns without masking each value: the
-// unsigned max is dominated by negative values (sign bit set) and the signed
-// max by positive ones.  Both keep NaN/inf patterns, which compare above
-// every finite magnitude.
-struct AbsMax {
-    unsigned umax = 0;
-    int smax = 0;
-    __device__ __forceinline__ void add4(f32x4 v) {
-        const unsigned b0 = __float_as_uint(v.x), b1 = __float_as_uint(v.y);
-        const unsigned b2 = __float_as_uint(v.z), b3 = __float_as_uint(v.w);
-        umax = max(umax, max(max(b0, b1), max(b2, b3)));
-        smax = max(smax, max(max((int)b0, (int)b1), max((int)b2, (int)b3)));
-    }
-    __device__ __forceinline__ void add1(float v) {
-        const unsigned b = __float_as_uint(v);
-        umax = max(umax, b);
-        smax = max(smax, (int)b);
-    }
-    // |max| as bits (>= 0x7F800000 if any value was NaN or inf).
-    __device__ __forceinline__ unsigned bits() const { return max(umax & 0x7FFFFFFFu, (unsigned)max(smax, 0)); }
-};
-
-__device__ __forceinline__ unsigned wave_max(unsigned v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = max(v, (unsigned)__shfl_xor((int)v, off, 64));
-    return v;
-}
-
-struct Scale {
-    double s;    // the reference's binary64 scale
-    float rf;    // binary32 reciprocal for the fast path
-    bool fast;   // fast path allowed for this slice
-    bool bad;    // slice holds NaN or +-inf
-};
-
-// quantize.py:67-68 from the absmax bit pattern.
-__device__ __forceinline__ Scale make_scale(unsigned mbits) {
-    Scale r;
-    r.bad = mbits >= KH_NONFINITE_BITS;
-    const float m = __uint_as_float(mbits);
-    r.s = r.bad ? __longlong_as_double(0x7FF8000000000000LL) : (m > 0.0f ? (double)m / 127.0 : 1.0);
-    r.rf = r.bad ? 0.0f : (float)(1.0 / r.s);
-    r.fast = !r.bad && mbits >= kFastMinBits;
-    return r;
-}
-
-__device__ __forceinline__ void flag_nonfinite(unsigned* fault) { atomicOr(fault, kh::kFaultNonFinite); }
-
-// quantize.py:69 exactly: binary64 divide, rint (ties to even), clamp.
-__device__ __forceinline__ int quant_exact(float v, double s) {
-    const int q = (int)rint((double)v / s);
-    return min(127, max(-127, q));
-}
-
-// Fast path for one value: a's low byte is the code; `ok` is cleared when
-// the exact path is needed.
-__device__ __forceinline__ unsigned quant_fast(float v, float rf, bool& ok) {
-    const float a = __builtin_fmaf(v, rf, kMagic);
-    const float d = __builtin_fmaf(v, rf, -(a - kMagic));
-    ok = ok && (fabsf(d) <= kFastHalf);
-    return __float_as_uint(a);
-}
-
-__device__ __forceinline__ int quant_one(float v, const Scale& sc) {
-    if (sc.bad) return 0;
-    if (sc.fast) {
-        bool ok = true;
-        const unsigned a = quant_fast(v, sc.rf, ok);
-        if (ok) return (int)(int8_t)(a & 0xFFu);
-    }
-    return quant_exact(v, sc.s);
-}
-
-// Four values -> four packed codes (byte e = code of v[e]) by the fast path.
-__device__ __forceinline__ unsigned pack4_fast(f32x4 v, float rf, bool& ok) {
-    const unsigned a0 = quant_fast(v.x, rf, ok);
-    const unsigned a1 = quant_fast(v.y, rf, ok);
-    const unsigned a2 = quant_fast(v.z, rf, ok);
-    const unsigned a3 = quant_fast(v.w, rf, ok);
-    // v_perm_b32: byte 0 of each source into bytes 0..3.
-    return __builtin_amdgcn_perm(a1, a0, 0x0c0c0400u) | __builtin_amdgcn_perm(a3, a2, 0x04000c0cu);
-}
-
-// Four values -> four packed codes, each by the fast path where it is
-// decisive and by the exact path otherwise.
-__device__ __forceinline__ unsigned pack4_checked(f32x4 v, const Scale& sc) {
-    if (sc.bad) return 0u;
-    const unsigned b0 = (unsigned)(quant_one(v.x, sc) & 0xFF);
-    const unsigned b1 = (unsigned)(quant_one(v.y, sc) & 0xFF);
-    const unsigned b2 = (unsigned)(quant_one(v.z, sc) & 0xFF);
-    const unsigned b3 = (unsigned)(quant_one(v.w, sc) & 0xFF);
-    return b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
-}
-
-__device__ __forceinline__ unsigned pack4(f32x4 v, const Scale& sc) {
-    if (sc.fast) {
-        bool ok = true;
-        const unsigned w = pack4_fast(v, sc.rf, ok);
-        if (ok) return w;
-    }
-    return pack4_checked(v, sc);
-}
 
 // ---------------------------------------------------------------------------
 // Per-row quantize, row held in registers.  ROW_THREADS = 64 * WAVES_PER_ROW

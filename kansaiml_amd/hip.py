@@ -154,9 +154,10 @@ def dequantize_acc(acc: DeviceTensor, sa: DeviceTensor, sb: DeviceTensor,
 
 
 def linear_i8(x: DeviceTensor, b_packed: DeviceTensor, sb: DeviceTensor,
-              bias: DeviceTensor | None = None) -> DeviceTensor:
+              bias: DeviceTensor | None = None, return_codes: bool = False):
     """Per-token dynamic quantize of x [M, K] fp32, then the int8 GEMM with
-    the fused epilogue."""
+    the fused epilogue.  With return_codes, also returns the activation codes
+    (int8 [M, K]) and per-token scales (float64 [M]) the call produced."""
     _need(x, "float32", 2, "linear_i8(x)")
     _need(b_packed, "int8", 2, "linear_i8(w)")
     M, K = x.shape
@@ -168,7 +169,7 @@ def linear_i8(x: DeviceTensor, b_packed: DeviceTensor, sb: DeviceTensor,
     sx = DeviceTensor([M], "float64")
     out = DeviceTensor([M, Nn], "float32")
     N.call("kh_linear_i8", x.ptr, M, K, b_packed.ptr, Nn, sb.ptr, sb_mode, _opt(bias), q.ptr, sx.ptr, out.ptr)
-    return out
+    return (out, q, sx) if return_codes else out
 
 
 # ---------------------------------------------------------------------------

@@ -150,6 +150,34 @@ def test_linear_i8_per_token(hip):
         np.testing.assert_array_equal(bits32(out), bits32(expect))
 
 
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 4096), (2, 4096, 11008), (1, 2048, 1000), (2, 8192, 33),
+                                   (1, 8192, 4096), (2, 2048, 17)])
+def test_linear_i8_decode_fused(hip, M, K, N):
+    """The fused one-launch decode path of kh_linear_i8 (M <= 2): outputs,
+    activation codes and per-token scales bit-exact against the oracle, with
+    an all-zero row, a row of exact ties (binary64 fallback), a per-tensor
+    weight scale and no bias."""
+    H, D = hip
+    gen = np.random.Generator(np.random.PCG64(M * 7919 + K + N))
+    x = gen.standard_normal((M, K), dtype=np.float32)
+    if M == 2:
+        x[1] = 0.0                                        # zero row: scale 1.0, codes 0
+    tie = x[0].copy()
+    tie[: K // 2] = np.float32(0.5)                       # 0.5 / (1 / 127) = 63.5: an exact tie
+    tie[K // 2:] = np.float32(1.0)                       # row max 1.0, so the scale is 1/127
+    qw = gen.integers(-127, 128, (N, K), dtype=np.int8)
+    sw = gen.uniform(1e-3, 1e-2, N)
+    bias = gen.standard_normal(N).astype(np.float32)
+    for xin, sb, bb in ((x, sw, bias), (x, sw[:1], None), (np.stack([tie] * M), sw, bias)):
+        out, q, sx = H.linear_i8(D.from_host(xin), D.from_host(qw), D.from_host(np.asarray(sb, np.float64)),
+                                 D.from_host(bb) if bb is not None else None, return_codes=True)
+        eq, esx = O.ko_quantize_rows(xin)
+        np.testing.assert_array_equal(q.numpy(), eq)
+        np.testing.assert_array_equal(sx.numpy().view(np.uint64), np.asarray(esx, np.float64).view(np.uint64))
+        expect = O.ko_epilogue(O.ko_gemm_i8(eq, qw), esx, sb, bb)
+        np.testing.assert_array_equal(bits32(out.numpy()), bits32(expect))
+
+
 def test_dequantize_acc_matches_fused(hip):
     H, D = hip
     gen = np.random.Generator(np.random.PCG64(9))
