@@ -101,110 +101,177 @@ __global__ __launch_bounds__(256) void gelu_kernel(const float* __restrict__ x, 
 }
 
 // ---------------------------------------------------------------------------
-// Causal attention, fp32, flash-style (online softmax).
+// Causal attention, fp32, flash-style (online softmax) on fp32 MFMA.
 //
 // qkv: [B*T, 3*D] row-major, the fused Q|K|V projection output (head h of Q
 // at columns h*dk .. h*dk+dk-1, K at D + h*dk, V at 2D + h*dk).  out: [B*T, D],
-// head h written to its own columns (heads are merged in place).
-// One thread per query: the query row and its output accumulator live in
-// registers; K and V rows are staged in LDS 64 keys at a time and every lane
-// of a wave reads the same K/V row (an LDS broadcast), so each 16-byte LDS
-// read feeds four FMAs per lane.  The softmax is rescaled once per chunk of
-// 16 keys.  A workgroup owns kQ queries of one (batch, head).  dk = 64.
+// head h written to its own columns (heads are merged in place).  dk = 64.
+//
+// A workgroup owns 64 queries of one (batch, head); wave w owns queries
+// 16w .. 16w+15 of them.  Keys go through LDS 64 at a time: K as [key][d]
+// and V transposed as [d][key], rows padded to 68 floats so the 16 lanes of
+// a fragment read hit distinct banks.  Both products run on
+// v_mfma_f32_16x16x4_f32 (D[i][j] += sum over k of A[i][k] B[k][j], lane
+// l supplying A[l % 16][l / 16] and B[l / 16][l % 16]).  The dot product over
+// the head dimension is order-free, so MFMA step s of lane group g = l / 16
+// takes d = 16g + s: each lane's operands for 16 steps are 16 consecutive
+// floats (four ds_read_b128).  S = (Q/8) K^T comes out with lane l holding
+// rows 4 * (l / 16) + r, key l % 16: row max and row sum reduce over the 16
+// lanes of a group.  P goes through a per-wave LDS tile to the A layout of
+// the P V product, whose k index (the key) is mapped the same way.
+// The 1/sqrt(dk) = 1/8 scale is applied to Q (exact: a power of two).
 // ---------------------------------------------------------------------------
 constexpr int kDk = 64;
-constexpr int kQ = 128;  // queries (threads) per workgroup
-constexpr int kKT = 64;  // keys per LDS tile
-constexpr int kChunk = 16;
+constexpr int kAttQ = 64;      // queries per workgroup (16 per wave)
+constexpr int kAttK = 64;      // keys per LDS tile
+constexpr int kAttPad = 68;    // padded LDS row, floats
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
-__global__ __launch_bounds__(kQ) void attention_kernel(const float* __restrict__ qkv, int B, int T, int H,
-                                                       float scale, float* __restrict__ out) {
-    __shared__ __attribute__((aligned(16))) float ks[kKT][kDk];
-    __shared__ __attribute__((aligned(16))) float vs[kKT][kDk];
+// max / sum over the 16 lanes of this lane's group (lanes 16g .. 16g+15).
+__device__ __forceinline__ float group16_max(float v) {
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+__device__ __forceinline__ float group16_sum(float v) {
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__global__ __launch_bounds__(256) void attention_mfma_kernel(const float* __restrict__ qkv, int B, int T, int H,
+                                                             float* __restrict__ out) {
+    __shared__ __attribute__((aligned(16))) float ks[kAttK][kAttPad];
+    __shared__ __attribute__((aligned(16))) float vt[kDk][kAttPad];
+    __shared__ __attribute__((aligned(16))) float ps[4][16][kAttPad];
     const int D = H * kDk;
     const int qb = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int tid = threadIdx.x;
-    const int q = qb * kQ + tid;
-    const bool qvalid = q < T;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, g = lane >> 4;
     const int64_t row0 = (int64_t)b * T;
+    const int q0 = qb * kAttQ + wave * 16;  // this wave's first query
 
-    float qv[kDk], o[kDk];
+    // Q fragment: query q0 + li, d = 16g .. 16g+15, scaled by 1/8.
+    float qf[16];
     {
-        const f32x4v* qr = reinterpret_cast<const f32x4v*>(qkv + (row0 + (qvalid ? q : 0)) * 3 * D + h * kDk);
+        const int q = q0 + li;
+        const f32x4v* qr = reinterpret_cast<const f32x4v*>(qkv + (row0 + min(q, T - 1)) * 3 * D + h * kDk + 16 * g);
 #pragma unroll
-        for (int d4 = 0; d4 < kDk / 4; ++d4) {
-            const f32x4v v = qr[d4];
+        for (int c = 0; c < 4; ++c) {
+            const f32x4v v = qr[c];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) qv[4 * d4 + e] = qvalid ? v[e] * scale : 0.0f;
+            for (int e = 0; e < 4; ++e) qf[4 * c + e] = q < T ? v[e] * 0.125f : 0.0f;
         }
     }
+    f32x4v o[4];  // output tile: d-subtile j, rows 4g + r, column d = 16j + li
 #pragma unroll
-    for (int d = 0; d < kDk; ++d) o[d] = 0.0f;
-    float m = -3.0e38f, l = 0.0f;
+    for (int j = 0; j < 4; ++j) o[j] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    float m[4], l[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        m[r] = -3.0e38f;
+        l[r] = 0.0f;
+    }
 
-    const int q_last = min(T, (qb + 1) * kQ) - 1;
-    for (int k0 = 0; k0 <= q_last; k0 += kKT) {
-        __syncthreads();
-        for (int e = tid; e < kKT * kDk / 4; e += kQ) {
-            const int kk = e / (kDk / 4), d4 = e % (kDk / 4);
+    const int q_hi = min(T, (qb + 1) * kAttQ) - 1;  // last query of the workgroup
+    for (int k0 = 0; k0 <= q_hi; k0 += kAttK) {
+        __syncthreads();  // previous tile's readers are done
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = tid + i * 256;
+            const int kk = e >> 4, d4 = e & 15;
             const int key = k0 + kk;
-            const bool ok = key < T;
-            const float* kr = qkv + (row0 + (ok ? key : 0)) * 3 * D;
-            const f32x4v zero = {0.f, 0.f, 0.f, 0.f};
-            reinterpret_cast<f32x4v*>(ks[kk])[d4] = ok ? reinterpret_cast<const f32x4v*>(kr + D + h * kDk)[d4] : zero;
-            reinterpret_cast<f32x4v*>(vs[kk])[d4] = ok ? reinterpret_cast<const f32x4v*>(kr + 2 * D + h * kDk)[d4] : zero;
+            f32x4v kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
+            if (key < T) {
+                const float* kr = qkv + (row0 + key) * 3 * D + h * kDk;
+                kv = reinterpret_cast<const f32x4v*>(kr + D)[d4];
+                vv = reinterpret_cast<const f32x4v*>(kr + 2 * D)[d4];
+            }
+            *reinterpret_cast<f32x4v*>(&ks[kk][4 * d4]) = kv;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) vt[4 * d4 + c][kk] = vv[c];
         }
         __syncthreads();
-        if (!qvalid || q < k0) continue;
-        const int n_keys = min(kKT, q - k0 + 1);  // keys <= q in this tile
-        for (int c0 = 0; c0 < n_keys; c0 += kChunk) {
-            float s[kChunk];
-            float cmax = -3.0e38f;
+
+        // S = Q K^T for 4 subtiles of 16 keys.
+        f32x4v sv[4];
 #pragma unroll
-            for (int j = 0; j < kChunk; ++j) {
-                const f32x4v* kr = reinterpret_cast<const f32x4v*>(ks[c0 + j]);
-                float acc = 0.0f;
+        for (int t = 0; t < 4; ++t) {
+            sv[t] = f32x4v{0.f, 0.f, 0.f, 0.f};
+            const f32x4v* kr = reinterpret_cast<const f32x4v*>(&ks[16 * t + li][16 * g]);
 #pragma unroll
-                for (int d4 = 0; d4 < kDk / 4; ++d4) {
-                    const f32x4v kv = kr[d4];
-                    acc += qv[4 * d4] * kv[0];
-                    acc += qv[4 * d4 + 1] * kv[1];
-                    acc += qv[4 * d4 + 2] * kv[2];
-                    acc += qv[4 * d4 + 3] * kv[3];
-                }
-                s[j] = (c0 + j < n_keys) ? acc : -3.0e38f;
-                cmax = fmaxf(cmax, s[j]);
+            for (int c = 0; c < 4; ++c) {
+                const f32x4v kv = kr[c];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    sv[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[4 * c + e], kv[e], sv[t], 0, 0, 0);
             }
-            const float m_new = fmaxf(m, cmax);
-            const float corr = __expf(m - m_new);
-            l *= corr;
+        }
+        // Causal mask (key > query) and keys past T; online softmax per row.
+        float corr[4];
 #pragma unroll
-            for (int d = 0; d < kDk; ++d) o[d] *= corr;
+        for (int r = 0; r < 4; ++r) {
+            const int q = q0 + 4 * g + r;
+            float mx = -3.0e38f;
 #pragma unroll
-            for (int j = 0; j < kChunk; ++j) {
-                const float p = (c0 + j < n_keys) ? __expf(s[j] - m_new) : 0.0f;
-                l += p;
-                const f32x4v* vr = reinterpret_cast<const f32x4v*>(vs[c0 + j]);
-#pragma unroll
-                for (int d4 = 0; d4 < kDk / 4; ++d4) {
-                    const f32x4v vv = vr[d4];
-                    o[4 * d4] += p * vv[0];
-                    o[4 * d4 + 1] += p * vv[1];
-                    o[4 * d4 + 2] += p * vv[2];
-                    o[4 * d4 + 3] += p * vv[3];
-                }
+            for (int t = 0; t < 4; ++t) {
+                const int key = k0 + 16 * t + li;
+                if (key > q || key >= T) sv[t][r] = -3.0e38f;
+                mx = fmaxf(mx, sv[t][r]);
             }
-            m = m_new;
+            mx = group16_max(mx);
+            const float m_new = fmaxf(m[r], mx);
+            corr[r] = __expf(m[r] - m_new);
+            float sum = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int key = k0 + 16 * t + li;
+                const float p = (key > q || key >= T) ? 0.0f : __expf(sv[t][r] - m_new);
+                sv[t][r] = p;
+                sum += p;
+            }
+            l[r] = l[r] * corr[r] + group16_sum(sum);
+            m[r] = m_new;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[j][r] *= corr[r];
+        // P to LDS (row 4g + r, key 16t + li), then read back in A layout.
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ps[wave][4 * g + r][16 * t + li] = sv[t][r];
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's P stores are done
+        __builtin_amdgcn_wave_barrier();
+        f32x4v pf[4];
+        {
+            const f32x4v* pr = reinterpret_cast<const f32x4v*>(&ps[wave][li][16 * g]);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) pf[c] = pr[c];
+        }
+        // O += P V: A = P (query li, key 16g + s), B = V (key 16g + s, d 16j + li).
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const f32x4v* vr = reinterpret_cast<const f32x4v*>(&vt[16 * j + li][16 * g]);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const f32x4v vv = vr[c];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(pf[c][e], vv[e], o[j], 0, 0, 0);
+            }
         }
     }
-    if (!qvalid) return;
-    const float inv = 1.0f / l;
-    f32x4v* orow = reinterpret_cast<f32x4v*>(out + (row0 + q) * D + h * kDk);
 #pragma unroll
-    for (int d4 = 0; d4 < kDk / 4; ++d4)
-        orow[d4] = f32x4v{o[4 * d4] * inv, o[4 * d4 + 1] * inv, o[4 * d4 + 2] * inv, o[4 * d4 + 3] * inv};
+    for (int r = 0; r < 4; ++r) {
+        const int q = q0 + 4 * g + r;
+        if (q >= T) continue;
+        const float inv = 1.0f / l[r];
+        float* orow = out + (row0 + q) * D + h * kDk;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) orow[16 * j + li] = o[j][r] * inv;
+    }
 }
 
 }  // namespace
@@ -250,11 +317,11 @@ int kh_causal_attention(const float* qkv, int B, int T, int H, int dk, float* ou
     KH_REQUIRE(qkv && out, "kh_causal_attention: null pointer");
     KH_DEVICE_OR_RETURN(d);
     KH_REQUIRE(kh::aligned(qkv, 16) && kh::aligned(out, 16), "kh_causal_attention: 16-byte aligned buffers required");
-    dim3 grid((unsigned)((T + kQ - 1) / kQ), (unsigned)H, (unsigned)B);
-    // 1/sqrt(d_k) as the reference forms it: a binary64 Python float narrowed
-    // to binary32 by from_flat (nn.py:413).
-    const float scale = (float)(1.0 / 8.0);
-    attention_kernel<<<grid, kQ, 0, d->stream>>>(qkv, B, T, H, scale, out);
+    dim3 grid((unsigned)((T + kAttQ - 1) / kAttQ), (unsigned)H, (unsigned)B);
+    // 1/sqrt(d_k) = 1/8 for dk = 64 (the reference's binary64 Python float,
+    // nn.py:413, is exactly representable in binary32); the kernel applies it
+    // to Q.
+    attention_mfma_kernel<<<grid, 256, 0, d->stream>>>(qkv, B, T, H, out);
     return kh::launch_status("attention");
 }
 
