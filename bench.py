@@ -212,6 +212,23 @@ def bench_c4(steps, warmup):
 COPY_BYTES = 1 << 30
 
 
+def bench_mfma_probe():
+    """The attainable int8 MFMA rate and the shader clock under that load
+    (kh_probe_mfma_i8): random operand bytes, no memory traffic in the loop.
+    The published 5.0 POP/s assumes the 2.4 GHz peak clock."""
+    from kansaiml_amd import _native as Nn
+    from kansaiml_amd.device import DeviceTensor as D
+    import ctypes
+    info = Nn.device_info()
+    nbytes = info["cus"] * 64 * 1024
+    ops = D.from_host(np.random.Generator(np.random.PCG64(11)).integers(-127, 128, nbytes, dtype=np.int8))
+    tops, mhz = ctypes.c_double(), ctypes.c_double()
+    Nn.call("kh_probe_mfma_i8", ops.ptr, nbytes, 2000, ctypes.byref(tops), ctypes.byref(mhz))  # warm up
+    Nn.call("kh_probe_mfma_i8", ops.ptr, nbytes, 20000, ctypes.byref(tops), ctypes.byref(mhz))
+    return {"workload": "v_mfma_i32_32x32x32_i8 only, random int8 operands in registers, 8 waves per CU",
+            "TOPS": round(tops.value, 1), "clock_MHz": round(mhz.value), "frac_of_published": round(tops.value / PEAK_INT8_TOPS, 4)}
+
+
 def bench_copy(steps, warmup):
     """1 GiB device-to-device copy (the library's copy16_kernel): the known-size
     reference for FETCH_SIZE / WRITE_SIZE calibration."""
@@ -225,7 +242,7 @@ def bench_copy(steps, warmup):
 
 # Kernel-name fragments (rocprofv3 Kernel_Name) of the kernels each bench line measures.
 KERNELS = {
-    "gemm_i8_8192": "gemm_i8_tiled_kernel",
+    "gemm_i8_8192": "gemm_i8_pingpong_kernel",
     "quant_rows_16384": "quant_rows_reg_kernel<4, 16>",
     "dequant_rows_16384": "dequant_vec_kernel",
     "fp32_matmul_4096": "gemm_f32_kernel",
@@ -335,7 +352,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", default="gemm,quant,f32,skinny,c4", help="comma list of gemm,quant,f32,skinny,c4,copy")
+    ap.add_argument("--only", default="gemm,probe,quant,f32,skinny,c4",
+                    help="comma list of gemm,probe,quant,f32,skinny,c4,copy")
     ap.add_argument("--summarize", metavar="DIR", help="summarize rocprofv3 CSV output and exit")
     args = ap.parse_args()
     if args.summarize:
@@ -361,6 +379,11 @@ def main():
         g_ms, g_tops, keep = bench_gemm(H, D, args.steps, args.warmup)
         log(f"int8 GEMM: {g_ms:.4f} ms/step, {g_tops:.1f} TOPS")
         del keep
+        Nn.call("kh_pool_trim")
+    probe = None
+    if "probe" in only:
+        probe = bench_mfma_probe()
+        log(f"MFMA-only ceiling: {probe['TOPS']:.0f} TOPS at {probe['clock_MHz']} MHz")
         Nn.call("kh_pool_trim")
     if "quant" in only:
         log("quantize/dequantize C2 ...")
@@ -411,7 +434,8 @@ def main():
         "config": {"workload": "C3a int8 GEMM M=N=K=8192, int32 accumulate, fused dequantize (sa=0.01, sb=0.02) "
                                "to fp32", "M": 8192, "N": 8192, "K": 8192, "parallelism": "single-gpu"},
         "roofline": {"bound": "mfma", "achieved": round(g_tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TOPS",
-                     "frac": round(g_tops / PEAK_INT8_TOPS, 4), "traffic": measured_traffic("gemm_i8_8192")},
+                     "frac": round(g_tops / PEAK_INT8_TOPS, 4), "traffic": measured_traffic("gemm_i8_8192"),
+                     "attainable": probe},
         "quant_dequant": {
             "workload": "C2 per-row quantize and dequantize of fp32 [16384,16384] (1 GiB), 0.1% +-50 outliers",
             "quantize": {"ms": round(q_ms, 5), "GB/s": round(q_gbs, 1),

@@ -215,6 +215,16 @@ int kh_gelu(const float* x, float* out, int64_t n);
  * columns h*dk..); out: [B*T, H*dk] with heads merged in place.  dk == 64. */
 int kh_causal_attention(const float* qkv, int B, int T, int H, int dk, float* out);
 
+/* ---- measurement utility (no reference counterpart) ------------------- */
+
+/* The int8 MFMA rate this device sustains on the given operand bytes and the
+ * shader clock it runs at meanwhile: one workgroup per CU, 8 waves, each
+ * issuing `iters` x 16 independent v_mfma_i32_32x32x32_i8 on 8 operand
+ * registers loaded once from `operands` (16-byte aligned, at least
+ * compute-units x 64 KiB).  Synchronous.  Used by bench.py to state the
+ * attainable int8 peak next to the published one. */
+int kh_probe_mfma_i8(const int8_t* operands, int64_t bytes, int64_t iters, double* tops, double* clock_mhz);
+
 #ifdef __cplusplus
 }
 #endif
