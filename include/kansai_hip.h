@@ -108,6 +108,18 @@ int kh_event_destroy(void* event);
  * tensor of n fp32 values: one scale, written to scale[0]. */
 int kh_quantize_tensor(const float* x, int64_t n, int8_t* q, double* scale);
 
+/* The two passes of kh_quantize_tensor taken apart, so the absmax pass can
+ * ride along with the kernel that produced x (the *_ex entry points below):
+ * kh_absmax_parts writes up to max_parts partial maxima of |x| (as IEEE bit
+ * patterns; NaN/inf sort above every finite value) and their count;
+ * kh_quantize_tensor_parts reduces `nparts` of them to the tensor's absmax
+ * and quantizes exactly as kh_quantize_tensor does.  Internal to the fused
+ * graph path; no reference counterpart (the reference's quantize_symmetric
+ * is one Python function, quantize.py:50-70). */
+int kh_absmax_parts(const float* x, int64_t n, unsigned* parts, int max_parts, int* nparts);
+int kh_quantize_tensor_parts(const float* x, int64_t n, const unsigned* parts, int nparts, int8_t* q,
+                             double* scale);
+
 /* quantize_symmetric applied to each row of a [rows, cols] matrix: one
  * scale per row (per token).  scales has `rows` entries. */
 int kh_quantize_rows(const float* x, int64_t rows, int64_t cols, int8_t* q, double* scales);
@@ -151,6 +163,22 @@ int kh_dequantize_packed(const int8_t* q_packed, int64_t k, int64_t n, const dou
 int kh_gemm_i8(const int8_t* a, const int8_t* b_packed, int64_t M, int64_t N, int64_t K,
                const double* sa, int sa_per_row, const double* sb, int sb_per_col,
                const float* bias, float* out, int32_t* acc_out);
+
+/* kh_gemm_i8's output with the graph's next elementwise steps fused into
+ * the epilogue, in the order the reference applies them:
+ *   y = (float)((double)acc * (sa_i * sb_j)) + bias[j];
+ *   y = act(y)            act: KH_ACT_NONE or KH_ACT_GELU (exact erf,
+ *                         backend/cpu/src/Ops.cpp:250-256);
+ *   out = residual + y    when residual (fp32 [M, N]) is not NULL -- the
+ *                         pre-LN block's x.add(linear(..)), nn.py:466-478.
+ * absmax_parts (may be NULL): up to max_parts partial maxima of |out| for
+ * kh_quantize_tensor_parts, count in *nparts. */
+#define KH_ACT_NONE 0
+#define KH_ACT_GELU 1
+int kh_gemm_i8_ex(const int8_t* a, const int8_t* b_packed, int64_t M, int64_t N, int64_t K,
+                  const double* sa, int sa_per_row, const double* sb, int sb_per_col,
+                  const float* bias, int act, const float* residual, float* out,
+                  unsigned* absmax_parts, int max_parts, int* nparts);
 
 /* Per-token activation quantize fused into the GEMM's producer: x fp32
  * [M, K] is quantized per row into q_scratch (int8 [M, K]) and
@@ -204,6 +232,9 @@ int kh_embedding(const int32_t* ids, int64_t rows, int T, const float* tok, int 
 /* LayerNorm over the last axis (nn.py:308-331): biased variance,
  * (x - mean) / sqrt(var + eps) * weight + bias.  D <= 1024. */
 int kh_layernorm(const float* x, int64_t rows, int D, const float* weight, const float* bias, float eps, float* out);
+/* ... also writing absmax partials of out (see kh_absmax_parts). */
+int kh_layernorm_ex(const float* x, int64_t rows, int D, const float* weight, const float* bias, float eps,
+                    float* out, unsigned* absmax_parts, int max_parts, int* nparts);
 
 /* Exact-erf GELU (backend/cpu/src/Ops.cpp:250-256). */
 int kh_gelu(const float* x, float* out, int64_t n);
@@ -214,6 +245,9 @@ int kh_gelu(const float* x, float* out, int64_t n);
  * mask) V.  qkv: [B*T, 3*H*dk], the fused Q|K|V projection (head h of Q at
  * columns h*dk..); out: [B*T, H*dk] with heads merged in place.  dk == 64. */
 int kh_causal_attention(const float* qkv, int B, int T, int H, int dk, float* out);
+/* ... also writing absmax partials of out (see kh_absmax_parts). */
+int kh_causal_attention_ex(const float* qkv, int B, int T, int H, int dk, float* out, unsigned* absmax_parts,
+                           int max_parts, int* nparts);
 
 /* ---- measurement utility (no reference counterpart) ------------------- */
 

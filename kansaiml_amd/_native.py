@@ -67,6 +67,12 @@ _SIGNATURES = {
     "kh_dequantize_packed": [_vp, _i64, _i64, _vp, _i64, _vp],
     "kh_dequantize_acc": [_vp, _i64, _i64, _vp, _int, _vp, _int, _vp, _vp],
     "kh_gemm_i8": [_vp, _vp, _i64, _i64, _i64, _vp, _int, _vp, _int, _vp, _vp, _vp],
+    "kh_gemm_i8_ex": [_vp, _vp, _i64, _i64, _i64, _vp, _int, _vp, _int, _vp, _int, _vp, _vp, _vp, _int,
+                      ctypes.POINTER(ctypes.c_int)],
+    "kh_absmax_parts": [_vp, _i64, _vp, _int, ctypes.POINTER(ctypes.c_int)],
+    "kh_quantize_tensor_parts": [_vp, _i64, _vp, _int, _vp, _vp],
+    "kh_layernorm_ex": [_vp, _i64, _int, _vp, _vp, ctypes.c_float, _vp, _vp, _int, ctypes.POINTER(ctypes.c_int)],
+    "kh_causal_attention_ex": [_vp, _int, _int, _int, _int, _vp, _vp, _int, ctypes.POINTER(ctypes.c_int)],
     "kh_linear_i8": [_vp, _i64, _i64, _vp, _i64, _vp, _int, _vp, _vp, _vp, _vp],
     "kh_matmul_f32": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "kh_probe_mfma_i8": [_vp, _i64, _i64, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)],

@@ -24,6 +24,7 @@
 
 #include "kh_common.h"
 #include "kh_quant_math.h"
+#include "kh_act.h"
 
 #pragma clang fp contract(off)
 
@@ -40,37 +41,78 @@ struct Epilogue {
     int32_t* acc;
     int sa_per_row;
     int sb_per_col;
+    int act;                // kActNone or kActGelu, applied after the bias
+    const float* residual;  // [M, N]: out = residual + y (the graph's x.add(linear(..)))
 };
+
+constexpr int kActNone = 0;
+constexpr int kActGelu = 1;
+
+// The fp32 output of one accumulator (see the file comment), then the fused
+// activation and residual add in the order the unfused graph applies them.
+__device__ __forceinline__ float epilogue_value(const Epilogue& ep, int64_t i, int64_t j, int64_t N, int32_t acc,
+                                                double s, float bj) {
+    float y = (float)((double)acc * s);
+    if (ep.bias) y = y + bj;
+    if (ep.act == kActGelu) y = kh::gelu_exact(y);
+    if (ep.residual) y = ep.residual[i * N + j] + y;
+    return y;
+}
 
 // One output element of the epilogue (see the file comment).
 __device__ __forceinline__ void epilogue_store(const Epilogue& ep, int64_t i, int64_t j, int64_t N, int32_t acc) {
     if (ep.acc) ep.acc[i * N + j] = acc;
     if (ep.out) {
         const double s = ep.sa[ep.sa_per_row ? i : 0] * ep.sb[ep.sb_per_col ? j : 0];
-        float y = (float)((double)acc * s);
-        if (ep.bias) y = y + ep.bias[j];
-        ep.out[i * N + j] = y;
+        ep.out[i * N + j] = epilogue_value(ep, i, j, N, acc, s, ep.bias ? ep.bias[j] : 0.0f);
     }
 }
 
 // Stores one 32x32 MFMA result block (register r of lane l holds row
 // 8*(r/4) + 4*(l/32) + r%4, column l%32, relative to (i0, j)).  The column's
-// scale and bias are read once per block.
-__device__ __forceinline__ void store_block32(const Epilogue& ep, int64_t i0, int64_t j, int64_t N, const i32x16& v) {
+// scale and bias are read once per block.  Returns the largest |out| bits
+// stored (for the absmax partials of a following per-tensor quantize).
+__device__ __forceinline__ unsigned store_block32(const Epilogue& ep, int64_t i0, int64_t j, int64_t N,
+                                                  const i32x16& v) {
     const double sbj = ep.sb ? ep.sb[ep.sb_per_col ? j : 0] : 0.0;
     const float bj = ep.bias ? ep.bias[j] : 0.0f;
     const double sa0 = (ep.sa && !ep.sa_per_row) ? ep.sa[0] * sbj : 0.0;
+    unsigned mx = 0;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const int64_t i = i0 + 8 * (r >> 2) + (r & 3);
         if (ep.acc) ep.acc[i * N + j] = v[r];
         if (ep.out) {
             const double s = ep.sa_per_row ? ep.sa[i] * sbj : sa0;
-            float y = (float)((double)v[r] * s);
-            if (ep.bias) y = y + bj;
+            const float y = epilogue_value(ep, i, j, N, v[r], s, bj);
             ep.out[i * N + j] = y;
+            mx = max(mx, kh::abs_bits32(y));
         }
     }
+    return mx;
+}
+
+// store_block32 for a block that may extend past row M or column N.
+__device__ __forceinline__ unsigned store_block32_masked(const Epilogue& ep, int64_t i0, int64_t j, int64_t M,
+                                                         int64_t N, const i32x16& v) {
+    if (j >= N) return 0;
+    const double sbj = ep.sb ? ep.sb[ep.sb_per_col ? j : 0] : 0.0;
+    const float bj = ep.bias ? ep.bias[j] : 0.0f;
+    const double sa0 = (ep.sa && !ep.sa_per_row) ? ep.sa[0] * sbj : 0.0;
+    unsigned mx = 0;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int64_t i = i0 + 8 * (r >> 2) + (r & 3);
+        if (i >= M) continue;
+        if (ep.acc) ep.acc[i * N + j] = v[r];
+        if (ep.out) {
+            const double s = ep.sa_per_row ? ep.sa[i] * sbj : sa0;
+            const float y = epilogue_value(ep, i, j, N, v[r], s, bj);
+            ep.out[i * N + j] = y;
+            mx = max(mx, kh::abs_bits32(y));
+        }
+    }
+    return mx;
 }
 
 template <int BM, int BN, int BK, int WM, int WN>
@@ -285,11 +327,12 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, void* dst, i
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, soff, 0, 0);
 }
 
-template <int NS>
+template <int BM, int BN, int NS>
 __global__ __launch_bounds__(512) void gemm_i8_pingpong_kernel(const int8_t* __restrict__ A,
                                                                const int8_t* __restrict__ B, int M, int N, int K,
-                                                               int group_m, Epilogue ep) {
-    constexpr int BM = 256, BN = 256, BK = 64, WM = 2, WN = 4, kWaves = WM * WN;
+                                                               int group_m, Epilogue ep, unsigned* parts) {
+    constexpr int BK = 64, WM = 2, WN = 4, kWaves = WM * WN;
+    static_assert((BM == 128 || BM == 256) && (BN == 128 || BN == 256), "tile");
     constexpr int kWaveM = BM / WM, kWaveN = BN / WN;
     constexpr int kTM = kWaveM / 32, kTN = kWaveN / 32;
     constexpr int kLdsA = BM * BK, kStage = (BM + BN) * BK;
@@ -299,15 +342,18 @@ __global__ __launch_bounds__(512) void gemm_i8_pingpong_kernel(const int8_t* __r
     static_assert(NS >= 3 && NS <= 5, "wait_loads_beyond covers up to 3 stages ahead");
     __shared__ __attribute__((aligned(1024))) int8_t lds[NS * kStage];
 
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     int tm, tn;
-    tile_of(blockIdx.x, M / BM, N / BN, group_m, tm, tn);
+    tile_of(blockIdx.x, tiles_m, tiles_n, group_m, tm, tn);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;
     const int group = wm;  // waves 0-3 and 4-7: one of each per SIMD
 
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(A + (int64_t)tm * BM * K, (uint32_t)BM * (uint32_t)K);
-    const __amdgpu_buffer_rsrc_t rb = make_rsrc(B + (int64_t)tn * BN * K, (uint32_t)BN * (uint32_t)K);
+    // Rows past M (N) lie outside the resource: their loads return zeros.
+    const int rows_a = min(BM, M - tm * BM), rows_b = min(BN, N - tn * BN);
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(A + (int64_t)tm * BM * K, (uint32_t)rows_a * (uint32_t)K);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(B + (int64_t)tn * BN * K, (uint32_t)rows_b * (uint32_t)K);
     auto swz = [](int r) { return (r >> 2) & 3; };
 
     // LDS-DMA sources: instruction i of this wave fills rows
@@ -399,13 +445,37 @@ __global__ __launch_bounds__(512) void gemm_i8_pingpong_kernel(const int8_t* __r
 
     const int64_t row_base = (int64_t)tm * BM + wm * kWaveM + 4 * fh;
     const int64_t col_base = (int64_t)tn * BN + wn * kWaveN + fr;
+    unsigned mx = 0;
+    if (rows_a == BM && rows_b == BN) {
 #pragma unroll
-    for (int a = 0; a < kTM; ++a)
+        for (int a = 0; a < kTM; ++a)
 #pragma unroll
-        for (int b = 0; b < kTN; ++b) {
-            store_block32(ep, row_base + a * 32, col_base + b * 32, N, acc[a][b]);
-            __builtin_amdgcn_sched_barrier(0);
+            for (int b = 0; b < kTN; ++b) {
+                mx = max(mx, store_block32(ep, row_base + a * 32, col_base + b * 32, N, acc[a][b]));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+    } else {
+#pragma unroll
+        for (int a = 0; a < kTM; ++a)
+#pragma unroll
+            for (int b = 0; b < kTN; ++b) {
+                mx = max(mx, store_block32_masked(ep, row_base + a * 32, col_base + b * 32, M, N, acc[a][b]));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+    }
+    if (parts) {
+        // Per-workgroup max |out| bits, for a following per-tensor quantize.
+        unsigned* wmax = reinterpret_cast<unsigned*>(lds);  // every stage's last reader passed the final barrier
+        mx = kh::quant::wave_max(mx);
+        if (lane == 0) wmax[wave] = mx;
+        __syncthreads();
+        if (tid == 0) {
+            unsigned m = wmax[0];
+#pragma unroll
+            for (int w = 1; w < kWaves; ++w) m = max(m, wmax[w]);
+            parts[blockIdx.x] = m;
         }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -473,12 +543,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_i8_skinny_kernel(const
             const int64_t i = t * 16 + 4 * (lane >> 4) + r;
             if (i >= M) continue;
             if (ep.acc) ep.acc[i * N + j] = sum[r];
-            if (ep.out) {
-                const double s = ep.sa[ep.sa_per_row ? i : 0] * sbj;
-                float y = (float)((double)sum[r] * s);
-                if (ep.bias) y = y + bj;
-                ep.out[i * N + j] = y;
-            }
+            if (ep.out) ep.out[i * N + j] = epilogue_value(ep, i, j, N, sum[r], ep.sa[ep.sa_per_row ? i : 0] * sbj, bj);
         }
     }
 }
@@ -498,17 +563,35 @@ int launch_skinny(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, in
     return kh::launch_status("gemm_i8_skinny");
 }
 
-int launch_pingpong(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
-                    const Epilogue& ep) {
-    const unsigned tiles = (unsigned)((M / 256) * (N / 256));
-    gemm_i8_pingpong_kernel<4><<<tiles, 512, 0, d->stream>>>(A, B, (int)M, (int)N, (int)K, 8, ep);
+template <int BM, int BN, int NS>
+int launch_pingpong_cfg(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
+                        const Epilogue& ep, unsigned* parts, int* nparts) {
+    const unsigned tiles = (unsigned)(((M + BM - 1) / BM) * ((N + BN - 1) / BN));
+    gemm_i8_pingpong_kernel<BM, BN, NS><<<tiles, 512, 0, d->stream>>>(A, B, (int)M, (int)N, (int)K, 8, ep, parts);
+    if (nparts) *nparts = (int)tiles;
     return kh::launch_status("gemm_i8_pingpong");
 }
 
-// True when the full-tile kernel applies to this shape.
+// The largest tile that still gives the chip at least 1.5 tiles per CU;
+// the smallest tile otherwise.  Short K gets a 3-stage ring.
+int launch_pingpong(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
+                    const Epilogue& ep, unsigned* parts = nullptr, int* nparts = nullptr) {
+    auto tiles = [&](int64_t bm, int64_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+    const int64_t want = (int64_t)d->cus * 3 / 2;
+    if (tiles(256, 256) >= want) {
+        if (K >= 1024) return launch_pingpong_cfg<256, 256, 4>(d, A, B, M, N, K, ep, parts, nparts);
+        return launch_pingpong_cfg<256, 256, 3>(d, A, B, M, N, K, ep, parts, nparts);
+    }
+    if (tiles(256, 128) >= want) return launch_pingpong_cfg<256, 128, 3>(d, A, B, M, N, K, ep, parts, nparts);
+    return launch_pingpong_cfg<128, 128, 3>(d, A, B, M, N, K, ep, parts, nparts);
+}
+
+// True when the ping-pong kernel applies to this shape (any M and N; K a
+// multiple of 64; 16-byte aligned operands; 32-bit offsets).
 bool pingpong_fits(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K) {
-    return M % 256 == 0 && N % 256 == 0 && K % 64 == 0 && K > 0 && kh::aligned(A, 16) && kh::aligned(B, 16) &&
-           256 * K <= 0x7FFFFFFFLL && M <= 0x7FFFFFFF && N <= 0x7FFFFFFF && (M / 256) * (N / 256) <= 0x7FFFFFFF;
+    return M > 0 && N > 0 && K % 64 == 0 && K > 0 && kh::aligned(A, 16) && kh::aligned(B, 16) &&
+           256 * K <= 0x7FFFFFFFLL && M <= 0x7FFFFFFF && N <= 0x7FFFFFFF &&
+           ((M + 127) / 128) * ((N + 127) / 128) <= 0x7FFFFFFF;
 }
 
 template <int BM, int BN, int BK, int WM, int WN>
@@ -677,23 +760,55 @@ bool decode_fits(const float* x, int64_t M, int64_t K, const int8_t* B, int64_t 
 
 extern "C" {
 
-int kh_gemm_i8(const int8_t* a, const int8_t* b_packed, int64_t M, int64_t N, int64_t K, const double* sa,
-               int sa_per_row, const double* sb, int sb_per_col, const float* bias, float* out, int32_t* acc_out) {
+static int gemm_i8_impl(const int8_t* a, const int8_t* b_packed, int64_t M, int64_t N, int64_t K, const double* sa,
+                        int sa_per_row, const double* sb, int sb_per_col, const float* bias, float* out,
+                        int32_t* acc_out, int act, const float* residual, unsigned* parts, int max_parts,
+                        int* nparts) {
     KH_REQUIRE(M >= 0 && N >= 0 && K >= 0, "kh_gemm_i8: negative shape");
     KH_REQUIRE(out || acc_out, "kh_gemm_i8: neither out nor acc_out given");
     KH_REQUIRE(K <= 133144, "kh_gemm_i8: K > 133144 could overflow the int32 accumulator");
     KH_REQUIRE(M <= 0xFFFFLL * 128 && N <= 0x7FFFFFFFLL, "kh_gemm_i8: shape too large");
+    KH_REQUIRE(act == kActNone || act == kActGelu, "kh_gemm_i8_ex: unknown activation");
+    KH_REQUIRE(!(act || residual || parts) || out, "kh_gemm_i8_ex: activation, residual and partials need out");
+    KH_REQUIRE(!parts || (nparts && max_parts > 0), "kh_gemm_i8_ex: partials need max_parts > 0 and nparts");
+    if (nparts) *nparts = 0;
     if (M == 0 || N == 0) return KH_OK;
     KH_REQUIRE(K == 0 || (a && b_packed), "kh_gemm_i8: null operand");
     KH_REQUIRE(!out || (sa && sb), "kh_gemm_i8: scales required when out is given");
     KH_DEVICE_OR_RETURN(d);
-    Epilogue ep{sa, sb, bias, out, acc_out, sa_per_row, sb_per_col};
-    if (skinny_fits(a, b_packed, M, N, K)) return launch_skinny(d, a, b_packed, M, N, K, ep);
-    if (pingpong_fits(a, b_packed, M, N, K)) return launch_pingpong(d, a, b_packed, M, N, K, ep);
-    const bool vec16 = (K % 16 == 0) && kh::aligned(a, 16) && kh::aligned(b_packed, 16);
-    if (M >= 2048 && N >= 2048)
-        return launch_gemm<256, 256, 64, 2, 4>(d, a, b_packed, M, N, K, ep, vec16);
-    return launch_gemm<128, 128, 64, 2, 2>(d, a, b_packed, M, N, K, ep, vec16);
+    Epilogue ep{sa, sb, bias, out, acc_out, sa_per_row, sb_per_col, act, residual};
+    int rc;
+    bool parts_done = false;
+    if (skinny_fits(a, b_packed, M, N, K)) {
+        rc = launch_skinny(d, a, b_packed, M, N, K, ep);
+    } else if (pingpong_fits(a, b_packed, M, N, K)) {
+        // The ping-pong kernel writes one partial per workgroup when they fit.
+        const int64_t worst = ((M + 127) / 128) * ((N + 127) / 128);
+        const bool fused = parts && worst <= max_parts;
+        rc = launch_pingpong(d, a, b_packed, M, N, K, ep, fused ? parts : nullptr, fused ? nparts : nullptr);
+        parts_done = fused;
+    } else {
+        const bool vec16 = (K % 16 == 0) && kh::aligned(a, 16) && kh::aligned(b_packed, 16);
+        if (M >= 2048 && N >= 2048)
+            rc = launch_gemm<256, 256, 64, 2, 4>(d, a, b_packed, M, N, K, ep, vec16);
+        else
+            rc = launch_gemm<128, 128, 64, 2, 2>(d, a, b_packed, M, N, K, ep, vec16);
+    }
+    if (rc || !parts || parts_done) return rc;
+    return kh_absmax_parts(out, M * N, parts, max_parts, nparts);
+}
+
+int kh_gemm_i8(const int8_t* a, const int8_t* b_packed, int64_t M, int64_t N, int64_t K, const double* sa,
+               int sa_per_row, const double* sb, int sb_per_col, const float* bias, float* out, int32_t* acc_out) {
+    return gemm_i8_impl(a, b_packed, M, N, K, sa, sa_per_row, sb, sb_per_col, bias, out, acc_out, kActNone,
+                        nullptr, nullptr, 0, nullptr);
+}
+
+int kh_gemm_i8_ex(const int8_t* a, const int8_t* b_packed, int64_t M, int64_t N, int64_t K, const double* sa,
+                  int sa_per_row, const double* sb, int sb_per_col, const float* bias, int act, const float* residual,
+                  float* out, unsigned* absmax_parts, int max_parts, int* nparts) {
+    return gemm_i8_impl(a, b_packed, M, N, K, sa, sa_per_row, sb, sb_per_col, bias, out, nullptr, act, residual,
+                        absmax_parts, max_parts, nparts);
 }
 
 int kh_linear_i8(const float* x, int64_t M, int64_t K, const int8_t* b_packed, int64_t N, const double* sb,

@@ -440,6 +440,40 @@ int kh_quantize_tensor(const float* x, int64_t n, int8_t* q, double* scale) {
     return kh::launch_status("quant_tensor");
 }
 
+int kh_absmax_parts(const float* x, int64_t n, unsigned* parts, int max_parts, int* nparts) {
+    KH_REQUIRE(n >= 0 && max_parts > 0 && parts && nparts, "kh_absmax_parts: bad arguments");
+    KH_REQUIRE(n == 0 || x, "kh_absmax_parts: null pointer");
+    KH_DEVICE_OR_RETURN(d);
+    if (n == 0) {
+        fill_u32_kernel<<<1, 256, 0, d->stream>>>(parts, 1, 0u);
+        *nparts = 1;
+        return kh::launch_status("fill_u32");
+    }
+    const bool vec = kh::aligned(x, 16);
+    const int g = grid_for(vec ? (n >> 2) : n, 8, std::min(max_parts, kMaxPartials));
+    if (vec)
+        absmax_partials_kernel<true><<<g, 256, 0, d->stream>>>(x, n, parts);
+    else
+        absmax_partials_kernel<false><<<g, 256, 0, d->stream>>>(x, n, parts);
+    *nparts = g;
+    return kh::launch_status("absmax_partials");
+}
+
+int kh_quantize_tensor_parts(const float* x, int64_t n, const unsigned* parts, int nparts, int8_t* q, double* scale) {
+    KH_REQUIRE(n >= 0, "kh_quantize_tensor_parts: negative size");
+    KH_REQUIRE(scale && parts && nparts > 0, "kh_quantize_tensor_parts: bad partials or scale");
+    KH_REQUIRE(n == 0 || (x && q), "kh_quantize_tensor_parts: null pointer");
+    KH_DEVICE_OR_RETURN(d);
+    if (n == 0) return fill_scales_one(d, scale, 1);
+    const bool vec = kh::aligned(x, 16) && kh::aligned(q, 4);
+    const int g = grid_for(vec ? (n >> 2) : n, 8, 8192);
+    if (vec)
+        quant_tensor_kernel<true><<<g, 256, 0, d->stream>>>(x, n, q, scale, parts, nparts, d->fault);
+    else
+        quant_tensor_kernel<false><<<g, 256, 0, d->stream>>>(x, n, q, scale, parts, nparts, d->fault);
+    return kh::launch_status("quant_tensor");
+}
+
 int kh_quantize_rows(const float* x, int64_t rows, int64_t cols, int8_t* q, double* scales) {
     KH_REQUIRE(rows >= 0 && cols >= 0, "kh_quantize_rows: negative shape");
     if (rows == 0) return KH_OK;

@@ -19,6 +19,7 @@
 #include <hip/hip_runtime.h>
 
 #include "kh_common.h"
+#include "kh_act.h"
 
 namespace {
 
@@ -53,12 +54,19 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 constexpr int kLnMaxPerLane = 16;
 
-__global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict__ x, int64_t rows, int D,
-                                                        const float* __restrict__ w, const float* __restrict__ b,
-                                                        float eps, float* __restrict__ out) {
-    const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= rows) return;
+// Max over a 256-thread workgroup (4 waves); every thread gets the result.
+__device__ __forceinline__ unsigned block4_max(unsigned v, unsigned* wmax) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = max(v, (unsigned)__shfl_xor((int)v, off, 64));
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
+}
+
+// One row of LayerNorm by one wave; returns this lane's largest |out| bits.
+__device__ __forceinline__ unsigned layernorm_row(const float* __restrict__ x, int64_t row, int D,
+                                                       const float* __restrict__ w, const float* __restrict__ b,
+                                                       float eps, float* __restrict__ out, int lane) {
     const float* xr = x + row * D;
     float v[kLnMaxPerLane];
     float s = 0.0f;
@@ -80,24 +88,42 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict_
     const float var = wave_sum(ss) / (float)D;
     const float denom = sqrtf(var + eps);
     float* orow = out + row * D;
+    unsigned mx = 0;
 #pragma unroll
     for (int i = 0; i < kLnMaxPerLane; ++i) {
         const int c = lane + i * 64;
-        if (c < D) orow[c] = v[i] / denom * w[c] + b[c];
+        if (c < D) {
+            const float y = v[i] / denom * w[c] + b[c];
+            orow[c] = y;
+            mx = max(mx, kh::abs_bits32(y));
+        }
+    }
+    return mx;
+}
+
+__global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict__ x, int64_t rows, int D,
+                                                        const float* __restrict__ w, const float* __restrict__ b,
+                                                        float eps, float* __restrict__ out,
+                                                        unsigned* __restrict__ parts) {
+    __shared__ unsigned wmax[4];
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    unsigned mx = 0;
+    if (row < rows) mx = layernorm_row(x, row, D, w, b, eps, out, lane);
+    if (parts) {
+        // Per-workgroup max |out| bits, for a following per-tensor quantize.
+        mx = block4_max(mx, wmax);
+        if (threadIdx.x == 0) parts[blockIdx.x] = mx;
     }
 }
+
 
 // ---------------------------------------------------------------------------
 // GELU (exact erf).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void gelu_kernel(const float* __restrict__ x, float* __restrict__ out, int64_t n) {
-    const float kInvSqrt2 = 0.70710678118654752440f;
     const int64_t stride = (int64_t)gridDim.x * 256;
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) {
-        const float xi = x[i];
-        const float cdf = 0.5f * (1.0f + erff(xi * kInvSqrt2));
-        out[i] = xi * cdf;
-    }
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) out[i] = kh::gelu_exact(x[i]);
 }
 
 // ---------------------------------------------------------------------------
@@ -141,7 +167,7 @@ __device__ __forceinline__ float group16_sum(float v) {
 }
 
 __global__ __launch_bounds__(256) void attention_mfma_kernel(const float* __restrict__ qkv, int B, int T, int H,
-                                                             float* __restrict__ out) {
+                                                             float* __restrict__ out, unsigned* __restrict__ parts) {
     __shared__ __attribute__((aligned(16))) float ks[kAttK][kAttPad];
     __shared__ __attribute__((aligned(16))) float vt[kDk][kAttPad];
     __shared__ __attribute__((aligned(16))) float ps[4][16][kAttPad];
@@ -263,6 +289,7 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(const float* __rest
             }
         }
     }
+    unsigned mx = 0;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int q = q0 + 4 * g + r;
@@ -270,7 +297,17 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(const float* __rest
         const float inv = 1.0f / l[r];
         float* orow = out + (row0 + q) * D + h * kDk;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) orow[16 * j + li] = o[j][r] * inv;
+        for (int j = 0; j < 4; ++j) {
+            const float y = o[j][r] * inv;
+            orow[16 * j + li] = y;
+            mx = max(mx, kh::abs_bits32(y));
+        }
+    }
+    if (parts) {
+        // Per-workgroup max |out| bits, for a following per-tensor quantize.
+        __shared__ unsigned wmax[4];
+        mx = block4_max(mx, wmax);
+        if (tid == 0) parts[((int64_t)b * gridDim.y + h) * gridDim.x + qb] = mx;
     }
 }
 
@@ -289,14 +326,30 @@ int kh_embedding(const int32_t* ids, int64_t rows, int T, const float* tok, int 
     return kh::launch_status("embedding");
 }
 
-int kh_layernorm(const float* x, int64_t rows, int D, const float* weight, const float* bias, float eps, float* out) {
+int kh_layernorm_ex(const float* x, int64_t rows, int D, const float* weight, const float* bias, float eps, float* out,
+                    unsigned* absmax_parts, int max_parts, int* nparts) {
     KH_REQUIRE(rows >= 0 && D > 0, "kh_layernorm: bad shape");
     KH_REQUIRE(D <= 64 * kLnMaxPerLane, "kh_layernorm: rows longer than 1024 are not supported");
+    KH_REQUIRE(!absmax_parts || (max_parts > 0 && nparts), "kh_layernorm_ex: partials need max_parts and nparts");
+    if (nparts) *nparts = 0;
     if (rows == 0) return KH_OK;
     KH_REQUIRE(x && weight && bias && out, "kh_layernorm: null pointer");
     KH_DEVICE_OR_RETURN(d);
-    layernorm_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, d->stream>>>(x, rows, D, weight, bias, eps, out);
-    return kh::launch_status("layernorm");
+    const int64_t blocks = (rows + 3) / 4;
+    const bool fused = absmax_parts && blocks <= max_parts;
+    layernorm_kernel<<<(unsigned)blocks, 256, 0, d->stream>>>(x, rows, D, weight, bias, eps, out,
+                                                              fused ? absmax_parts : nullptr);
+    int rc = kh::launch_status("layernorm");
+    if (rc || !absmax_parts) return rc;
+    if (fused) {
+        *nparts = (int)blocks;
+        return KH_OK;
+    }
+    return kh_absmax_parts(out, rows * D, absmax_parts, max_parts, nparts);
+}
+
+int kh_layernorm(const float* x, int64_t rows, int D, const float* weight, const float* bias, float eps, float* out) {
+    return kh_layernorm_ex(x, rows, D, weight, bias, eps, out, nullptr, 0, nullptr);
 }
 
 int kh_gelu(const float* x, float* out, int64_t n) {
@@ -310,19 +363,34 @@ int kh_gelu(const float* x, float* out, int64_t n) {
     return kh::launch_status("gelu");
 }
 
-int kh_causal_attention(const float* qkv, int B, int T, int H, int dk, float* out) {
+int kh_causal_attention_ex(const float* qkv, int B, int T, int H, int dk, float* out, unsigned* absmax_parts,
+                           int max_parts, int* nparts) {
     KH_REQUIRE(B > 0 && T > 0 && H > 0, "kh_causal_attention: bad shape");
     KH_REQUIRE(dk == kDk, "kh_causal_attention: only head dimension 64 is supported");
     KH_REQUIRE(B <= 65535 && H <= 65535, "kh_causal_attention: too many batches or heads");
     KH_REQUIRE(qkv && out, "kh_causal_attention: null pointer");
+    KH_REQUIRE(!absmax_parts || (max_parts > 0 && nparts), "kh_causal_attention_ex: partials need max_parts and nparts");
+    if (nparts) *nparts = 0;
     KH_DEVICE_OR_RETURN(d);
     KH_REQUIRE(kh::aligned(qkv, 16) && kh::aligned(out, 16), "kh_causal_attention: 16-byte aligned buffers required");
     dim3 grid((unsigned)((T + kAttQ - 1) / kAttQ), (unsigned)H, (unsigned)B);
+    const int64_t blocks = (int64_t)grid.x * grid.y * grid.z;
+    const bool fused = absmax_parts && blocks <= max_parts;
     // 1/sqrt(d_k) = 1/8 for dk = 64 (the reference's binary64 Python float,
     // nn.py:413, is exactly representable in binary32); the kernel applies it
     // to Q.
-    attention_mfma_kernel<<<grid, 256, 0, d->stream>>>(qkv, B, T, H, out);
-    return kh::launch_status("attention");
+    attention_mfma_kernel<<<grid, 256, 0, d->stream>>>(qkv, B, T, H, out, fused ? absmax_parts : nullptr);
+    int rc = kh::launch_status("attention");
+    if (rc || !absmax_parts) return rc;
+    if (fused) {
+        *nparts = (int)blocks;
+        return KH_OK;
+    }
+    return kh_absmax_parts(out, (int64_t)B * T * H * kDk, absmax_parts, max_parts, nparts);
+}
+
+int kh_causal_attention(const float* qkv, int B, int T, int H, int dk, float* out) {
+    return kh_causal_attention_ex(qkv, B, T, H, dk, out, nullptr, 0, nullptr);
 }
 
 }  // extern "C"

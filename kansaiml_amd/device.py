@@ -33,7 +33,9 @@ def _dtype_name(dt) -> str:
 class DeviceTensor:
     """A contiguous device buffer with a shape and a KIR dtype string."""
 
-    __slots__ = ("ptr", "shape", "dtype", "nbytes", "_owned", "__weakref__")
+    # absmax_parts: the per-tensor absmax partials the producing kernel wrote
+    # alongside this tensor, when a fused graph asked for them (kir.py).
+    __slots__ = ("ptr", "shape", "dtype", "nbytes", "_owned", "absmax_parts", "__weakref__")
 
     def __init__(self, shape, dtype: str = "float32"):
         if dtype not in DTYPES:
@@ -47,6 +49,7 @@ class DeviceTensor:
         N.call("kh_alloc", max(self.nbytes, 1), ctypes.byref(p))
         self.ptr = p
         self._owned = True
+        self.absmax_parts = None
 
     # -- construction -----------------------------------------------------
     @classmethod

@@ -9,6 +9,8 @@ waits unless a result is downloaded or synchronize() is called.
 
 from __future__ import annotations
 
+import ctypes
+
 from . import _native as N
 from .device import DeviceTensor
 
@@ -219,3 +221,92 @@ def relu(x: DeviceTensor) -> DeviceTensor:
     out = DeviceTensor(x.shape, "float32")
     N.call("kh_relu", x.ptr, out.ptr, x.numel())
     return out
+
+
+# ---------------------------------------------------------------------------
+# Fused producers of a per-tensor quantize: the absmax pass rides along
+# ---------------------------------------------------------------------------
+
+ABSMAX_PARTS = 8192  # partial maxima a fused producer may write
+
+
+class AbsmaxParts:
+    """Per-workgroup maxima of |x| (IEEE bit patterns in an int32 buffer) that
+    a producer kernel wrote alongside x, for quantize_tensor_parts."""
+
+    def __init__(self):
+        self.buf = DeviceTensor([ABSMAX_PARTS], "int32")
+        self._n = ctypes.c_int(0)
+
+    @property
+    def count(self) -> int:
+        return self._n.value
+
+    def release(self):
+        self.buf.release()
+
+
+ACTS = {None: 0, "gelu": 1}
+
+
+def gemm_i8_fused(a: DeviceTensor, b_packed: DeviceTensor, sa: DeviceTensor, sb: DeviceTensor,
+                  bias: DeviceTensor | None = None, *, act: str | None = None,
+                  residual: DeviceTensor | None = None, absmax: bool = False):
+    """gemm_i8's fp32 output with the following elementwise steps fused into
+    its epilogue (bias, then act, then residual + y) and optionally the
+    absmax partials of the result.  Returns (out, AbsmaxParts | None)."""
+    _need(a, "int8", 2, "gemm_i8(a)")
+    _need(b_packed, "int8", 2, "gemm_i8(b)")
+    M, K = a.shape
+    Nn, K2 = b_packed.shape
+    if K != K2:
+        raise RuntimeError(f"gemm_i8: incompatible shapes {a.shape} x {b_packed.shape}^T")
+    if act not in ACTS:
+        raise ValueError(f"gemm_i8_fused: unknown activation {act!r}")
+    sa_mode = _scale_mode(sa, M, "gemm_i8(sa)")
+    sb_mode = _scale_mode(sb, Nn, "gemm_i8(sb)")
+    if bias is not None:
+        _need(bias, "float32", 1, "gemm_i8(bias)")
+        if bias.shape[0] != Nn:
+            raise RuntimeError("gemm_i8: bias must have N entries")
+    if residual is not None:
+        _need(residual, "float32", 2, "gemm_i8(residual)")
+        if list(residual.shape) != [M, Nn]:
+            raise RuntimeError("gemm_i8_fused: residual must be [M, N]")
+    out = DeviceTensor([M, Nn], "float32")
+    parts = AbsmaxParts() if absmax else None
+    N.call("kh_gemm_i8_ex", a.ptr, b_packed.ptr, M, Nn, K, sa.ptr, sa_mode, sb.ptr, sb_mode, _opt(bias), ACTS[act],
+           _opt(residual), out.ptr, parts.buf.ptr if parts else None, ABSMAX_PARTS if parts else 0,
+           ctypes.byref(parts._n) if parts else None)
+    return out, parts
+
+
+def layer_norm(x: DeviceTensor, w: DeviceTensor, b: DeviceTensor, eps: float = 1e-5, *, absmax: bool = False):
+    """LayerNorm over the last axis (nn.py:308-331).  Returns (out, AbsmaxParts | None)."""
+    _need(x, "float32", 2, "layer_norm(x)")
+    out = DeviceTensor(x.shape, "float32")
+    parts = AbsmaxParts() if absmax else None
+    N.call("kh_layernorm_ex", x.ptr, x.shape[0], x.shape[1], w.ptr, b.ptr, eps, out.ptr,
+           parts.buf.ptr if parts else None, ABSMAX_PARTS if parts else 0, ctypes.byref(parts._n) if parts else None)
+    return out, parts
+
+
+def causal_attention(qkv: DeviceTensor, batch: int, seq: int, heads: int, d_model: int, *, absmax: bool = False):
+    """Causal multi-head attention core (nn.py:381-427).  Returns (out, AbsmaxParts | None)."""
+    _need(qkv, "float32", 2, "causal_attention(qkv)")
+    out = DeviceTensor([batch * seq, d_model], "float32")
+    parts = AbsmaxParts() if absmax else None
+    N.call("kh_causal_attention_ex", qkv.ptr, batch, seq, heads, d_model // heads, out.ptr,
+           parts.buf.ptr if parts else None, ABSMAX_PARTS if parts else 0, ctypes.byref(parts._n) if parts else None)
+    return out, parts
+
+
+def quantize_tensor_parts(x: DeviceTensor, parts: AbsmaxParts):
+    """quantize_tensor with the absmax partials its producer wrote."""
+    _need(x, "float32", None, "quantize_tensor(x)")
+    if parts.count <= 0:
+        raise RuntimeError("quantize_tensor_parts: the producer wrote no partials")
+    q = DeviceTensor(x.shape, "int8")
+    s = DeviceTensor([1], "float64")
+    N.call("kh_quantize_tensor_parts", x.ptr, x.numel(), parts.buf.ptr, parts.count, q.ptr, s.ptr)
+    return q, s

@@ -227,9 +227,15 @@ def _is_bias(graph, by_id, x_id, b_id) -> bool:
 
 def quant_fusion(graph) -> Graph:
     """Fuses, where the intermediate has no other user:
-      int8_matmul -> dequantize [-> add(bias)]  =>  int8_linear
+      int8_matmul -> dequantize [-> add(bias)] [-> gelu] [-> add(x, .)]
+                                                 =>  int8_linear
       matmul -> add(bias)                        =>  matmul_bias
       add(bias) -> relu                          =>  fused_bias_relu
+    int8_linear's attrs record what it absorbed: bias (bool), act ("gelu" or
+    None) and residual (bool; the residual operand comes last).  Then every
+    int8_linear, layer_norm or causal_attention whose output feeds a
+    per-tensor quantize is marked absmax=True: its kernel writes the absmax
+    partials that quantize needs, so the quantize reads its input once.
     The fused node takes the place of the last node of its pattern (every
     operand, e.g. a bias constant traced after the matmul, precedes it).
     Returns a new Graph; node order is preserved, ids are renumbered."""
@@ -240,8 +246,8 @@ def quant_fusion(graph) -> Graph:
         u = users[nid]
         return u[0] if len(u) == 1 and nid != graph.output else None
 
-    # Phase 1: find patterns.  fused[last] = (op, [operand ids]); absorbed
-    # nodes are dropped.
+    # Phase 1: find patterns.  fused[last] = (op, [operand ids], attrs);
+    # absorbed nodes are dropped.
     fused, absorbed = {}, set()
     for n in graph.nodes:
         if n.id in absorbed:
@@ -249,14 +255,30 @@ def quant_fusion(graph) -> Graph:
         if n.op == "int8_matmul":
             dq = only_user(n.id)
             if dq is not None and by_id[dq].op == "dequantize":
-                last, ins = dq, list(n.inputs)
-                ad = only_user(dq)
-                if ad is not None and by_id[ad].op == "add":
-                    a_in = by_id[ad].inputs
+                chain, ins, attrs = [n.id, dq], list(n.inputs), {"bias": False, "act": None, "residual": False}
+                nxt = only_user(dq)
+                if nxt is not None and by_id[nxt].op == "add":
+                    a_in = by_id[nxt].inputs
                     if a_in[0] == dq and _is_bias(graph, by_id, dq, a_in[1]):
-                        last, ins = ad, ins + [a_in[1]]
-                absorbed.update({n.id, dq, last} - {last})
-                fused[last] = ("int8_linear", ins)
+                        chain.append(nxt)
+                        ins.append(a_in[1])
+                        attrs["bias"] = True
+                        nxt = only_user(nxt)
+                if nxt is not None and by_id[nxt].op == "gelu":
+                    chain.append(nxt)
+                    attrs["act"] = "gelu"
+                    nxt = only_user(nxt)
+                if nxt is not None and by_id[nxt].op == "add":
+                    a_in = by_id[nxt].inputs
+                    other = a_in[1] if a_in[0] == chain[-1] else a_in[0]
+                    if (len(a_in) == 2 and chain[-1] in a_in and other != chain[-1]
+                            and list(by_id[other].shape) == list(by_id[chain[-1]].shape)):
+                        chain.append(nxt)
+                        ins.append(other)
+                        attrs["residual"] = True
+                last = chain[-1]
+                absorbed.update(set(chain) - {last})
+                fused[last] = ("int8_linear", ins, attrs)
                 continue
         if n.op == "matmul":
             ad = only_user(n.id)
@@ -264,13 +286,13 @@ def quant_fusion(graph) -> Graph:
                 a_in = by_id[ad].inputs
                 if a_in[0] == n.id and _is_bias(graph, by_id, n.id, a_in[1]):
                     absorbed.add(n.id)
-                    fused[ad] = ("matmul_bias", list(n.inputs) + [a_in[1]])
+                    fused[ad] = ("matmul_bias", list(n.inputs) + [a_in[1]], {})
                     continue
         if n.op == "add" and n.id not in fused and len(n.inputs) == 2 and _is_bias(graph, by_id, *n.inputs):
             r = only_user(n.id)
             if r is not None and by_id[r].op == "relu":
                 absorbed.add(n.id)
-                fused[r] = ("fused_bias_relu", list(n.inputs))
+                fused[r] = ("fused_bias_relu", list(n.inputs), {})
 
     # Phase 2: emit in order.
     out, remap = Graph(), {}
@@ -278,14 +300,24 @@ def quant_fusion(graph) -> Graph:
         if n.id in absorbed:
             continue
         if n.id in fused:
-            op, ins = fused[n.id]
-            nid = out.add(op, [remap[i] for i in ins], n.shape, "float32")
+            op, ins, attrs = fused[n.id]
+            nid = out.add(op, [remap[i] for i in ins], n.shape, "float32", **attrs)
         else:
             nid = out.add(n.op, [remap[i] for i in n.inputs], n.shape, n.dtype, **n.attrs)
         remap[n.id] = nid
     out.inputs = [remap[i] for i in graph.inputs]
     out.output = remap[graph.output]
+
+    # Phase 3: producers of a per-tensor quantize write its absmax partials.
+    for n in out.nodes:
+        if n.op == "quantize" and n.attrs.get("granularity", "tensor") == "tensor":
+            src = out.nodes[n.inputs[0]]
+            if src.op in _ABSMAX_PRODUCERS:
+                src.attrs["absmax"] = True
     return out
+
+
+_ABSMAX_PRODUCERS = ("int8_linear", "layer_norm", "causal_attention")
 
 
 # ---------------------------------------------------------------------------
@@ -390,8 +422,17 @@ def _quantize_node(x, node):
     if node.attrs.get("granularity", "tensor") == "row":
         q, s = H.quantize_rows(x)
         return QTensor(q, s, list(x.shape), "row", packed=False)
-    q, s = H.quantize_tensor(x)
+    parts = getattr(x, "absmax_parts", None)
+    q, s = H.quantize_tensor_parts(x, parts) if parts is not None else H.quantize_tensor(x)
     return QTensor(q, s, list(x.shape), "tensor", packed=False)
+
+
+def _with_parts(out, parts):
+    """Attaches the absmax partials a producer wrote to its output tensor
+    (read by the next per-tensor quantize, released with the tensor)."""
+    if parts is not None:
+        out.absmax_parts = parts
+    return out
 
 
 def _int8_operands(qa, qb, what):
@@ -426,7 +467,15 @@ def _exec(node, vals):
         return _Acc(acc, sa, sb)
     if op == "int8_linear":
         a, b, sa, sb = _int8_operands(ins[0], ins[1], "int8_linear")
-        out, _ = H.gemm_i8(a, b, sa, sb, ins[2] if len(ins) > 2 else None)
+        at = node.attrs
+        has_bias = at.get("bias", len(ins) > 2 and not at.get("residual"))
+        bias = ins[2] if has_bias else None
+        residual = ins[-1] if at.get("residual") else None
+        if at.get("act") or residual is not None or at.get("absmax"):
+            out, parts = H.gemm_i8_fused(a, b, sa, sb, bias, act=at.get("act"), residual=residual,
+                                         absmax=bool(at.get("absmax")))
+            return _with_parts(out, parts)
+        out, _ = H.gemm_i8(a, b, sa, sb, bias)
         return out
     if op == "embedding":
         ids, tok, pos = ins
@@ -436,20 +485,16 @@ def _exec(node, vals):
         return out
     if op == "layer_norm":
         x, w, b = ins
-        out = DeviceTensor(x.shape, "float32")
-        N.call("kh_layernorm", x.ptr, x.shape[0], x.shape[1], w.ptr, b.ptr, node.attrs.get("eps", 1e-5), out.ptr)
-        return out
+        out, parts = H.layer_norm(x, w, b, node.attrs.get("eps", 1e-5), absmax=bool(node.attrs.get("absmax")))
+        return _with_parts(out, parts)
     if op == "gelu":
         out = DeviceTensor(ins[0].shape, "float32")
         N.call("kh_gelu", ins[0].ptr, out.ptr, ins[0].numel())
         return out
     if op == "causal_attention":
-        qkv = ins[0]
-        heads = node.attrs["heads"]
-        out = DeviceTensor(node.shape, "float32")
-        N.call("kh_causal_attention", qkv.ptr, node.attrs["batch"], node.attrs["seq"], heads,
-               node.shape[1] // heads, out.ptr)
-        return out
+        out, parts = H.causal_attention(ins[0], node.attrs["batch"], node.attrs["seq"], node.attrs["heads"],
+                                        node.shape[1], absmax=bool(node.attrs.get("absmax")))
+        return _with_parts(out, parts)
     if op == "tuple":
         return tuple(ins)
     raise KeyError(op)
@@ -458,6 +503,9 @@ def _exec(node, vals):
 def _release(v):
     from .quantize import QTensor
     if isinstance(v, DeviceTensor):
+        parts = getattr(v, "absmax_parts", None)
+        if parts is not None:
+            parts.release()
         v.release()
     elif isinstance(v, _Acc):
         v.acc.release()

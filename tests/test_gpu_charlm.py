@@ -109,9 +109,20 @@ def _check_node(node, got, ins):
         assert got[1][0] == s
     elif op == "int8_linear":
         (qa, sa), (qw, sw) = ins[0], ins[1]
-        bias = ins[2] if len(ins) > 2 else None
+        at = node.attrs
+        bias = ins[2] if at.get("bias") else None
         ref = O.ko_epilogue(O.ko_gemm_i8(qa, qw), sa, sw, bias)
-        np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+        if at.get("act") == "gelu":
+            # the fused epilogue applies the GELU kernel's binary32 arithmetic
+            # to the bit-exact linear output
+            x = ref.astype(np.float64)
+            gref = x * 0.5 * (1 + erf(x / np.sqrt(2)))
+            assert np.abs(got - gref).max() < 4e-6 * max(1.0, np.abs(gref).max())
+        elif at.get("residual"):
+            ref = (ins[-1] + ref).astype(np.float32)  # x.add(linear(..)): one fp32 add
+            np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+        else:
+            np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
     elif op == "layer_norm":
         x, w, b = ins
         ref = R.layer_norm(x.astype(np.float64), w, b, node.attrs.get("eps", 1e-5))
@@ -156,7 +167,12 @@ def test_small_model_matches_restatement(G, seq):
         ins = [ids if by_id[i].op == "placeholder" else seen[i][1] for i in node.inputs]
         _check_node(node, got, ins)
         checked.add(node.op)
-    assert checked == {"embedding", "layer_norm", "quantize", "int8_linear", "causal_attention", "add", "gelu"}
+    # GELU and the residual adds are fused into the int8_linear epilogues.
+    assert checked == {"embedding", "layer_norm", "quantize", "int8_linear", "causal_attention"}
+    acts = {(n.attrs.get("act"), bool(n.attrs.get("residual"))) for n in g.nodes if n.op == "int8_linear"}
+    assert acts == {(None, False), ("gelu", False), (None, True)}
+    assert all(n.attrs.get("absmax") for n in g.nodes
+               if n.op in ("layer_norm", "causal_attention") or (n.op == "int8_linear" and n.attrs.get("act")))
     np.testing.assert_array_equal(seen[g.output][1].view(np.uint32), y.view(np.uint32))
     # and the int8 model stays near the fp32 one (quantization error)
     fp = R.forward(w, ids, quantized=False)

@@ -48,6 +48,8 @@ SHAPES = [
     (33, 40, 130), (100, 50, 77), (5, 7, 3),  # K % 16 != 0: byte-gather path
     (2, 100, 512), (17, 4096, 4096), (31, 64, 1024), (16, 16, 512), (5, 11008, 4096), (32, 40, 512),  # skinny
     (512, 768, 64), (768, 512, 192), (1024, 256, 4160),  # full-tile kernel: K % 64 == 0, K % 128 != 0
+    (1000, 1000, 128), (257, 129, 64), (33, 300, 640),    # ping-pong kernel, partial tiles in M and N
+    (16384, 1152, 384), (16384, 384, 1536),               # C4 QKV and fc2 shapes
 ]
 
 
@@ -229,3 +231,82 @@ def test_matmul_f32_c3b_full_size(hip):
     rows = gen.choice(n, size=64, replace=False)
     ref64 = a[rows].astype(np.float64) @ b.astype(np.float64)
     assert (np.abs(got[rows] - ref64) <= _f32_bound(a[rows], b)).all()
+
+
+# ---------------------------------------------------------------------------
+# Fused epilogues (kh_gemm_i8_ex) and absmax partials for per-tensor quantize
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("M,N,K", [(512, 512, 256),      # ping-pong, full tiles
+                                   (300, 1152, 384),     # ping-pong, partial tiles
+                                   (130, 70, 80),        # general kernel (K % 64 != 0)
+                                   (8, 512, 512)])       # skinny kernel
+def test_gemm_i8_fused_epilogues(hip, M, N, K):
+    """GELU and residual epilogues give the same bits as the unfused graph
+    (gemm -> gelu kernel, gemm -> fp32 add), and the absmax partials a fused
+    GEMM writes quantize its output exactly like kh_quantize_tensor."""
+    from kansaiml_amd import _native as Nn
+    H, D = hip
+    gen = np.random.Generator(np.random.PCG64(M + 3 * N + 7 * K))
+    a = gen.integers(-127, 128, (M, K), dtype=np.int8)
+    bt = gen.integers(-127, 128, (N, K), dtype=np.int8)
+    sa, sb = np.array([3e-4]), gen.uniform(1e-4, 1e-3, N)
+    bias = gen.standard_normal(N).astype(np.float32)
+    res = gen.standard_normal((M, N)).astype(np.float32)
+    ad, bd, sad, sbd, biasd = D.from_host(a), D.from_host(bt), D.from_host(sa), D.from_host(sb), D.from_host(bias)
+    plain, _ = H.gemm_i8(ad, bd, sad, sbd, biasd)
+    expect = O.ko_epilogue(O.ko_gemm_i8(a, bt), sa, sb, bias)
+    np.testing.assert_array_equal(bits32(plain.numpy()), bits32(expect))
+
+    g_out, g_parts = H.gemm_i8_fused(ad, bd, sad, sbd, biasd, act="gelu", absmax=True)
+    g_ref = D([M, N])
+    Nn.call("kh_gelu", plain.ptr, g_ref.ptr, M * N)
+    np.testing.assert_array_equal(bits32(g_out.numpy()), bits32(g_ref.numpy()))
+    q1, s1 = H.quantize_tensor_parts(g_out, g_parts)
+    q2, s2 = H.quantize_tensor(g_out)
+    np.testing.assert_array_equal(q1.numpy(), q2.numpy())
+    assert s1.numpy()[0] == s2.numpy()[0]
+
+    r_out, r_parts = H.gemm_i8_fused(ad, bd, sad, sbd, biasd, residual=D.from_host(res), absmax=True)
+    np.testing.assert_array_equal(bits32(r_out.numpy()), bits32((res + expect).astype(np.float32)))
+    q1, s1 = H.quantize_tensor_parts(r_out, r_parts)
+    q2, s2 = H.quantize_tensor(r_out)
+    np.testing.assert_array_equal(q1.numpy(), q2.numpy())
+    assert s1.numpy()[0] == s2.numpy()[0]
+
+
+def test_layernorm_and_attention_absmax_parts(hip):
+    """LayerNorm and attention outputs quantized from the partials their
+    kernels wrote equal kh_quantize_tensor of the same outputs; a partials
+    buffer too small for the grid falls back to a separate absmax pass."""
+    from kansaiml_amd import _native as Nn
+    import ctypes
+    H, D = hip
+    gen = np.random.Generator(np.random.PCG64(41))
+    x = (gen.standard_normal((1000, 384)) * 3).astype(np.float32)
+    w, b = gen.standard_normal(384).astype(np.float32), gen.standard_normal(384).astype(np.float32)
+    out, parts = H.layer_norm(D.from_host(x), D.from_host(w), D.from_host(b), absmax=True)
+    assert parts.count == 250  # one partial per 4-row workgroup
+    q1, s1 = H.quantize_tensor_parts(out, parts)
+    q_ln, s_ln = H.quantize_tensor(out)
+    np.testing.assert_array_equal(q1.numpy(), q_ln.numpy())
+    assert s1.numpy()[0] == s_ln.numpy()[0]
+
+    qkv = (gen.standard_normal((2 * 100, 3 * 128)) * 1.5).astype(np.float32)
+    aout, aparts = H.causal_attention(D.from_host(qkv), 2, 100, 2, 128, absmax=True)
+    q1, s1 = H.quantize_tensor_parts(aout, aparts)
+    q2, s2 = H.quantize_tensor(aout)
+    np.testing.assert_array_equal(q1.numpy(), q2.numpy())
+    assert s1.numpy()[0] == s2.numpy()[0]
+
+    small = D([4], "int32")  # 4 slots < 250 workgroups: separate pass
+    n = ctypes.c_int(0)
+    out2 = D([1000, 384])
+    xd, wd, bd = D.from_host(x), D.from_host(w), D.from_host(b)  # keep the buffers alive across the call
+    Nn.call("kh_layernorm_ex", xd.ptr, 1000, 384, wd.ptr, bd.ptr, 1e-5, out2.ptr, small.ptr, 4, ctypes.byref(n))
+    assert 1 <= n.value <= 4
+    q3 = D([1000, 384], "int8")
+    s3 = D([1], "float64")
+    Nn.call("kh_quantize_tensor_parts", out2.ptr, 1000 * 384, small.ptr, n.value, q3.ptr, s3.ptr)
+    np.testing.assert_array_equal(q3.numpy(), q_ln.numpy())
+    assert s3.numpy()[0] == s_ln.numpy()[0]
