@@ -50,12 +50,17 @@ constexpr int kActGelu = 1;
 
 // The fp32 output of one accumulator (see the file comment), then the fused
 // activation and residual add in the order the unfused graph applies them.
+// FUSED = false compiles the plain epilogue only (no activation or residual
+// code: the kernels that never fuse keep their register budget).
+template <bool FUSED = true>
 __device__ __forceinline__ float epilogue_value(const Epilogue& ep, int64_t i, int64_t j, int64_t N, int32_t acc,
                                                 double s, float bj) {
     float y = (float)((double)acc * s);
     if (ep.bias) y = y + bj;
-    if (ep.act == kActGelu) y = kh::gelu_exact(y);
-    if (ep.residual) y = ep.residual[i * N + j] + y;
+    if (FUSED) {
+        if (ep.act == kActGelu) y = kh::gelu_exact(y);
+        if (ep.residual) y = ep.residual[i * N + j] + y;
+    }
     return y;
 }
 
@@ -72,6 +77,7 @@ __device__ __forceinline__ void epilogue_store(const Epilogue& ep, int64_t i, in
 // 8*(r/4) + 4*(l/32) + r%4, column l%32, relative to (i0, j)).  The column's
 // scale and bias are read once per block.  Returns the largest |out| bits
 // stored (for the absmax partials of a following per-tensor quantize).
+template <bool FUSED = true>
 __device__ __forceinline__ unsigned store_block32(const Epilogue& ep, int64_t i0, int64_t j, int64_t N,
                                                   const i32x16& v) {
     const double sbj = ep.sb ? ep.sb[ep.sb_per_col ? j : 0] : 0.0;
@@ -84,7 +90,7 @@ __device__ __forceinline__ unsigned store_block32(const Epilogue& ep, int64_t i0
         if (ep.acc) ep.acc[i * N + j] = v[r];
         if (ep.out) {
             const double s = ep.sa_per_row ? ep.sa[i] * sbj : sa0;
-            const float y = epilogue_value(ep, i, j, N, v[r], s, bj);
+            const float y = epilogue_value<FUSED>(ep, i, j, N, v[r], s, bj);
             ep.out[i * N + j] = y;
             mx = max(mx, kh::abs_bits32(y));
         }
@@ -93,6 +99,7 @@ __device__ __forceinline__ unsigned store_block32(const Epilogue& ep, int64_t i0
 }
 
 // store_block32 for a block that may extend past row M or column N.
+template <bool FUSED = true>
 __device__ __forceinline__ unsigned store_block32_masked(const Epilogue& ep, int64_t i0, int64_t j, int64_t M,
                                                          int64_t N, const i32x16& v) {
     if (j >= N) return 0;
@@ -107,7 +114,7 @@ __device__ __forceinline__ unsigned store_block32_masked(const Epilogue& ep, int
         if (ep.acc) ep.acc[i * N + j] = v[r];
         if (ep.out) {
             const double s = ep.sa_per_row ? ep.sa[i] * sbj : sa0;
-            const float y = epilogue_value(ep, i, j, N, v[r], s, bj);
+            const float y = epilogue_value<FUSED>(ep, i, j, N, v[r], s, bj);
             ep.out[i * N + j] = y;
             mx = max(mx, kh::abs_bits32(y));
         }
@@ -327,10 +334,13 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, void* dst, i
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, soff, 0, 0);
 }
 
-template <int BM, int BN, int NS>
-__global__ __launch_bounds__(512) void gemm_i8_pingpong_kernel(const int8_t* __restrict__ A,
-                                                               const int8_t* __restrict__ B, int M, int N, int K,
-                                                               int group_m, Epilogue ep, unsigned* parts) {
+// FUSED: the epilogue may apply an activation and a residual add.  Waves per
+// SIMD: 2 for 256-wide N tiles (128 accumulators per wave), 4 otherwise (two
+// resident workgroups per CU within the 128-register budget).
+template <int BM, int BN, int NS, bool FUSED>
+__global__ __launch_bounds__(512, BN == 256 ? 2 : 4) void gemm_i8_pingpong_kernel(
+    const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, int N, int K, int group_m, Epilogue ep,
+    unsigned* parts) {
     constexpr int BK = 64, WM = 2, WN = 4, kWaves = WM * WN;
     static_assert((BM == 128 || BM == 256) && (BN == 128 || BN == 256), "tile");
     constexpr int kWaveM = BM / WM, kWaveN = BN / WN;
@@ -451,7 +461,7 @@ __global__ __launch_bounds__(512) void gemm_i8_pingpong_kernel(const int8_t* __r
         for (int a = 0; a < kTM; ++a)
 #pragma unroll
             for (int b = 0; b < kTN; ++b) {
-                mx = max(mx, store_block32(ep, row_base + a * 32, col_base + b * 32, N, acc[a][b]));
+                mx = max(mx, store_block32<FUSED>(ep, row_base + a * 32, col_base + b * 32, N, acc[a][b]));
                 __builtin_amdgcn_sched_barrier(0);
             }
     } else {
@@ -459,7 +469,7 @@ __global__ __launch_bounds__(512) void gemm_i8_pingpong_kernel(const int8_t* __r
         for (int a = 0; a < kTM; ++a)
 #pragma unroll
             for (int b = 0; b < kTN; ++b) {
-                mx = max(mx, store_block32_masked(ep, row_base + a * 32, col_base + b * 32, M, N, acc[a][b]));
+                mx = max(mx, store_block32_masked<FUSED>(ep, row_base + a * 32, col_base + b * 32, M, N, acc[a][b]));
                 __builtin_amdgcn_sched_barrier(0);
             }
     }
@@ -567,7 +577,12 @@ template <int BM, int BN, int NS>
 int launch_pingpong_cfg(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
                         const Epilogue& ep, unsigned* parts, int* nparts) {
     const unsigned tiles = (unsigned)(((M + BM - 1) / BM) * ((N + BN - 1) / BN));
-    gemm_i8_pingpong_kernel<BM, BN, NS><<<tiles, 512, 0, d->stream>>>(A, B, (int)M, (int)N, (int)K, 8, ep, parts);
+    if (ep.act != kActNone || ep.residual)
+        gemm_i8_pingpong_kernel<BM, BN, NS, true>
+            <<<tiles, 512, 0, d->stream>>>(A, B, (int)M, (int)N, (int)K, 8, ep, parts);
+    else
+        gemm_i8_pingpong_kernel<BM, BN, NS, false>
+            <<<tiles, 512, 0, d->stream>>>(A, B, (int)M, (int)N, (int)K, 8, ep, parts);
     if (nparts) *nparts = (int)tiles;
     return kh::launch_status("gemm_i8_pingpong");
 }

@@ -64,10 +64,52 @@ __device__ __forceinline__ unsigned block4_max(unsigned v, unsigned* wmax) {
 }
 
 // One row of LayerNorm by one wave; returns this lane's largest |out| bits.
+// VEC: D % 4 == 0 and 16-byte aligned rows, lanes hold float4s (D <= 1024).
+template <bool VEC>
 __device__ __forceinline__ unsigned layernorm_row(const float* __restrict__ x, int64_t row, int D,
-                                                       const float* __restrict__ w, const float* __restrict__ b,
-                                                       float eps, float* __restrict__ out, int lane) {
+                                                  const float* __restrict__ w, const float* __restrict__ b, float eps,
+                                                  float* __restrict__ out, int lane) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
     const float* xr = x + row * D;
+    float* orow = out + row * D;
+    unsigned mx = 0;
+    if (VEC) {
+        constexpr int kV = kLnMaxPerLane / 4;  // float4 per lane
+        f4 v[kV];
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kV; ++i) {
+            const int c4 = lane + i * 64;
+            v[i] = c4 * 4 < D ? reinterpret_cast<const f4*>(xr)[c4] : f4{0.f, 0.f, 0.f, 0.f};
+            s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+        }
+        const float mean = wave_sum(s) / (float)D;
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kV; ++i) {
+            if ((lane + i * 64) * 4 < D) {
+                v[i] -= mean;
+                ss += (v[i].x * v[i].x + v[i].y * v[i].y) + (v[i].z * v[i].z + v[i].w * v[i].w);
+            }
+        }
+        const float var = wave_sum(ss) / (float)D;
+        const float denom = sqrtf(var + eps);
+#pragma unroll
+        for (int i = 0; i < kV; ++i) {
+            const int c4 = lane + i * 64;
+            if (c4 * 4 < D) {
+                const f4 wv = reinterpret_cast<const f4*>(w)[c4], bv = reinterpret_cast<const f4*>(b)[c4];
+                f4 y;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    y[e] = v[i][e] / denom * wv[e] + bv[e];
+                    mx = max(mx, kh::abs_bits32(y[e]));
+                }
+                reinterpret_cast<f4*>(orow)[c4] = y;
+            }
+        }
+        return mx;
+    }
     float v[kLnMaxPerLane];
     float s = 0.0f;
 #pragma unroll
@@ -87,8 +129,6 @@ __device__ __forceinline__ unsigned layernorm_row(const float* __restrict__ x, i
     }
     const float var = wave_sum(ss) / (float)D;
     const float denom = sqrtf(var + eps);
-    float* orow = out + row * D;
-    unsigned mx = 0;
 #pragma unroll
     for (int i = 0; i < kLnMaxPerLane; ++i) {
         const int c = lane + i * 64;
@@ -101,22 +141,29 @@ __device__ __forceinline__ unsigned layernorm_row(const float* __restrict__ x, i
     return mx;
 }
 
+// A 256-thread workgroup normalizes kLnRowsPerBlock rows, each wave one row
+// at a time, and (when parts is given) writes the max |out| of its rows.
+constexpr int kLnRowsPerBlock = 16;
+
+template <bool VEC>
 __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict__ x, int64_t rows, int D,
                                                         const float* __restrict__ w, const float* __restrict__ b,
                                                         float eps, float* __restrict__ out,
                                                         unsigned* __restrict__ parts) {
     __shared__ unsigned wmax[4];
     const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     unsigned mx = 0;
-    if (row < rows) mx = layernorm_row(x, row, D, w, b, eps, out, lane);
+#pragma unroll 1
+    for (int k = threadIdx.x >> 6; k < kLnRowsPerBlock; k += 4) {
+        const int64_t row = (int64_t)blockIdx.x * kLnRowsPerBlock + k;
+        if (row < rows) mx = max(mx, layernorm_row<VEC>(x, row, D, w, b, eps, out, lane));
+    }
     if (parts) {
         // Per-workgroup max |out| bits, for a following per-tensor quantize.
         mx = block4_max(mx, wmax);
         if (threadIdx.x == 0) parts[blockIdx.x] = mx;
     }
 }
-
 
 // ---------------------------------------------------------------------------
 // GELU (exact erf).
@@ -335,10 +382,17 @@ int kh_layernorm_ex(const float* x, int64_t rows, int D, const float* weight, co
     if (rows == 0) return KH_OK;
     KH_REQUIRE(x && weight && bias && out, "kh_layernorm: null pointer");
     KH_DEVICE_OR_RETURN(d);
-    const int64_t blocks = (rows + 3) / 4;
+    const int64_t blocks = (rows + kLnRowsPerBlock - 1) / kLnRowsPerBlock;
+    KH_REQUIRE(blocks <= 0x7FFFFFFFLL, "kh_layernorm: too many rows");
     const bool fused = absmax_parts && blocks <= max_parts;
-    layernorm_kernel<<<(unsigned)blocks, 256, 0, d->stream>>>(x, rows, D, weight, bias, eps, out,
-                                                              fused ? absmax_parts : nullptr);
+    const bool vec = D % 4 == 0 && kh::aligned(x, 16) && kh::aligned(out, 16) && kh::aligned(weight, 16) &&
+                     kh::aligned(bias, 16);
+    if (vec)
+        layernorm_kernel<true><<<(unsigned)blocks, 256, 0, d->stream>>>(x, rows, D, weight, bias, eps, out,
+                                                                        fused ? absmax_parts : nullptr);
+    else
+        layernorm_kernel<false><<<(unsigned)blocks, 256, 0, d->stream>>>(x, rows, D, weight, bias, eps, out,
+                                                                         fused ? absmax_parts : nullptr);
     int rc = kh::launch_status("layernorm");
     if (rc || !absmax_parts) return rc;
     if (fused) {
