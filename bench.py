@@ -17,7 +17,7 @@ CPU baseline: the reference's own compiled backend/cpu/src/Ops.cpp matmul
 dequantizing the weight (python/kansai/quantize.py:115-122) -- on one core,
 over a time-bounded slab of rows of the same workload.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--only gemm,quant,f32,copy]
+    python bench.py [--gpus 1] [--steps 50] [--warmup 50] [--no-cpu] [--only gemm,probe,quant,f32,skinny,c4,copy]
 
 Profiling (the summaries under profiles/ are made this way):
     rocprofv3 --kernel-trace --stats -d OUT/trace -o run --output-format csv -- python3 bench.py --no-cpu
@@ -133,7 +133,7 @@ def bench_f32(H, D, steps, warmup):
     return ms, 2.0 * n ** 3 / (ms * 1e-3) / 1e12
 
 
-def bench_skinny(steps):
+def bench_skinny(steps, warmup):
     """Config C5: kh_linear_i8 (per-token quantize of fp32 x, int8 GEMM,
     per-output-channel weight scales, fused epilogue) for M in {1, 8, 32},
     (K, N) in {(4096, 4096), (4096, 11008)}.  Weight copies are rotated so
@@ -161,7 +161,7 @@ def bench_skinny(steps):
             out = D([M, N], "float32")
             call = lambda w: Nn.call("kh_linear_i8", x.ptr, M, K, w.ptr, N, sw.ptr, 1, bias.ptr, q.ptr, sx.ptr,  # noqa: E731
                                      out.ptr)
-            for i in range(3):
+            for i in range(max(3, warmup)):
                 call(ws[i % copies])
             Nn.synchronize()
             e0, e1 = Nn.Event(), Nn.Event()
@@ -349,8 +349,10 @@ def cpu_baseline(budget_s=12.0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    # The shader clock ramps up over the first ~10 ms of load: 50 untimed
+    # steps let every leg reach its sustained rate before timing.
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="gemm,probe,quant,f32,skinny,c4",
                     help="comma list of gemm,probe,quant,f32,skinny,c4,copy")
@@ -400,11 +402,11 @@ def main():
     skinny = None
     if "skinny" in only:
         log("skinny decode GEMMs C5 ...")
-        skinny = bench_skinny(max(20, args.steps))
+        skinny = bench_skinny(max(20, args.steps), args.warmup)
     c4 = None
     if "c4" in only:
         log("C4 int8 char-LM forward ...")
-        c4 = bench_c4(max(5, args.steps // 4), 2)
+        c4 = bench_c4(max(5, args.steps // 4), max(2, args.warmup // 10))
         log(f"C4 forward: {c4['ms_per_forward']:.3f} ms ({c4['tokens_per_s']:.0f} tokens/s)")
         Nn.call("kh_pool_trim")
     if "copy" in only:
