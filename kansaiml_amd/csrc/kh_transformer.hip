@@ -181,18 +181,21 @@ __global__ __launch_bounds__(256) void gelu_kernel(const float* __restrict__ x, 
 // head h written to its own columns (heads are merged in place).  dk = 64.
 //
 // A workgroup owns 64 queries of one (batch, head); wave w owns queries
-// 16w .. 16w+15 of them.  Keys go through LDS 64 at a time: K as [key][d]
-// and V transposed as [d][key], rows padded to 68 floats so the 16 lanes of
-// a fragment read hit distinct banks.  Both products run on
-// v_mfma_f32_16x16x4_f32 (D[i][j] += sum over k of A[i][k] B[k][j], lane
-// l supplying A[l % 16][l / 16] and B[l / 16][l % 16]).  The dot product over
-// the head dimension is order-free, so MFMA step s of lane group g = l / 16
-// takes d = 16g + s: each lane's operands for 16 steps are 16 consecutive
-// floats (four ds_read_b128).  S = (Q/8) K^T comes out with lane l holding
-// rows 4 * (l / 16) + r, key l % 16: row max and row sum reduce over the 16
-// lanes of a group.  P goes through a per-wave LDS tile to the A layout of
-// the P V product, whose k index (the key) is mapped the same way.
-// The 1/sqrt(dk) = 1/8 scale is applied to Q (exact: a power of two).
+// 16w .. 16w+15 of them, lane l query 16w + l % 16.  Keys go through LDS 64
+// at a time: K as [key][d] and V transposed as [d][key] (4-key groups
+// XOR-swizzled), rows padded to 68 floats.  Both products run on
+// v_mfma_f32_16x16x4_f32 (D[i][j] += sum over k of A[i][k] B[k][j]; lane l
+// supplies A[l % 16][l / 16] and B[l / 16][l % 16]; result register r of lane
+// l is D[4 * (l / 16) + r][l % 16]).  The reduction index of each product is
+// order-free, so it is mapped to keep operands in registers:
+//   S^T = K Q^T (k = head dim; step s of lane group g = l / 16 takes
+//   d = 16g + s): lane l ends up holding, for its own query, the scores of
+//   keys 16t + 4g + r (t, r = 0..3) of the tile;
+//   O^T = V^T P^T (k = key; step (t, r) of lane group g takes key
+//   16t + 4g + r): P^T's operand is exactly the probabilities lane l holds, so
+//   P never leaves registers, and V^T's operand is a 16-byte LDS read.
+// The softmax of a query reduces over its lane's 16 scores and the 4 lanes
+// l % 16 + 16g.  The 1/sqrt(dk) = 1/8 scale is applied to Q (exact).
 // ---------------------------------------------------------------------------
 constexpr int kDk = 64;
 constexpr int kAttQ = 64;      // queries per workgroup (16 per wave)
@@ -201,34 +204,39 @@ constexpr int kAttPad = 68;    // padded LDS row, floats
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
-// max / sum over the 16 lanes of this lane's group (lanes 16g .. 16g+15).
-__device__ __forceinline__ float group16_max(float v) {
-#pragma unroll
-    for (int off = 8; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
+// Column of key kk in row d of the transposed V tile: groups of 4 keys are
+// XOR-swizzled by (d / 16) % 4, so the transposing stores (64 lanes: 16
+// values of d / 4, 4 keys) hit 64 distinct banks; a 4-key group stays
+// contiguous for the 16-byte operand reads.
+__device__ __forceinline__ int vt_col(int d, int kk) { return ((((kk >> 2) ^ (d >> 4)) & 15) << 2) | (kk & 3); }
+
+// max / sum over the 4 lanes l % 16 + 16g holding one query's scores.
+__device__ __forceinline__ float query4_max(float v) {
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    return fmaxf(v, __shfl_xor(v, 32, 64));
 }
-__device__ __forceinline__ float group16_sum(float v) {
-#pragma unroll
-    for (int off = 8; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
+__device__ __forceinline__ float query4_sum(float v) {
+    v += __shfl_xor(v, 16, 64);
+    return v + __shfl_xor(v, 32, 64);
 }
 
 __global__ __launch_bounds__(256) void attention_mfma_kernel(const float* __restrict__ qkv, int B, int T, int H,
                                                              float* __restrict__ out, unsigned* __restrict__ parts) {
     __shared__ __attribute__((aligned(16))) float ks[kAttK][kAttPad];
     __shared__ __attribute__((aligned(16))) float vt[kDk][kAttPad];
-    __shared__ __attribute__((aligned(16))) float ps[4][16][kAttPad];
     const int D = H * kDk;
-    const int qb = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    // Query blocks in reverse: the workgroups with the most key tiles (the
+    // last queries of the causal triangle) are dispatched first.
+    const int qb = gridDim.x - 1 - blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, g = lane >> 4;
     const int64_t row0 = (int64_t)b * T;
     const int q0 = qb * kAttQ + wave * 16;  // this wave's first query
+    const int q = q0 + li;                  // this lane's query
 
-    // Q fragment: query q0 + li, d = 16g .. 16g+15, scaled by 1/8.
+    // Q operand: query q, d = 16g .. 16g+15, scaled by 1/8.
     float qf[16];
     {
-        const int q = q0 + li;
         const f32x4v* qr = reinterpret_cast<const f32x4v*>(qkv + (row0 + min(q, T - 1)) * 3 * D + h * kDk + 16 * g);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
@@ -237,15 +245,10 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(const float* __rest
             for (int e = 0; e < 4; ++e) qf[4 * c + e] = q < T ? v[e] * 0.125f : 0.0f;
         }
     }
-    f32x4v o[4];  // output tile: d-subtile j, rows 4g + r, column d = 16j + li
+    f32x4v o[4];  // O^T: register r of o[j] is O[q][16j + 4g + r]
 #pragma unroll
     for (int j = 0; j < 4; ++j) o[j] = f32x4v{0.f, 0.f, 0.f, 0.f};
-    float m[4], l[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        m[r] = -3.0e38f;
-        l[r] = 0.0f;
-    }
+    float m = -3.0e38f, l = 0.0f;
 
     const int q_hi = min(T, (qb + 1) * kAttQ) - 1;  // last query of the workgroup
     for (int k0 = 0; k0 <= q_hi; k0 += kAttK) {
@@ -263,98 +266,85 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(const float* __rest
             }
             *reinterpret_cast<f32x4v*>(&ks[kk][4 * d4]) = kv;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) vt[4 * d4 + c][kk] = vv[c];
+            for (int c = 0; c < 4; ++c) vt[4 * d4 + c][vt_col(4 * d4 + c, kk)] = vv[c];
         }
         __syncthreads();
 
-        // S = Q K^T for 4 subtiles of 16 keys.
-        f32x4v sv[4];
+        // S^T = K Q^T, 4 subtiles of 16 keys: st[t][r] = score of key 16t + 4g + r.
+        f32x4v st[4];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            sv[t] = f32x4v{0.f, 0.f, 0.f, 0.f};
-            const f32x4v* kr = reinterpret_cast<const f32x4v*>(&ks[16 * t + li][16 * g]);
+        for (int t = 0; t < 4; ++t) st[t] = f32x4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const f32x4v kv = kr[c];
+        for (int c = 0; c < 4; ++c) {
+            f32x4v kv[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    sv[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[4 * c + e], kv[e], sv[t], 0, 0, 0);
-            }
+            for (int t = 0; t < 4; ++t) kv[t] = reinterpret_cast<const f32x4v*>(&ks[16 * t + li][16 * g])[c];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    st[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[t][e], qf[4 * c + e], st[t], 0, 0, 0);
         }
-        // Causal mask (key > query) and keys past T; online softmax per row.
-        float corr[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int q = q0 + 4 * g + r;
-            float mx = -3.0e38f;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const int key = k0 + 16 * t + li;
-                if (key > q || key >= T) sv[t][r] = -3.0e38f;
-                mx = fmaxf(mx, sv[t][r]);
-            }
-            mx = group16_max(mx);
-            const float m_new = fmaxf(m[r], mx);
-            corr[r] = __expf(m[r] - m_new);
-            float sum = 0.0f;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const int key = k0 + 16 * t + li;
-                const float p = (key > q || key >= T) ? 0.0f : __expf(sv[t][r] - m_new);
-                sv[t][r] = p;
-                sum += p;
-            }
-            l[r] = l[r] * corr[r] + group16_sum(sum);
-            m[r] = m_new;
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) o[j][r] *= corr[r];
-        // P to LDS (row 4g + r, key 16t + li), then read back in A layout.
+        // Causal mask (key > query) and keys past T -- only where the tile
+        // reaches this wave's diagonal or the sequence end.
+        const bool full = k0 + kAttK - 1 <= q0 && k0 + kAttK <= T;
+        float mx = -3.0e38f;
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) ps[wave][4 * g + r][16 * t + li] = sv[t][r];
-        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's P stores are done
-        __builtin_amdgcn_wave_barrier();
-        f32x4v pf[4];
-        {
-            const f32x4v* pr = reinterpret_cast<const f32x4v*>(&ps[wave][li][16 * g]);
-#pragma unroll
-            for (int c = 0; c < 4; ++c) pf[c] = pr[c];
-        }
-        // O += P V: A = P (query li, key 16g + s), B = V (key 16g + s, d 16j + li).
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const f32x4v* vr = reinterpret_cast<const f32x4v*>(&vt[16 * j + li][16 * g]);
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const f32x4v vv = vr[c];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(pf[c][e], vv[e], o[j], 0, 0, 0);
+            for (int r = 0; r < 4; ++r) {
+                const int key = k0 + 16 * t + 4 * g + r;
+                if (!full && (key > q || key >= T)) st[t][r] = -3.0e38f;
+                mx = fmaxf(mx, st[t][r]);
             }
+        mx = query4_max(mx);
+        const float m_new = fmaxf(m, mx);
+        const float corr = __expf(m - m_new);
+        float sum = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int key = k0 + 16 * t + 4 * g + r;
+                const float p = (!full && (key > q || key >= T)) ? 0.0f : __expf(st[t][r] - m_new);
+                st[t][r] = p;
+                sum += p;
+            }
+        l = l * corr + query4_sum(sum);
+        m = m_new;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] *= corr;
+        // O^T += V^T P^T: A = V^T (d 16j + li, key 16t + 4g + r), B = P^T (in registers).
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            f32x4v va[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                va[j] = *reinterpret_cast<const f32x4v*>(&vt[16 * j + li][vt_col(16 * j + li, 16 * t + 4 * g)]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(va[j][r], st[t][r], o[j], 0, 0, 0);
         }
     }
-    unsigned mx = 0;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int q = q0 + 4 * g + r;
-        if (q >= T) continue;
-        const float inv = 1.0f / l[r];
-        float* orow = out + (row0 + q) * D + h * kDk;
+    unsigned mxo = 0;
+    if (q < T) {
+        const float inv = 1.0f / l;
+        float* orow = out + (row0 + q) * D + h * kDk + 4 * g;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const float y = o[j][r] * inv;
-            orow[16 * j + li] = y;
-            mx = max(mx, kh::abs_bits32(y));
+            const f32x4v y = o[j] * inv;
+            *reinterpret_cast<f32x4v*>(orow + 16 * j) = y;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) mxo = max(mxo, kh::abs_bits32(y[r]));
         }
     }
     if (parts) {
         // Per-workgroup max |out| bits, for a following per-tensor quantize.
         __shared__ unsigned wmax[4];
-        mx = block4_max(mx, wmax);
-        if (tid == 0) parts[((int64_t)b * gridDim.y + h) * gridDim.x + qb] = mx;
+        mxo = block4_max(mxo, wmax);
+        if (tid == 0) parts[((int64_t)b * gridDim.y + h) * gridDim.x + blockIdx.x] = mxo;
     }
 }
 
