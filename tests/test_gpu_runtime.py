@@ -65,3 +65,24 @@ def test_invalid_arguments_raise(rt):
         N.call("kh_quantize_rows", None, -1, 4, None, None)
     with pytest.raises(RuntimeError):
         N.call("kh_gemm_i8", None, None, 4, 4, 4, None, 0, None, 0, None, None, None)
+
+
+def test_mfma_probe_reports_rate_and_clock():
+    """kh_probe_mfma_i8: a positive int8 rate no higher than the published
+    5.0 POP/s, a shader clock in (0, 2.5 GHz], and an error (not a fault) for
+    an operand buffer smaller than compute units x 64 KiB."""
+    import ctypes
+
+    import numpy as np
+
+    from kansaiml_amd import _native as N
+    from kansaiml_amd.device import DeviceTensor as D
+    cus = N.device_info()["cus"]
+    nbytes = cus * 64 * 1024
+    ops = D.from_host(np.random.Generator(np.random.PCG64(1)).integers(-127, 128, nbytes, dtype=np.int8))
+    tops, mhz = ctypes.c_double(), ctypes.c_double()
+    N.call("kh_probe_mfma_i8", ops.ptr, nbytes, 200, ctypes.byref(tops), ctypes.byref(mhz))
+    assert 0.0 < tops.value <= 5100.0
+    assert 0.0 < mhz.value <= 2500.0
+    with pytest.raises(RuntimeError):
+        N.call("kh_probe_mfma_i8", ops.ptr, nbytes - 16, 200, ctypes.byref(tops), ctypes.byref(mhz))
