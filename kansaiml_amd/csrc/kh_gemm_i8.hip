@@ -588,11 +588,15 @@ int launch_pingpong_cfg(kh::Device* d, const int8_t* A, const int8_t* B, int64_t
 }
 
 // The largest tile that still gives the chip at least 1.5 tiles per CU;
-// the smallest tile otherwise.  Short K gets a 3-stage ring.
+// the smallest tile otherwise.  Short K (<= 512: a handful of K-steps, where
+// writing the fp32 tile dominates) takes 128x128 tiles, several resident per
+// CU, so one workgroup's epilogue overlaps another's main loop.  Short K gets
+// a 3-stage ring.
 int launch_pingpong(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
                     const Epilogue& ep, unsigned* parts = nullptr, int* nparts = nullptr) {
     auto tiles = [&](int64_t bm, int64_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
     const int64_t want = (int64_t)d->cus * 3 / 2;
+    if (K <= 512) return launch_pingpong_cfg<128, 128, 3>(d, A, B, M, N, K, ep, parts, nparts);
     if (tiles(256, 256) >= want) {
         if (K >= 1024) return launch_pingpong_cfg<256, 256, 4>(d, A, B, M, N, K, ep, parts, nparts);
         return launch_pingpong_cfg<256, 256, 3>(d, A, B, M, N, K, ep, parts, nparts);
