@@ -22,6 +22,8 @@
 // distinct banks.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "kh_common.h"
 #include "kh_quant_math.h"
 #include "kh_act.h"
@@ -49,19 +51,26 @@ constexpr int kActNone = 0;
 constexpr int kActGelu = 1;
 
 // The fp32 output of one accumulator (see the file comment), then the fused
-// activation and residual add in the order the unfused graph applies them.
+// activation and residual add in the order the unfused graph applies them;
+// `resid` is residual[i, j] (read by the caller, ignored without a residual).
 // FUSED = false compiles the plain epilogue only (no activation or residual
 // code: the kernels that never fuse keep their register budget).
 template <bool FUSED = true>
-__device__ __forceinline__ float epilogue_value(const Epilogue& ep, int64_t i, int64_t j, int64_t N, int32_t acc,
-                                                double s, float bj) {
+__device__ __forceinline__ float epilogue_finish(const Epilogue& ep, int32_t acc, double s, float bj, float resid) {
     float y = (float)((double)acc * s);
     if (ep.bias) y = y + bj;
     if (FUSED) {
         if (ep.act == kActGelu) y = kh::gelu_exact(y);
-        if (ep.residual) y = ep.residual[i * N + j] + y;
+        if (ep.residual) y = resid + y;
     }
     return y;
+}
+
+template <bool FUSED = true>
+__device__ __forceinline__ float epilogue_value(const Epilogue& ep, int64_t i, int64_t j, int64_t N, int32_t acc,
+                                                double s, float bj) {
+    const float resid = (FUSED && ep.residual) ? ep.residual[i * N + j] : 0.0f;
+    return epilogue_finish<FUSED>(ep, acc, s, bj, resid);
 }
 
 // One output element of the epilogue (see the file comment).
@@ -74,52 +83,59 @@ __device__ __forceinline__ void epilogue_store(const Epilogue& ep, int64_t i, in
 }
 
 // Stores one 32x32 MFMA result block (register r of lane l holds row
-// 8*(r/4) + 4*(l/32) + r%4, column l%32, relative to (i0, j)).  The column's
-// scale and bias are read once per block.  Returns the largest |out| bits
-// stored (for the absmax partials of a following per-tensor quantize).
-template <bool FUSED = true>
-__device__ __forceinline__ unsigned store_block32(const Epilogue& ep, int64_t i0, int64_t j, int64_t N,
-                                                  const i32x16& v) {
+// 8*(r/4) + 4*(l/32) + r%4, column l%32, relative to (i0, j)); MASKED skips
+// rows >= M and columns >= N.  The column's scale and bias are read once per
+// block.  The residual is read RG rows at a time, each group before any of
+// its stores: the output may alias nothing the compiler can prove, so a load
+// left after a store would wait for it (one memory round trip per element
+// instead of one per group).  Returns the largest |out| bits stored (for the
+// absmax partials of a following per-tensor quantize).
+template <bool FUSED, int RG, bool MASKED>
+__device__ __forceinline__ unsigned store_block32_impl(const Epilogue& ep, int64_t i0, int64_t j, int64_t M,
+                                                       int64_t N, const i32x16& v) {
+    static_assert(16 % RG == 0, "residual group");
+    if (MASKED && j >= N) return 0;
     const double sbj = ep.sb ? ep.sb[ep.sb_per_col ? j : 0] : 0.0;
     const float bj = ep.bias ? ep.bias[j] : 0.0f;
     const double sa0 = (ep.sa && !ep.sa_per_row) ? ep.sa[0] * sbj : 0.0;
     unsigned mx = 0;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int64_t i = i0 + 8 * (r >> 2) + (r & 3);
-        if (ep.acc) ep.acc[i * N + j] = v[r];
-        if (ep.out) {
-            const double s = ep.sa_per_row ? ep.sa[i] * sbj : sa0;
-            const float y = epilogue_value<FUSED>(ep, i, j, N, v[r], s, bj);
-            ep.out[i * N + j] = y;
-            mx = max(mx, kh::abs_bits32(y));
+    for (int g0 = 0; g0 < 16; g0 += RG) {
+        float res[RG];
+#pragma unroll
+        for (int rr = 0; rr < RG; ++rr) {
+            const int r = g0 + rr;
+            const int64_t i = i0 + 8 * (r >> 2) + (r & 3);
+            res[rr] = (FUSED && ep.residual && (!MASKED || i < M)) ? ep.residual[i * N + j] : 0.0f;
+        }
+#pragma unroll
+        for (int rr = 0; rr < RG; ++rr) {
+            const int r = g0 + rr;
+            const int64_t i = i0 + 8 * (r >> 2) + (r & 3);
+            if (MASKED && i >= M) continue;
+            if (ep.acc) ep.acc[i * N + j] = v[r];
+            if (ep.out) {
+                const double s = ep.sa_per_row ? ep.sa[i] * sbj : sa0;
+                const float y = epilogue_finish<FUSED>(ep, v[r], s, bj, res[rr]);
+                ep.out[i * N + j] = y;
+                mx = max(mx, kh::abs_bits32(y));
+            }
         }
     }
     return mx;
 }
 
+template <bool FUSED = true, int RG = 16>
+__device__ __forceinline__ unsigned store_block32(const Epilogue& ep, int64_t i0, int64_t j, int64_t N,
+                                                  const i32x16& v) {
+    return store_block32_impl<FUSED, RG, false>(ep, i0, j, 0, N, v);
+}
+
 // store_block32 for a block that may extend past row M or column N.
-template <bool FUSED = true>
+template <bool FUSED = true, int RG = 16>
 __device__ __forceinline__ unsigned store_block32_masked(const Epilogue& ep, int64_t i0, int64_t j, int64_t M,
                                                          int64_t N, const i32x16& v) {
-    if (j >= N) return 0;
-    const double sbj = ep.sb ? ep.sb[ep.sb_per_col ? j : 0] : 0.0;
-    const float bj = ep.bias ? ep.bias[j] : 0.0f;
-    const double sa0 = (ep.sa && !ep.sa_per_row) ? ep.sa[0] * sbj : 0.0;
-    unsigned mx = 0;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int64_t i = i0 + 8 * (r >> 2) + (r & 3);
-        if (i >= M) continue;
-        if (ep.acc) ep.acc[i * N + j] = v[r];
-        if (ep.out) {
-            const double s = ep.sa_per_row ? ep.sa[i] * sbj : sa0;
-            const float y = epilogue_value<FUSED>(ep, i, j, N, v[r], s, bj);
-            ep.out[i * N + j] = y;
-            mx = max(mx, kh::abs_bits32(y));
-        }
-    }
-    return mx;
+    return store_block32_impl<FUSED, RG, true>(ep, i0, j, M, N, v);
 }
 
 template <int BM, int BN, int BK, int WM, int WN>
@@ -349,6 +365,10 @@ __global__ __launch_bounds__(512, BN == 256 ? 2 : 4) void gemm_i8_pingpong_kerne
     constexpr int kAInst = BM / 16 / kWaves, kBInst = BN / 16 / kWaves;  // 1 KB = 16 rows per instruction
     constexpr int kLoads = kAInst + kBInst;  // LDS-DMA instructions per wave per stage
     constexpr int D = NS - 1;                // prefetch distance in stages
+    // Residual rows read ahead of their stores in the fused epilogue: all 16
+    // of a block where the register budget allows, 4 in the 256x128 tile
+    // (4 waves per SIMD leave it no room for 16).
+    constexpr int kResidRows = (BM == 256 && BN == 128) ? 4 : 16;
     static_assert(NS >= 3 && NS <= 5, "wait_loads_beyond covers up to 3 stages ahead");
     __shared__ __attribute__((aligned(1024))) int8_t lds[NS * kStage];
 
@@ -461,7 +481,7 @@ __global__ __launch_bounds__(512, BN == 256 ? 2 : 4) void gemm_i8_pingpong_kerne
         for (int a = 0; a < kTM; ++a)
 #pragma unroll
             for (int b = 0; b < kTN; ++b) {
-                mx = max(mx, store_block32<FUSED>(ep, row_base + a * 32, col_base + b * 32, N, acc[a][b]));
+                mx = max(mx, store_block32<FUSED, kResidRows>(ep, row_base + a * 32, col_base + b * 32, N, acc[a][b]));
                 __builtin_amdgcn_sched_barrier(0);
             }
     } else {
@@ -469,7 +489,7 @@ __global__ __launch_bounds__(512, BN == 256 ? 2 : 4) void gemm_i8_pingpong_kerne
         for (int a = 0; a < kTM; ++a)
 #pragma unroll
             for (int b = 0; b < kTN; ++b) {
-                mx = max(mx, store_block32_masked<FUSED>(ep, row_base + a * 32, col_base + b * 32, M, N, acc[a][b]));
+                mx = max(mx, store_block32_masked<FUSED, kResidRows>(ep, row_base + a * 32, col_base + b * 32, M, N, acc[a][b]));
                 __builtin_amdgcn_sched_barrier(0);
             }
     }
@@ -494,67 +514,115 @@ __global__ __launch_bounds__(512, BN == 256 ? 2 : 4) void gemm_i8_pingpong_kerne
 // A workgroup owns 16 output columns for all M rows; its SKW waves split K,
 // each streaming its slice of those 16 packed weight rows (16 B per lane per
 // 64-k step) through v_mfma_i32_16x16x64_i8 with up to two 16-row tiles of
-// activations.  Rows >= M read zeros: their buffer offsets fall past the
-// activation resource, whose loads return 0.  The waves' partial int32
-// accumulators are summed through LDS (integer sums are exact in any order)
-// and the first wave applies the epilogue.  Bound: HBM bytes of the weight,
-// N*K, plus the activations (L2 resident) and the output.
+// activations.  Each wave takes its slice in chunks of C steps (8 where the
+// slice allows) and issues all of a chunk's loads, the weights first and
+// then the activations, before its first MFMA (scheduling barriers keep the
+// compiler from interleaving them with the MFMAs' waits), so the HBM stream
+// and the L2-resident activations are in flight together instead of one
+// latency after the other.  Rows >= M read zeros: their buffer offsets fall past the activation
+// resource, whose loads return 0.  The waves' partial int32 accumulators are
+// summed through LDS (integer sums are exact in any order) and the first MT
+// waves apply the epilogue, one 16-row tile each.  Bound: HBM bytes of the
+// weight, N*K, plus the activations (L2 resident) and the output.
 // ---------------------------------------------------------------------------
 typedef int i32x4v __attribute__((ext_vector_type(4)));
 constexpr int kSkinnyWaves = 8;
 
-template <int MT>
+template <int MT, int NT, int C, bool ONE>
 __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_i8_skinny_kernel(const int8_t* __restrict__ A,
                                                                            const int8_t* __restrict__ B, int M,
                                                                            int N, int K, Epilogue ep) {
-    __shared__ i32x4v red[kSkinnyWaves][MT][64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int n0 = blockIdx.x * 16;
-    const int col = n0 + (lane & 15);
+    static_assert(MT * NT <= kSkinnyWaves, "one epilogue wave per 16x16 tile");
+    __shared__ i32x4v red[kSkinnyWaves][MT * NT][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n0 = blockIdx.x * 16 * NT;
     const int kg = (lane >> 4) * 16;
-    const int kper = K / kSkinnyWaves;
+    // The launch guarantees K % (512 * C) == 0 and K > 0; saying so lets the
+    // compiler load every kernel argument before the first weight load
+    // instead of after a loop-skip branch.
+    __builtin_assume(K >= 64 * kSkinnyWaves * C);
+    constexpr int AC = C < 4 ? C : 4;
+    const int kper = K / kSkinnyWaves;  // a multiple of 64 * C; exactly 64 * C when ONE
     const int k_begin = wave * kper;
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, (uint32_t)M * (uint32_t)K);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(B, (uint32_t)N * (uint32_t)K);
-    const int b_off = min(col, N - 1) * K + kg;
+    int b_off[NT];
+#pragma unroll
+    for (int u = 0; u < NT; ++u) b_off[u] = min(n0 + u * 16 + (lane & 15), N - 1) * K + kg;
     int a_off[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t) a_off[t] = (t * 16 + (lane & 15)) * K + kg;
 
-    i32x4v acc[MT];
+    i32x4v acc[MT][NT];
 #pragma unroll
-    for (int t = 0; t < MT; ++t) acc[t] = i32x4v{0, 0, 0, 0};
-#pragma unroll 8
-    for (int k = k_begin; k < k_begin + kper; k += 64) {
-        const i32x4v b = __builtin_amdgcn_raw_buffer_load_b128(rb, b_off, k, 0);
+    for (int t = 0; t < MT; ++t)
 #pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            const i32x4v a = __builtin_amdgcn_raw_buffer_load_b128(ra, a_off[t], k, 0);
-            acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc[t], 0, 0, 0);
+        for (int u = 0; u < NT; ++u) acc[t][u] = i32x4v{0, 0, 0, 0};
+    auto chunk = [&](int k0) {
+        i32x4v b[NT][C];
+#pragma unroll
+        for (int u = 0; u < NT; ++u)
+#pragma unroll
+            for (int c = 0; c < C; ++c) b[u][c] = __builtin_amdgcn_raw_buffer_load_b128(rb, b_off[u], k0 + 64 * c, 0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int c0 = 0; c0 < C; c0 += AC) {
+            i32x4v a[MT][AC];
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int c = 0; c < AC; ++c)
+                    a[t][c] = __builtin_amdgcn_raw_buffer_load_b128(ra, a_off[t], k0 + 64 * (c0 + c), 0);
+#pragma unroll
+            for (int c = 0; c < AC; ++c)
+#pragma unroll
+                for (int t = 0; t < MT; ++t)
+#pragma unroll
+                    for (int u = 0; u < NT; ++u)
+                        acc[t][u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t][c], b[u][c0 + c], acc[t][u], 0, 0, 0);
         }
+    };
+    // A wave's whole slice as one chunk where it fits (measured ~1 us faster
+    // than the same loads under a loop, even one that runs once).
+    if constexpr (ONE) {
+        chunk(k_begin);
+    } else {
+        for (int k0 = k_begin; k0 < k_begin + kper; k0 += 64 * C) chunk(k0);
     }
 #pragma unroll
-    for (int t = 0; t < MT; ++t) red[wave][t][lane] = acc[t];
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int u = 0; u < NT; ++u) red[wave][t * NT + u][lane] = acc[t][u];
     __syncthreads();
-    if (wave != 0) return;
-    // 16x16 MFMA result layout: register r of lane l holds row 4*(l/16) + r,
-    // column l%16.
-    const int64_t j = col;
+    if (wave >= MT * NT) return;
+    // Wave w finishes row tile w / NT of column tile w % NT.  16x16 MFMA
+    // result layout: register r of lane l holds row 4*(l/16) + r, column l%16.
+    const int t = wave / NT;
+    const int64_t j = n0 + (wave % NT) * 16 + (lane & 15);
     if (j >= N) return;
+    // Every load of the epilogue is issued before its first store (the
+    // output may alias nothing the compiler can prove, so a load left after
+    // a store would wait for it: one memory round trip per row).
     const double sbj = ep.sb ? ep.sb[ep.sb_per_col ? j : 0] : 0.0;
     const float bj = ep.bias ? ep.bias[j] : 0.0f;
+    double sai[4];
+    float res[4];
 #pragma unroll
-    for (int t = 0; t < MT; ++t) {
-        i32x4v sum = red[0][t][lane];
+    for (int r = 0; r < 4; ++r) {
+        const int64_t i = min((int64_t)(t * 16 + 4 * (lane >> 4) + r), (int64_t)M - 1);
+        sai[r] = ep.out ? ep.sa[ep.sa_per_row ? i : 0] : 0.0;
+        res[r] = ep.residual ? ep.residual[i * N + j] : 0.0f;
+    }
+    i32x4v sum = red[0][wave][lane];
 #pragma unroll
-        for (int w = 1; w < kSkinnyWaves; ++w) sum += red[w][t][lane];
+    for (int w = 1; w < kSkinnyWaves; ++w) sum += red[w][wave][lane];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int64_t i = t * 16 + 4 * (lane >> 4) + r;
-            if (i >= M) continue;
-            if (ep.acc) ep.acc[i * N + j] = sum[r];
-            if (ep.out) ep.out[i * N + j] = epilogue_value(ep, i, j, N, sum[r], ep.sa[ep.sa_per_row ? i : 0] * sbj, bj);
-        }
+    for (int r = 0; r < 4; ++r) {
+        const int64_t i = t * 16 + 4 * (lane >> 4) + r;
+        if (i >= M) continue;
+        if (ep.acc) ep.acc[i * N + j] = sum[r];
+        if (ep.out) ep.out[i * N + j] = epilogue_finish(ep, sum[r], sai[r] * sbj, bj, res[r]);
     }
 }
 
@@ -565,11 +633,43 @@ bool skinny_fits(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t
 
 int launch_skinny(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
                   const Epilogue& ep) {
-    const unsigned blocks = (unsigned)((N + 15) / 16);
-    if (M <= 16)
-        gemm_i8_skinny_kernel<1><<<blocks, kSkinnyWaves * 64, 0, d->stream>>>(A, B, (int)M, (int)N, (int)K, ep);
-    else
-        gemm_i8_skinny_kernel<2><<<blocks, kSkinnyWaves * 64, 0, d->stream>>>(A, B, (int)M, (int)N, (int)K, ep);
+    const int64_t steps = K / (64 * kSkinnyWaves);  // 64-k steps per wave
+    // 32 columns per workgroup (each activation fragment feeds two weight
+    // tiles, halving the activation reads from L2) for two row tiles, where
+    // that still leaves a workgroup per CU and the slice is one chunk of 4 or
+    // 8 steps.  With one row tile the activation reads are small and the
+    // halved workgroup count costs more than it saves (measured).
+    const bool wide = M > 16 && N >= 32LL * d->cus && (steps == 4 || steps == 8);
+    auto go = [&](auto mt, auto nt, auto c, auto one) {
+        constexpr int NT = decltype(nt)::value;
+        const unsigned blocks = (unsigned)((N + 16 * NT - 1) / (16 * NT));
+        gemm_i8_skinny_kernel<decltype(mt)::value, NT, decltype(c)::value, decltype(one)::value>
+            <<<blocks, kSkinnyWaves * 64, 0, d->stream>>>(A, B, (int)M, (int)N, (int)K, ep);
+    };
+    auto pick = [&](auto mt) {
+        using T = std::true_type;
+        using F = std::false_type;
+        using N1 = std::integral_constant<int, 1>;
+        using N2 = std::integral_constant<int, 2>;
+        if (wide) {
+            if (steps == 4) return go(mt, N2(), std::integral_constant<int, 4>(), T());
+            return go(mt, N2(), std::integral_constant<int, 8>(), T());
+        }
+        switch (steps) {
+            case 1: return go(mt, N1(), std::integral_constant<int, 1>(), T());
+            case 2: return go(mt, N1(), std::integral_constant<int, 2>(), T());
+            case 4: return go(mt, N1(), std::integral_constant<int, 4>(), T());
+            case 8: return go(mt, N1(), std::integral_constant<int, 8>(), T());
+            case 16: return go(mt, N1(), std::integral_constant<int, 16>(), T());
+            default: break;
+        }
+        if (steps % 8 == 0) go(mt, N1(), std::integral_constant<int, 8>(), F());
+        else if (steps % 4 == 0) go(mt, N1(), std::integral_constant<int, 4>(), F());
+        else if (steps % 2 == 0) go(mt, N1(), std::integral_constant<int, 2>(), F());
+        else go(mt, N1(), std::integral_constant<int, 1>(), F());
+    };
+    if (M <= 16) pick(std::integral_constant<int, 1>());
+    else pick(std::integral_constant<int, 2>());
     return kh::launch_status("gemm_i8_skinny");
 }
 

@@ -47,6 +47,8 @@ SHAPES = [
     (129, 257, 80), (300, 200, 48), (2048, 2048, 512), (2304, 2176, 1024),
     (33, 40, 130), (100, 50, 77), (5, 7, 3),  # K % 16 != 0: byte-gather path
     (2, 100, 512), (17, 4096, 4096), (31, 64, 1024), (16, 16, 512), (5, 11008, 4096), (32, 40, 512),  # skinny
+    (30, 8200, 2048), (20, 8216, 4096),  # skinny, 32 columns per workgroup, partial last workgroup
+    (9, 40, 8192), (2, 33, 1536),       # skinny: a 16-step slice; a 3-step slice (chunk loop)
     (512, 768, 64), (768, 512, 192), (1024, 256, 4160),  # full-tile kernel: K % 64 == 0, K % 128 != 0
     (1000, 1000, 128), (257, 129, 64), (33, 300, 640),    # ping-pong kernel, partial tiles in M and N
     (16384, 1152, 384), (16384, 384, 1536),               # C4 QKV and fc2 shapes
