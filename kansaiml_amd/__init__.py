@@ -7,6 +7,9 @@ Modules:
   hip       tensor-level ops (shape checks + kernel calls)
   quantize  the reference's quantize.py API on the GPU
   kir       the KIR graph schema, tracer, memory planner and run_hip
+  serialize KAN1 parameter checkpoints, with int8 weights that load
+            straight to the device
+  charlm    the int8 char-LM forward (config C4)
   build     compiles kansaiml_amd/csrc/*.hip for gfx950
 
 Importing the package does not touch the GPU.

@@ -28,8 +28,20 @@ from .device import DeviceTensor
 from .quantize import QTensor
 
 
+# Parameter names of the reference's BigGPT, in its named_parameters() order
+# (train_shakespeare_large.py:61-79 over nn.py:19-39: tok_embed, pos_embed,
+# blocks.i = TransformerBlock nn.py:466-472 {ln1, attn (w_q, w_k, w_v, w_o,
+# nn.py:384-390), ln2, fc1, fc2}, ln_f, head), with the key each has here.
+_BLOCK_PARAMS = (("ln1.weight", "ln1_w"), ("ln1.bias", "ln1_b"), ("attn.w_q", "w_q"), ("attn.w_k", "w_k"),
+                 ("attn.w_v", "w_v"), ("attn.w_o", "w_o"), ("ln2.weight", "ln2_w"), ("ln2.bias", "ln2_b"),
+                 ("fc1.weight", "fc1_w"), ("fc1.bias", "fc1_b"), ("fc2.weight", "fc2_w"), ("fc2.bias", "fc2_b"))
+
+
 class CharLMWeights:
-    """fp32 parameters of the model, host side (numpy), seeded."""
+    """fp32 parameters of the model, host side (numpy), seeded.
+
+    named_parameters() / set_parameter() use the reference BigGPT's names, so
+    kansaiml_amd.serialize reads and writes checkpoints of it."""
 
     def __init__(self, vocab=65, d_model=384, heads=6, layers=6, d_ff=1536, seq=256, seed=0, std=0.02,
                  bias_std=0.0):
@@ -57,10 +69,47 @@ class CharLMWeights:
         self.lnf_w, self.lnf_b = np.ones(d_model, f32), np.zeros(d_model, f32)
         self.head_w, self.head_b = lin(d_model, vocab), bias(vocab)
 
+    def _slots(self):
+        """(reference name, container, key) for every parameter."""
+        yield "tok_embed.weight", self, "tok"
+        yield "pos_embed.weight", self, "pos"
+        for i, b in enumerate(self.blocks):
+            for name, key in _BLOCK_PARAMS:
+                yield f"blocks.{i}.{name}", b, key
+        for name, key in (("ln_f.weight", "lnf_w"), ("ln_f.bias", "lnf_b"), ("head.weight", "head_w"),
+                          ("head.bias", "head_b")):
+            yield name, self, key
+
+    def named_parameters(self):
+        for name, c, key in self._slots():
+            yield name, (c[key] if isinstance(c, dict) else getattr(c, key))
+
+    def set_parameter(self, name: str, value) -> None:
+        """Stores a loaded value (an int8 QTensor is dequantized on the device
+        first, quantize.py:73-77)."""
+        from .quantize import QTensor
+        for n, c, key in self._slots():
+            if n == name:
+                if isinstance(value, QTensor):
+                    value = value.dequantize().numpy()
+                arr = np.array(value, dtype=np.float32)
+                if isinstance(c, dict):
+                    c[key] = arr
+                else:
+                    setattr(c, key, arr)
+                return
+        raise KeyError(name)
+
 
 class CharLM:
     """Device-resident int8 model; `forward(ids)` returns fp32 logits
-    [batch * seq, vocab] (numpy by default)."""
+    [batch * seq, vocab] (numpy by default).
+
+    named_parameters() yields the device parameters under the reference
+    BigGPT's names (Q, K and V as row slices of the fused QKV weight), so
+    kansaiml_amd.serialize saves an int8 checkpoint of the model and loads
+    one (or a float32 checkpoint, quantized per output channel on the way)
+    into it in place.  `w` stays the construction-time weights."""
 
     def __init__(self, w: CharLMWeights):
         self.w = w
@@ -78,6 +127,32 @@ class CharLM:
         self.lnf_w, self.lnf_b = up(w.lnf_w), up(w.lnf_b)
         self.head, self.head_b = QTensor.from_weight(w.head_w, "col"), up(w.head_b)
         self._graphs = {}
+
+    def named_parameters(self):
+        yield "tok_embed.weight", self.tok
+        yield "pos_embed.weight", self.pos
+        d = self.w.d_model
+        for i, p in enumerate(self.blocks):
+            qkv = p["w_qkv"]
+            views = {}
+            for j, key in enumerate(("w_q", "w_k", "w_v")):
+                views[key] = QTensor(qkv.codes.view(j * d * d, [d, d]), qkv.scales.view(j * d, [d]), [d, d], "col",
+                                     packed=True, owned=False)
+            own = dict(ln1_w=p["ln1_w"], ln1_b=p["ln1_b"], w_o=p["w_o"], ln2_w=p["ln2_w"], ln2_b=p["ln2_b"],
+                       fc1_w=p["fc1"], fc1_b=p["fc1_b"], fc2_w=p["fc2"], fc2_b=p["fc2_b"], **views)
+            for name, key in _BLOCK_PARAMS:
+                yield f"blocks.{i}.{name}", own[key]
+        yield "ln_f.weight", self.lnf_w
+        yield "ln_f.bias", self.lnf_b
+        yield "head.weight", self.head
+        yield "head.bias", self.head_b
+
+    def set_parameter(self, name: str, value) -> None:
+        from .serialize import assign_in_place
+        for n, target in self.named_parameters():
+            if n == name:
+                return assign_in_place(name, target, value)
+        raise KeyError(name)
 
     def _fn(self, batch, seq):
         def linear(x, qw, b=None):

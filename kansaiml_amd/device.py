@@ -35,7 +35,8 @@ class DeviceTensor:
 
     # absmax_parts: the per-tensor absmax partials the producing kernel wrote
     # alongside this tensor, when a fused graph asked for them (kir.py).
-    __slots__ = ("ptr", "shape", "dtype", "nbytes", "_owned", "absmax_parts", "__weakref__")
+    # _base: the tensor a view was cut from (kept alive as long as the view).
+    __slots__ = ("ptr", "shape", "dtype", "nbytes", "_owned", "absmax_parts", "_base", "__weakref__")
 
     def __init__(self, shape, dtype: str = "float32"):
         if dtype not in DTYPES:
@@ -50,6 +51,7 @@ class DeviceTensor:
         self.ptr = p
         self._owned = True
         self.absmax_parts = None
+        self._base = None
 
     # -- construction -----------------------------------------------------
     @classmethod
@@ -92,7 +94,39 @@ class DeviceTensor:
             raise ValueError(f"reshape: cannot view {self.shape} as {shape}")
         v = object.__new__(DeviceTensor)
         v.ptr, v.shape, v.dtype, v.nbytes, v._owned = self.ptr, shape, self.dtype, self.nbytes, False
+        v.absmax_parts, v._base = None, self
         return v
+
+    def view(self, offset: int, shape) -> "DeviceTensor":
+        """A view of elements [offset, offset + prod(shape)) of this buffer,
+        in the given shape (the view does not own the memory and keeps this
+        tensor alive)."""
+        shape = [int(s) for s in shape]
+        n = math.prod(shape)
+        if offset < 0 or offset + n > self.numel():
+            raise ValueError(f"view: elements [{offset}, {offset + n}) outside a tensor of {self.numel()}")
+        item = np.dtype(DTYPES[self.dtype]).itemsize
+        v = object.__new__(DeviceTensor)
+        v.ptr = ctypes.c_void_p(self.addr + offset * item)
+        v.shape, v.dtype, v.nbytes, v._owned = shape, self.dtype, n * item, False
+        v.absmax_parts, v._base = None, self
+        return v
+
+    def copy_from(self, src) -> None:
+        """Overwrites this buffer with `src` (a DeviceTensor of the same dtype
+        and element count: a stream-ordered device copy; or a host array:
+        a synchronous upload)."""
+        if isinstance(src, DeviceTensor):
+            if src.dtype != self.dtype or src.numel() != self.numel():
+                raise ValueError(f"copy_from: {src} does not match {self}")
+            if self.nbytes:
+                N.call("kh_memcpy_d2d", self.ptr, src.ptr, self.nbytes)
+            return
+        a = as_host_array(src, self.dtype)
+        if a.size != self.numel():
+            raise ValueError(f"copy_from: {a.size} elements do not match {self}")
+        if self.nbytes:
+            N.call("kh_memcpy_h2d", self.ptr, ctypes.c_void_p(a.ctypes.data), self.nbytes)
 
     def release(self):
         """Returns the buffer to the pool (idempotent)."""

@@ -164,6 +164,22 @@ class QLinear:
         b = getattr(linear, "bias", None)
         self.bias = to_device(b, "float32") if b is not None else None
 
+    def named_parameters(self):
+        """The reference Linear's names (nn.py:77-78): the weight as its int8
+        QTensor, the bias as float32."""
+        yield "weight", self.qweight
+        if self.bias is not None:
+            yield "bias", self.bias
+
+    def set_parameter(self, name: str, value) -> None:
+        """In-place load (kansaiml_amd.serialize): a float32 weight is
+        quantized with this layer's weight granularity."""
+        from .serialize import assign_in_place
+        target = dict(self.named_parameters()).get(name)
+        if target is None:
+            raise KeyError(name)
+        assign_in_place(name, target, value)
+
     def __call__(self, x):
         from .kir import TraceValue
         if isinstance(x, TraceValue):
