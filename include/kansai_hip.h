@@ -180,6 +180,19 @@ int kh_gemm_i8_ex(const int8_t* a, const int8_t* b_packed, int64_t M, int64_t N,
                   const float* bias, int act, const float* residual, float* out,
                   unsigned* absmax_parts, int max_parts, int* nparts);
 
+/* kh_gemm_i8_ex's fp32 result quantized per tensor, as kh_quantize_tensor
+ * would quantize it (quantize.py:50-70 on the output of qlinear and the
+ * pre-LN block's GELU / residual, nn.py:466-478), without the fp32 result
+ * ever being written: codes int8 [M, N] into q, the binary64 scale into
+ * *scale.  Two passes over the GEMM (absmax, then quantize), which is the
+ * cheaper order when the fp32 output would be read again only to be
+ * quantized (the graph's fc1 -> GELU -> quantize).  Uses the library's
+ * scratch area; a NaN/inf result reports KH_ERR_NONFINITE at the next
+ * synchronize, as kh_quantize_tensor does. */
+int kh_gemm_i8_quant(const int8_t* a, const int8_t* b_packed, int64_t M, int64_t N, int64_t K,
+                     const double* sa, int sa_per_row, const double* sb, int sb_per_col,
+                     const float* bias, int act, const float* residual, int8_t* q, double* scale);
+
 /* Per-token activation quantize fused into the GEMM's producer: x fp32
  * [M, K] is quantized per row into q_scratch (int8 [M, K]) and
  * sx_scratch (binary64 [M]), then kh_gemm_i8 runs with sa = sx_scratch
@@ -235,6 +248,14 @@ int kh_layernorm(const float* x, int64_t rows, int D, const float* weight, const
 /* ... also writing absmax partials of out (see kh_absmax_parts). */
 int kh_layernorm_ex(const float* x, int64_t rows, int D, const float* weight, const float* bias, float eps,
                     float* out, unsigned* absmax_parts, int max_parts, int* nparts);
+/* LayerNorm followed by the per-tensor quantize of its output
+ * (quantize.py:50-70 on nn.LayerNorm's result, the pre-LN block's
+ * x -> ln -> Linear input, nn.py:466-478), without writing the fp32
+ * output: two passes over x (absmax, then quantize), codes int8
+ * [rows, D] into q and the binary64 scale into *scale.  Codes equal
+ * kh_quantize_tensor of kh_layernorm's output bit for bit. */
+int kh_layernorm_quant(const float* x, int64_t rows, int D, const float* weight, const float* bias, float eps,
+                       int8_t* q, double* scale);
 
 /* Exact-erf GELU (backend/cpu/src/Ops.cpp:250-256). */
 int kh_gelu(const float* x, float* out, int64_t n);

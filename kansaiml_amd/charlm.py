@@ -111,8 +111,12 @@ class CharLM:
     one (or a float32 checkpoint, quantized per output channel on the way)
     into it in place.  `w` stays the construction-time weights."""
 
-    def __init__(self, w: CharLMWeights):
+    def __init__(self, w: CharLMWeights, producer_quant: bool = False):
+        """producer_quant: LayerNorm and fc1 (-> GELU) emit their int8 codes
+        directly instead of fp32 (kir.quant_fusion's option; less memory,
+        not faster)."""
         self.w = w
+        self.producer_quant = producer_quant
         up = DeviceTensor.from_host
         self.tok, self.pos = up(w.tok), up(w.pos)
         self.blocks = []
@@ -175,7 +179,8 @@ class CharLM:
     def graph(self, batch, seq):
         key = (batch, seq)
         if key not in self._graphs:
-            g = kir.quant_fusion(kir.trace(self._fn(batch, seq), np.zeros((batch, seq), np.int32)))
+            g = kir.quant_fusion(kir.trace(self._fn(batch, seq), np.zeros((batch, seq), np.int32)),
+                                 producer_quant=self.producer_quant)
             self._graphs[key] = (g, kir.plan_memory(g))
         return self._graphs[key]
 

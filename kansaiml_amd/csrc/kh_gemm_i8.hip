@@ -45,6 +45,13 @@ struct Epilogue {
     int sb_per_col;
     int act;                // kActNone or kActGelu, applied after the bias
     const float* residual;  // [M, N]: out = residual + y (the graph's x.add(linear(..)))
+    // Output mode kOutQuant (the fp32 result quantized per tensor, never
+    // stored): codes [M, N], the pass-1 absmax partials, the scale's slot.
+    int8_t* q;
+    const unsigned* qparts;
+    int nqparts;
+    double* qscale;
+    unsigned* fault;
 };
 
 constexpr int kActNone = 0;
@@ -90,9 +97,9 @@ __device__ __forceinline__ void epilogue_store(const Epilogue& ep, int64_t i, in
 // left after a store would wait for it (one memory round trip per element
 // instead of one per group).  Returns the largest |out| bits stored (for the
 // absmax partials of a following per-tensor quantize).
-template <bool FUSED, int RG, bool MASKED>
+template <bool FUSED, int RG, bool MASKED, int MODE>
 __device__ __forceinline__ unsigned store_block32_impl(const Epilogue& ep, int64_t i0, int64_t j, int64_t M,
-                                                       int64_t N, const i32x16& v) {
+                                                       int64_t N, const i32x16& v, const kh::quant::Scale& sc) {
     static_assert(16 % RG == 0, "residual group");
     if (MASKED && j >= N) return 0;
     const double sbj = ep.sb ? ep.sb[ep.sb_per_col ? j : 0] : 0.0;
@@ -113,6 +120,15 @@ __device__ __forceinline__ unsigned store_block32_impl(const Epilogue& ep, int64
             const int r = g0 + rr;
             const int64_t i = i0 + 8 * (r >> 2) + (r & 3);
             if (MASKED && i >= M) continue;
+            if (MODE != kh::quant::kOutStore) {
+                // The value the fp32 epilogue would store: its absmax
+                // (pass 1) or its per-tensor code (pass 2).
+                const double s = ep.sa_per_row ? ep.sa[i] * sbj : sa0;
+                const float y = epilogue_finish<FUSED>(ep, v[r], s, bj, res[rr]);
+                mx = max(mx, kh::abs_bits32(y));
+                if (MODE == kh::quant::kOutQuant) ep.q[i * N + j] = (int8_t)kh::quant::quant_one(y, sc);
+                continue;
+            }
             if (ep.acc) ep.acc[i * N + j] = v[r];
             if (ep.out) {
                 const double s = ep.sa_per_row ? ep.sa[i] * sbj : sa0;
@@ -125,17 +141,17 @@ __device__ __forceinline__ unsigned store_block32_impl(const Epilogue& ep, int64
     return mx;
 }
 
-template <bool FUSED = true, int RG = 16>
+template <bool FUSED = true, int RG = 16, int MODE = kh::quant::kOutStore>
 __device__ __forceinline__ unsigned store_block32(const Epilogue& ep, int64_t i0, int64_t j, int64_t N,
-                                                  const i32x16& v) {
-    return store_block32_impl<FUSED, RG, false>(ep, i0, j, 0, N, v);
+                                                  const i32x16& v, const kh::quant::Scale& sc) {
+    return store_block32_impl<FUSED, RG, false, MODE>(ep, i0, j, 0, N, v, sc);
 }
 
 // store_block32 for a block that may extend past row M or column N.
-template <bool FUSED = true, int RG = 16>
+template <bool FUSED = true, int RG = 16, int MODE = kh::quant::kOutStore>
 __device__ __forceinline__ unsigned store_block32_masked(const Epilogue& ep, int64_t i0, int64_t j, int64_t M,
-                                                         int64_t N, const i32x16& v) {
-    return store_block32_impl<FUSED, RG, true>(ep, i0, j, M, N, v);
+                                                         int64_t N, const i32x16& v, const kh::quant::Scale& sc) {
+    return store_block32_impl<FUSED, RG, true, MODE>(ep, i0, j, M, N, v, sc);
 }
 
 template <int BM, int BN, int BK, int WM, int WN>
@@ -353,7 +369,7 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, void* dst, i
 // FUSED: the epilogue may apply an activation and a residual add.  Waves per
 // SIMD: 2 for 256-wide N tiles (128 accumulators per wave), 4 otherwise (two
 // resident workgroups per CU within the 128-register budget).
-template <int BM, int BN, int NS, bool FUSED>
+template <int BM, int BN, int NS, bool FUSED, int MODE = kh::quant::kOutStore>
 __global__ __launch_bounds__(512, BN == 256 ? 2 : 4) void gemm_i8_pingpong_kernel(
     const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, int N, int K, int group_m, Epilogue ep,
     unsigned* parts) {
@@ -371,6 +387,18 @@ __global__ __launch_bounds__(512, BN == 256 ? 2 : 4) void gemm_i8_pingpong_kerne
     constexpr int kResidRows = (BM == 256 && BN == 128) ? 4 : 16;
     static_assert(NS >= 3 && NS <= 5, "wait_loads_beyond covers up to 3 stages ahead");
     __shared__ __attribute__((aligned(1024))) int8_t lds[NS * kStage];
+
+    // kOutQuant: the tensor's scale from the pass-1 partials, before the
+    // pipeline starts (workgroup 0 stores it for the caller).
+    kh::quant::Scale sc{};
+    if constexpr (MODE == kh::quant::kOutQuant) {
+        __shared__ unsigned qred[kWaves];
+        sc = kh::quant::make_scale(kh::quant::block_reduce_partials(ep.qparts, ep.nqparts, qred));
+        if (blockIdx.x == 0 && threadIdx.x == 0) {
+            *ep.qscale = sc.s;
+            if (sc.bad) kh::quant::flag_nonfinite(ep.fault);
+        }
+    }
 
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     int tm, tn;
@@ -481,7 +509,8 @@ __global__ __launch_bounds__(512, BN == 256 ? 2 : 4) void gemm_i8_pingpong_kerne
         for (int a = 0; a < kTM; ++a)
 #pragma unroll
             for (int b = 0; b < kTN; ++b) {
-                mx = max(mx, store_block32<FUSED, kResidRows>(ep, row_base + a * 32, col_base + b * 32, N, acc[a][b]));
+                mx = max(mx, store_block32<FUSED, kResidRows, MODE>(ep, row_base + a * 32, col_base + b * 32, N,
+                                                                    acc[a][b], sc));
                 __builtin_amdgcn_sched_barrier(0);
             }
     } else {
@@ -489,11 +518,12 @@ __global__ __launch_bounds__(512, BN == 256 ? 2 : 4) void gemm_i8_pingpong_kerne
         for (int a = 0; a < kTM; ++a)
 #pragma unroll
             for (int b = 0; b < kTN; ++b) {
-                mx = max(mx, store_block32_masked<FUSED, kResidRows>(ep, row_base + a * 32, col_base + b * 32, M, N, acc[a][b]));
+                mx = max(mx, store_block32_masked<FUSED, kResidRows, MODE>(ep, row_base + a * 32, col_base + b * 32,
+                                                                           M, N, acc[a][b], sc));
                 __builtin_amdgcn_sched_barrier(0);
             }
     }
-    if (parts) {
+    if (MODE != kh::quant::kOutQuant && parts) {
         // Per-workgroup max |out| bits, for a following per-tensor quantize.
         unsigned* wmax = reinterpret_cast<unsigned*>(lds);  // every stage's last reader passed the final barrier
         mx = kh::quant::wave_max(mx);
@@ -675,9 +705,21 @@ int launch_skinny(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, in
 
 template <int BM, int BN, int NS>
 int launch_pingpong_cfg(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
-                        const Epilogue& ep, unsigned* parts, int* nparts) {
+                        const Epilogue& ep, unsigned* parts, int* nparts, int mode) {
+    using namespace kh::quant;
     const unsigned tiles = (unsigned)(((M + BM - 1) / BM) * ((N + BN - 1) / BN));
-    if (ep.act != kActNone || ep.residual)
+    if constexpr (BM == 128 && BN == 128) {
+        if (mode == kOutMaxOnly)
+            gemm_i8_pingpong_kernel<BM, BN, NS, true, kOutMaxOnly>
+                <<<tiles, 512, 0, d->stream>>>(A, B, (int)M, (int)N, (int)K, 8, ep, parts);
+        else if (mode == kOutQuant)
+            gemm_i8_pingpong_kernel<BM, BN, NS, true, kOutQuant>
+                <<<tiles, 512, 0, d->stream>>>(A, B, (int)M, (int)N, (int)K, 8, ep, nullptr);
+    }
+    if (mode != kOutStore) {
+        // The quantize passes exist for the 128x128 tile only (launch_pingpong
+        // routes them there; in the 256-row tiles the pass-1 epilogue spills).
+    } else if (ep.act != kActNone || ep.residual)
         gemm_i8_pingpong_kernel<BM, BN, NS, true>
             <<<tiles, 512, 0, d->stream>>>(A, B, (int)M, (int)N, (int)K, 8, ep, parts);
     else
@@ -691,18 +733,21 @@ int launch_pingpong_cfg(kh::Device* d, const int8_t* A, const int8_t* B, int64_t
 // the smallest tile otherwise.  Short K (<= 512: a handful of K-steps, where
 // writing the fp32 tile dominates) takes 128x128 tiles, several resident per
 // CU, so one workgroup's epilogue overlaps another's main loop.  Short K gets
-// a 3-stage ring.
+// a 3-stage ring.  The two passes of a fused quantize (mode kOutMaxOnly,
+// then kOutQuant) both take 128x128 tiles.
 int launch_pingpong(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
-                    const Epilogue& ep, unsigned* parts = nullptr, int* nparts = nullptr) {
+                    const Epilogue& ep, unsigned* parts = nullptr, int* nparts = nullptr,
+                    int mode = kh::quant::kOutStore) {
     auto tiles = [&](int64_t bm, int64_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
     const int64_t want = (int64_t)d->cus * 3 / 2;
-    if (K <= 512) return launch_pingpong_cfg<128, 128, 3>(d, A, B, M, N, K, ep, parts, nparts);
+    if (K <= 512 || mode != kh::quant::kOutStore)
+        return launch_pingpong_cfg<128, 128, 3>(d, A, B, M, N, K, ep, parts, nparts, mode);
     if (tiles(256, 256) >= want) {
-        if (K >= 1024) return launch_pingpong_cfg<256, 256, 4>(d, A, B, M, N, K, ep, parts, nparts);
-        return launch_pingpong_cfg<256, 256, 3>(d, A, B, M, N, K, ep, parts, nparts);
+        if (K >= 1024) return launch_pingpong_cfg<256, 256, 4>(d, A, B, M, N, K, ep, parts, nparts, mode);
+        return launch_pingpong_cfg<256, 256, 3>(d, A, B, M, N, K, ep, parts, nparts, mode);
     }
-    if (tiles(256, 128) >= want) return launch_pingpong_cfg<256, 128, 3>(d, A, B, M, N, K, ep, parts, nparts);
-    return launch_pingpong_cfg<128, 128, 3>(d, A, B, M, N, K, ep, parts, nparts);
+    if (tiles(256, 128) >= want) return launch_pingpong_cfg<256, 128, 3>(d, A, B, M, N, K, ep, parts, nparts, mode);
+    return launch_pingpong_cfg<128, 128, 3>(d, A, B, M, N, K, ep, parts, nparts, mode);
 }
 
 // True when the ping-pong kernel applies to this shape (any M and N; K a
@@ -928,6 +973,49 @@ int kh_gemm_i8_ex(const int8_t* a, const int8_t* b_packed, int64_t M, int64_t N,
                   float* out, unsigned* absmax_parts, int max_parts, int* nparts) {
     return gemm_i8_impl(a, b_packed, M, N, K, sa, sa_per_row, sb, sb_per_col, bias, out, nullptr, act, residual,
                         absmax_parts, max_parts, nparts);
+}
+
+int kh_gemm_i8_quant(const int8_t* a, const int8_t* b_packed, int64_t M, int64_t N, int64_t K, const double* sa,
+                     int sa_per_row, const double* sb, int sb_per_col, const float* bias, int act,
+                     const float* residual, int8_t* q, double* scale) {
+    KH_REQUIRE(M >= 0 && N >= 0 && K >= 0, "kh_gemm_i8_quant: negative shape");
+    KH_REQUIRE(K <= 133144, "kh_gemm_i8_quant: K > 133144 could overflow the int32 accumulator");
+    KH_REQUIRE(M <= 0xFFFFLL * 128 && N <= 0x7FFFFFFFLL, "kh_gemm_i8_quant: shape too large");
+    KH_REQUIRE(act == kActNone || act == kActGelu, "kh_gemm_i8_quant: unknown activation");
+    KH_REQUIRE(scale, "kh_gemm_i8_quant: null scale");
+    KH_DEVICE_OR_RETURN(d);
+    if (M == 0 || N == 0) {
+        const double one = 1.0;  // the reference's quantize of an empty tensor
+        return kh_memcpy_h2d(scale, &one, sizeof(one));
+    }
+    KH_REQUIRE(q && sa && sb && (K == 0 || (a && b_packed)), "kh_gemm_i8_quant: null pointer");
+    if (pingpong_fits(a, b_packed, M, N, K) && !skinny_fits(a, b_packed, M, N, K)) {
+        // Pass 1: the epilogue's values reduced to one absmax partial per
+        // workgroup, nothing stored.  Pass 2: the same GEMM and epilogue
+        // (so the same values), quantized with the scale of those partials;
+        // the fp32 result never reaches memory.
+        const int64_t worst = ((M + 127) / 128) * ((N + 127) / 128);
+        auto* parts = static_cast<unsigned*>(kh::scratch(d, (size_t)worst * sizeof(unsigned)));
+        if (!parts) return KH_ERR_OOM;
+        Epilogue ep{sa, sb, bias, nullptr, nullptr, sa_per_row, sb_per_col, act, residual,
+                    q, parts, 0, scale, d->fault};
+        int nparts = 0;
+        int rc = launch_pingpong(d, a, b_packed, M, N, K, ep, parts, &nparts, kh::quant::kOutMaxOnly);
+        if (rc) return rc;
+        ep.nqparts = nparts;
+        return launch_pingpong(d, a, b_packed, M, N, K, ep, nullptr, nullptr, kh::quant::kOutQuant);
+    }
+    // Other shapes: the fp32 result through a pooled temporary, then the
+    // per-tensor quantize.
+    void* tmp = nullptr;
+    int rc = kh_alloc((size_t)(M * N) * sizeof(float), &tmp);
+    if (rc) return rc;
+    float* out = static_cast<float*>(tmp);
+    rc = gemm_i8_impl(a, b_packed, M, N, K, sa, sa_per_row, sb, sb_per_col, bias, out, nullptr, act, residual,
+                      nullptr, 0, nullptr);
+    if (!rc) rc = kh_quantize_tensor(out, M * N, q, scale);
+    kh_free(tmp);  // stream-ordered reuse: later work is queued behind the quantize
+    return rc;
 }
 
 int kh_linear_i8(const float* x, int64_t M, int64_t K, const int8_t* b_packed, int64_t N, const double* sb,

@@ -163,28 +163,6 @@ __global__ __launch_bounds__(256) void absmax_partials_kernel(const float* __res
     if (threadIdx.x == 0) partials[blockIdx.x] = max(max(red[0], red[1]), max(red[2], red[3]));
 }
 
-// Reduces partials[0..count) across the block; every thread gets the max.
-__device__ __forceinline__ unsigned block_reduce_partials(const unsigned* __restrict__ partials, int count,
-                                                          unsigned* red) {
-    // Eight independent loads in flight per thread (the partials are L2
-    // resident; a dependent chain of loads would be latency-bound).
-    unsigned m8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    const int step = blockDim.x;
-    int i = threadIdx.x;
-    for (; i + 7 * step < count; i += 8 * step) {
-#pragma unroll
-        for (int u = 0; u < 8; ++u) m8[u] = max(m8[u], partials[i + u * step]);
-    }
-    for (; i < count; i += step) m8[0] = max(m8[0], partials[i]);
-    unsigned mb = max(max(max(m8[0], m8[1]), max(m8[2], m8[3])), max(max(m8[4], m8[5]), max(m8[6], m8[7])));
-    mb = wave_max(mb);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x / 64] = mb;
-    __syncthreads();
-    mb = red[0];
-    for (int i = 1; i < (int)(blockDim.x / 64); ++i) mb = max(mb, red[i]);
-    return mb;
-}
-
 template <bool VEC>
 __global__ __launch_bounds__(256) void quant_tensor_kernel(const float* __restrict__ x, int64_t n,
                                                            int8_t* __restrict__ q, double* __restrict__ scale,

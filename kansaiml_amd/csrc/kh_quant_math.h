@@ -135,5 +135,38 @@ __device__ __forceinline__ unsigned pack4(f32x4 v, const Scale& sc) {
     return pack4_checked(v, sc);
 }
 
+// Reduces per-workgroup absmax partials[0..count) across the block (any
+// multiple of 64 threads up to 1024; `red` holds blockDim.x / 64 words of
+// LDS); every thread gets the max bits.
+__device__ __forceinline__ unsigned block_reduce_partials(const unsigned* __restrict__ partials, int count,
+                                                          unsigned* red) {
+    // Eight independent loads in flight per thread (the partials are L2
+    // resident; a dependent chain of loads would be latency-bound).
+    unsigned m8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    const int step = blockDim.x;
+    int i = threadIdx.x;
+    for (; i + 7 * step < count; i += 8 * step) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) m8[u] = max(m8[u], partials[i + u * step]);
+    }
+    for (; i < count; i += step) m8[0] = max(m8[0], partials[i]);
+    unsigned mb = max(max(max(m8[0], m8[1]), max(m8[2], m8[3])), max(max(m8[4], m8[5]), max(m8[6], m8[7])));
+    mb = wave_max(mb);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x / 64] = mb;
+    __syncthreads();
+    mb = red[0];
+    for (int i = 1; i < (int)(blockDim.x / 64); ++i) mb = max(mb, red[i]);
+    return mb;
+}
+
+// What a kernel producing the input of a per-tensor quantize does with each
+// value it computes: store it (fp32), only reduce its absmax into the
+// workgroup's partial (pass 1 of a fused producer + quantize), or quantize
+// it with the scale reduced from those partials and store the int8 code
+// (pass 2: the fp32 tensor is never written).
+constexpr int kOutStore = 0;
+constexpr int kOutMaxOnly = 1;
+constexpr int kOutQuant = 2;
+
 }  // namespace quant
 }  // namespace kh

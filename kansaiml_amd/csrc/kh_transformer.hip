@@ -20,6 +20,10 @@
 
 #include "kh_common.h"
 #include "kh_act.h"
+#include "kh_quant_math.h"
+// kh_quant_math.h turns FP contraction off for the exact quantize arithmetic
+// it defines; the fp32 kernels of this file keep the compiler's default.
+#pragma clang fp contract(fast)
 
 namespace {
 
@@ -65,13 +69,18 @@ __device__ __forceinline__ unsigned block4_max(unsigned v, unsigned* wmax) {
 
 // One row of LayerNorm by one wave; returns this lane's largest |out| bits.
 // VEC: D % 4 == 0 and 16-byte aligned rows, lanes hold float4s (D <= 1024).
-template <bool VEC>
+// MODE (kh::quant::kOut*): store the fp32 row to `out`, only reduce its
+// absmax, or store its int8 codes under scale `sc` to `q`.
+template <bool VEC, int MODE>
 __device__ __forceinline__ unsigned layernorm_row(const float* __restrict__ x, int64_t row, int D,
                                                   const float* __restrict__ w, const float* __restrict__ b, float eps,
-                                                  float* __restrict__ out, int lane) {
+                                                  float* __restrict__ out, int8_t* __restrict__ q,
+                                                  const kh::quant::Scale& sc, int lane) {
+    using namespace kh::quant;
     typedef float f4 __attribute__((ext_vector_type(4)));
     const float* xr = x + row * D;
     float* orow = out + row * D;
+    int8_t* qrow = q + row * D;
     unsigned mx = 0;
     if (VEC) {
         constexpr int kV = kLnMaxPerLane / 4;  // float4 per lane
@@ -105,7 +114,8 @@ __device__ __forceinline__ unsigned layernorm_row(const float* __restrict__ x, i
                     y[e] = v[i][e] / denom * wv[e] + bv[e];
                     mx = max(mx, kh::abs_bits32(y[e]));
                 }
-                reinterpret_cast<f4*>(orow)[c4] = y;
+                if (MODE == kOutStore) reinterpret_cast<f4*>(orow)[c4] = y;
+                if (MODE == kOutQuant) reinterpret_cast<unsigned*>(qrow)[c4] = pack4(y, sc);
             }
         }
         return mx;
@@ -134,7 +144,8 @@ __device__ __forceinline__ unsigned layernorm_row(const float* __restrict__ x, i
         const int c = lane + i * 64;
         if (c < D) {
             const float y = v[i] / denom * w[c] + b[c];
-            orow[c] = y;
+            if (MODE == kOutStore) orow[c] = y;
+            if (MODE == kOutQuant) qrow[c] = (int8_t)quant_one(y, sc);
             mx = max(mx, kh::abs_bits32(y));
         }
     }
@@ -143,22 +154,35 @@ __device__ __forceinline__ unsigned layernorm_row(const float* __restrict__ x, i
 
 // A 256-thread workgroup normalizes kLnRowsPerBlock rows, each wave one row
 // at a time, and (when parts is given) writes the max |out| of its rows.
+// MODE kOutQuant first reduces the pass-1 partials qparts[0..nqparts) to the
+// tensor's scale (workgroup 0 stores it to *qscale).
 constexpr int kLnRowsPerBlock = 16;
 
-template <bool VEC>
+template <bool VEC, int MODE>
 __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict__ x, int64_t rows, int D,
                                                         const float* __restrict__ w, const float* __restrict__ b,
                                                         float eps, float* __restrict__ out,
-                                                        unsigned* __restrict__ parts) {
+                                                        unsigned* __restrict__ parts, int8_t* __restrict__ q,
+                                                        const unsigned* __restrict__ qparts, int nqparts,
+                                                        double* __restrict__ qscale, unsigned* __restrict__ fault) {
+    using namespace kh::quant;
     __shared__ unsigned wmax[4];
     const int lane = threadIdx.x & 63;
+    Scale sc{};
+    if (MODE == kOutQuant) {
+        sc = make_scale(block_reduce_partials(qparts, nqparts, wmax));
+        if (blockIdx.x == 0 && threadIdx.x == 0) {
+            *qscale = sc.s;
+            if (sc.bad) flag_nonfinite(fault);
+        }
+    }
     unsigned mx = 0;
 #pragma unroll 1
     for (int k = threadIdx.x >> 6; k < kLnRowsPerBlock; k += 4) {
         const int64_t row = (int64_t)blockIdx.x * kLnRowsPerBlock + k;
-        if (row < rows) mx = max(mx, layernorm_row<VEC>(x, row, D, w, b, eps, out, lane));
+        if (row < rows) mx = max(mx, layernorm_row<VEC, MODE>(x, row, D, w, b, eps, out, q, sc, lane));
     }
-    if (parts) {
+    if (MODE != kOutQuant && parts) {
         // Per-workgroup max |out| bits, for a following per-tensor quantize.
         mx = block4_max(mx, wmax);
         if (threadIdx.x == 0) parts[blockIdx.x] = mx;
@@ -377,12 +401,14 @@ int kh_layernorm_ex(const float* x, int64_t rows, int D, const float* weight, co
     const bool fused = absmax_parts && blocks <= max_parts;
     const bool vec = D % 4 == 0 && kh::aligned(x, 16) && kh::aligned(out, 16) && kh::aligned(weight, 16) &&
                      kh::aligned(bias, 16);
+    using kh::quant::kOutStore;
+    unsigned* parts = fused ? absmax_parts : nullptr;
     if (vec)
-        layernorm_kernel<true><<<(unsigned)blocks, 256, 0, d->stream>>>(x, rows, D, weight, bias, eps, out,
-                                                                        fused ? absmax_parts : nullptr);
+        layernorm_kernel<true, kOutStore><<<(unsigned)blocks, 256, 0, d->stream>>>(
+            x, rows, D, weight, bias, eps, out, parts, nullptr, nullptr, 0, nullptr, d->fault);
     else
-        layernorm_kernel<false><<<(unsigned)blocks, 256, 0, d->stream>>>(x, rows, D, weight, bias, eps, out,
-                                                                         fused ? absmax_parts : nullptr);
+        layernorm_kernel<false, kOutStore><<<(unsigned)blocks, 256, 0, d->stream>>>(
+            x, rows, D, weight, bias, eps, out, parts, nullptr, nullptr, 0, nullptr, d->fault);
     int rc = kh::launch_status("layernorm");
     if (rc || !absmax_parts) return rc;
     if (fused) {
@@ -394,6 +420,43 @@ int kh_layernorm_ex(const float* x, int64_t rows, int D, const float* weight, co
 
 int kh_layernorm(const float* x, int64_t rows, int D, const float* weight, const float* bias, float eps, float* out) {
     return kh_layernorm_ex(x, rows, D, weight, bias, eps, out, nullptr, 0, nullptr);
+}
+
+int kh_layernorm_quant(const float* x, int64_t rows, int D, const float* weight, const float* bias, float eps,
+                       int8_t* q, double* scale) {
+    KH_REQUIRE(rows >= 0 && D > 0, "kh_layernorm_quant: bad shape");
+    KH_REQUIRE(D <= 64 * kLnMaxPerLane, "kh_layernorm_quant: rows longer than 1024 are not supported");
+    KH_REQUIRE(scale, "kh_layernorm_quant: null scale");
+    KH_DEVICE_OR_RETURN(d);
+    if (rows == 0) {
+        // The reference's quantize of an empty tensor: max 0, scale 1.0.
+        const double one = 1.0;
+        return kh_memcpy_h2d(scale, &one, sizeof(one));
+    }
+    KH_REQUIRE(x && weight && bias && q, "kh_layernorm_quant: null pointer");
+    const int64_t blocks = (rows + kLnRowsPerBlock - 1) / kLnRowsPerBlock;
+    KH_REQUIRE(blocks <= 0x7FFFFFFFLL, "kh_layernorm_quant: too many rows");
+    auto* parts = static_cast<unsigned*>(kh::scratch(d, (size_t)blocks * sizeof(unsigned)));
+    if (!parts) return KH_ERR_OOM;
+    const bool vec = D % 4 == 0 && kh::aligned(x, 16) && kh::aligned(q, 4) && kh::aligned(weight, 16) &&
+                     kh::aligned(bias, 16);
+    using kh::quant::kOutMaxOnly;
+    using kh::quant::kOutQuant;
+    // Pass 1 reduces the normalized values' absmax into one partial per
+    // workgroup without storing them; pass 2 recomputes them (the same
+    // arithmetic, so the same values) and stores their codes.
+    if (vec) {
+        layernorm_kernel<true, kOutMaxOnly><<<(unsigned)blocks, 256, 0, d->stream>>>(
+            x, rows, D, weight, bias, eps, nullptr, parts, nullptr, nullptr, 0, nullptr, d->fault);
+        layernorm_kernel<true, kOutQuant><<<(unsigned)blocks, 256, 0, d->stream>>>(
+            x, rows, D, weight, bias, eps, nullptr, nullptr, q, parts, (int)blocks, scale, d->fault);
+    } else {
+        layernorm_kernel<false, kOutMaxOnly><<<(unsigned)blocks, 256, 0, d->stream>>>(
+            x, rows, D, weight, bias, eps, nullptr, parts, nullptr, nullptr, 0, nullptr, d->fault);
+        layernorm_kernel<false, kOutQuant><<<(unsigned)blocks, 256, 0, d->stream>>>(
+            x, rows, D, weight, bias, eps, nullptr, nullptr, q, parts, (int)blocks, scale, d->fault);
+    }
+    return kh::launch_status("layernorm_quant");
 }
 
 int kh_gelu(const float* x, float* out, int64_t n) {

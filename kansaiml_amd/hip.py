@@ -281,6 +281,46 @@ def gemm_i8_fused(a: DeviceTensor, b_packed: DeviceTensor, sa: DeviceTensor, sb:
     return out, parts
 
 
+def gemm_i8_quant(a: DeviceTensor, b_packed: DeviceTensor, sa: DeviceTensor, sb: DeviceTensor,
+                  bias: DeviceTensor | None = None, *, act: str | None = None,
+                  residual: DeviceTensor | None = None):
+    """quantize_tensor(gemm_i8_fused(...)) without writing the fp32 result:
+    returns (codes int8 [M, N], scale float64 [1])."""
+    _need(a, "int8", 2, "gemm_i8(a)")
+    _need(b_packed, "int8", 2, "gemm_i8(b)")
+    M, K = a.shape
+    Nn, K2 = b_packed.shape
+    if K != K2:
+        raise RuntimeError(f"gemm_i8: incompatible shapes {a.shape} x {b_packed.shape}^T")
+    if act not in ACTS:
+        raise ValueError(f"gemm_i8_quant: unknown activation {act!r}")
+    sa_mode = _scale_mode(sa, M, "gemm_i8(sa)")
+    sb_mode = _scale_mode(sb, Nn, "gemm_i8(sb)")
+    if bias is not None:
+        _need(bias, "float32", 1, "gemm_i8(bias)")
+        if bias.shape[0] != Nn:
+            raise RuntimeError("gemm_i8: bias must have N entries")
+    if residual is not None:
+        _need(residual, "float32", 2, "gemm_i8(residual)")
+        if list(residual.shape) != [M, Nn]:
+            raise RuntimeError("gemm_i8_quant: residual must be [M, N]")
+    q = DeviceTensor([M, Nn], "int8")
+    s = DeviceTensor([1], "float64")
+    N.call("kh_gemm_i8_quant", a.ptr, b_packed.ptr, M, Nn, K, sa.ptr, sa_mode, sb.ptr, sb_mode, _opt(bias),
+           ACTS[act], _opt(residual), q.ptr, s.ptr)
+    return q, s
+
+
+def layer_norm_quant(x: DeviceTensor, w: DeviceTensor, b: DeviceTensor, eps: float = 1e-5):
+    """quantize_tensor(layer_norm(x)) without writing the fp32 output:
+    returns (codes int8 like x, scale float64 [1])."""
+    _need(x, "float32", 2, "layer_norm(x)")
+    q = DeviceTensor(x.shape, "int8")
+    s = DeviceTensor([1], "float64")
+    N.call("kh_layernorm_quant", x.ptr, x.shape[0], x.shape[1], w.ptr, b.ptr, eps, q.ptr, s.ptr)
+    return q, s
+
+
 def layer_norm(x: DeviceTensor, w: DeviceTensor, b: DeviceTensor, eps: float = 1e-5, *, absmax: bool = False):
     """LayerNorm over the last axis (nn.py:308-331).  Returns (out, AbsmaxParts | None)."""
     _need(x, "float32", 2, "layer_norm(x)")

@@ -225,17 +225,26 @@ def _is_bias(graph, by_id, x_id, b_id) -> bool:
     return len(xs) == 2 and len(bs) == 1 and xs[1] == bs[0]
 
 
-def quant_fusion(graph) -> Graph:
+def quant_fusion(graph, producer_quant: bool = False) -> Graph:
     """Fuses, where the intermediate has no other user:
       int8_matmul -> dequantize [-> add(bias)] [-> gelu] [-> add(x, .)]
                                                  =>  int8_linear
       matmul -> add(bias)                        =>  matmul_bias
       add(bias) -> relu                          =>  fused_bias_relu
+    and, with producer_quant=True,
+      ... the int8_linear chain -> quantize (per tensor) => int8_linear_quant
+      layer_norm -> quantize (per tensor)        =>  layer_norm_quant
     int8_linear's attrs record what it absorbed: bias (bool), act ("gelu" or
-    None) and residual (bool; the residual operand comes last).  Then every
-    int8_linear, layer_norm or causal_attention whose output feeds a
-    per-tensor quantize is marked absmax=True: its kernel writes the absmax
-    partials that quantize needs, so the quantize reads its input once.
+    None) and residual (bool; the residual operand comes last).  The *_quant
+    nodes produce the quantized tensor directly: their kernels run the
+    producer twice (absmax, then codes) and never write the fp32 values.
+    That saves the fp32 intermediate's memory but not time on MI355X (the
+    GELU epilogue and LayerNorm are VALU- and latency-bound, so a second
+    pass costs more than the fp32 round trip it replaces), hence off by
+    default.  Then every int8_linear, layer_norm or causal_attention whose
+    output feeds a per-tensor quantize is marked absmax=True: its kernel
+    writes the absmax partials that quantize needs, so the quantize reads
+    its input once.
     The fused node takes the place of the last node of its pattern (every
     operand, e.g. a bias constant traced after the matmul, precedes it).
     Returns a new Graph; node order is preserved, ids are renumbered."""
@@ -249,8 +258,19 @@ def quant_fusion(graph) -> Graph:
     # Phase 1: find patterns.  fused[last] = (op, [operand ids], attrs);
     # absorbed nodes are dropped.
     fused, absorbed = {}, set()
+
+    def tensor_quantize(nid):
+        """The per-tensor quantize that is the only user of nid, if any (and
+        producer fusion is on)."""
+        if not producer_quant:
+            return None
+        q = only_user(nid)
+        if q is not None and by_id[q].op == "quantize" and by_id[q].attrs.get("granularity", "tensor") == "tensor":
+            return q
+        return None
+
     for n in graph.nodes:
-        if n.id in absorbed:
+        if n.id in absorbed or n.id in fused:
             continue
         if n.op == "int8_matmul":
             dq = only_user(n.id)
@@ -277,8 +297,19 @@ def quant_fusion(graph) -> Graph:
                         ins.append(other)
                         attrs["residual"] = True
                 last = chain[-1]
-                absorbed.update(set(chain) - {last})
-                fused[last] = ("int8_linear", ins, attrs)
+                q = tensor_quantize(last)
+                if q is not None:
+                    absorbed.update(chain)
+                    fused[q] = ("int8_linear_quant", ins, attrs)
+                else:
+                    absorbed.update(set(chain) - {last})
+                    fused[last] = ("int8_linear", ins, attrs)
+                continue
+        if n.op == "layer_norm":
+            q = tensor_quantize(n.id)
+            if q is not None:
+                absorbed.add(n.id)
+                fused[q] = ("layer_norm_quant", list(n.inputs), dict(n.attrs))
                 continue
         if n.op == "matmul":
             ad = only_user(n.id)
@@ -301,7 +332,8 @@ def quant_fusion(graph) -> Graph:
             continue
         if n.id in fused:
             op, ins, attrs = fused[n.id]
-            nid = out.add(op, [remap[i] for i in ins], n.shape, "float32", **attrs)
+            dtype = n.dtype if op.endswith("_quant") else "float32"
+            nid = out.add(op, [remap[i] for i in ins], n.shape, dtype, **attrs)
         else:
             nid = out.add(n.op, [remap[i] for i in n.inputs], n.shape, n.dtype, **n.attrs)
         remap[n.id] = nid
@@ -477,6 +509,19 @@ def _exec(node, vals):
             return _with_parts(out, parts)
         out, _ = H.gemm_i8(a, b, sa, sb, bias)
         return out
+    if op == "int8_linear_quant":
+        from .quantize import QTensor
+        a, b, sa, sb = _int8_operands(ins[0], ins[1], "int8_linear_quant")
+        at = node.attrs
+        bias = ins[2] if at.get("bias") else None
+        residual = ins[-1] if at.get("residual") else None
+        q, s = H.gemm_i8_quant(a, b, sa, sb, bias, act=at.get("act"), residual=residual)
+        return QTensor(q, s, list(node.shape), "tensor", packed=False)
+    if op == "layer_norm_quant":
+        from .quantize import QTensor
+        x, w, b = ins
+        q, s = H.layer_norm_quant(x, w, b, node.attrs.get("eps", 1e-5))
+        return QTensor(q, s, list(node.shape), "tensor", packed=False)
     if op == "embedding":
         ids, tok, pos = ins
         rows, D = node.shape

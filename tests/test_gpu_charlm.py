@@ -123,6 +123,37 @@ def _check_node(node, got, ins):
             np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
         else:
             np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+    elif op == "layer_norm_quant":
+        # the unfused composition on the same input: kh_layernorm (checked
+        # against the restatement as the layer_norm node is), then the
+        # oracle's per-tensor quantize -- bit for bit
+        from kansaiml_amd import hip as H
+        from kansaiml_amd.device import DeviceTensor as D
+        x, w, b = ins
+        y, _ = H.layer_norm(D.from_host(x), D.from_host(w), D.from_host(b), node.attrs.get("eps", 1e-5))
+        yh = y.numpy()
+        ref = R.layer_norm(x.astype(np.float64), w, b, node.attrs.get("eps", 1e-5))
+        assert np.abs(yh - ref).max() < 2e-5 * max(1.0, np.abs(ref).max())
+        q, s = O.ko_quantize_tensor(yh)
+        np.testing.assert_array_equal(got[0], q.reshape(got[0].shape))
+        assert got[1][0] == s
+    elif op == "int8_linear_quant":
+        # the unfused int8_linear on the same inputs (checked against the
+        # oracle as the int8_linear node is), then the oracle's quantize
+        from kansaiml_amd import hip as H
+        from kansaiml_amd.device import DeviceTensor as D
+        (qa, sa), (qw, sw) = ins[0], ins[1]
+        at = node.attrs
+        bias = ins[2] if at.get("bias") else None
+        residual = ins[-1] if at.get("residual") else None
+        y, _ = H.gemm_i8_fused(D.from_host(qa), D.from_host(qw), D.from_host(sa), D.from_host(sw),
+                               D.from_host(bias) if bias is not None else None, act=at.get("act"),
+                               residual=D.from_host(residual) if residual is not None else None)
+        yh = y.numpy()
+        _check_node(type("N", (), {"op": "int8_linear", "attrs": at})(), yh, ins)
+        q, s = O.ko_quantize_tensor(yh)
+        np.testing.assert_array_equal(got[0], q.reshape(got[0].shape))
+        assert got[1][0] == s
     elif op == "layer_norm":
         x, w, b = ins
         ref = R.layer_norm(x.astype(np.float64), w, b, node.attrs.get("eps", 1e-5))
@@ -139,8 +170,8 @@ def _check_node(node, got, ins):
         raise AssertionError(f"unchecked node kind {op}")
 
 
-@pytest.mark.parametrize("seq", [64, 100])
-def test_small_model_matches_restatement(G, seq):
+@pytest.mark.parametrize("seq,producer_quant", [(64, False), (100, False), (100, True)])
+def test_small_model_matches_restatement(G, seq, producer_quant):
     """Two layers of the C4 architecture (d 384, 6 heads, FFN 1536, vocab 65)
     with nonzero biases, checked node by node: every node's GPU output
     against the restatement of that node applied to the GPU's own inputs.
@@ -154,7 +185,7 @@ def test_small_model_matches_restatement(G, seq):
     from kansaiml_amd.charlm import CharLM, CharLMWeights
     w = CharLMWeights(layers=2, seq=128, seed=1, bias_std=0.02)
     ids = np.random.Generator(np.random.PCG64(2)).integers(0, 65, (2, seq)).astype(np.int32)
-    model = CharLM(w)
+    model = CharLM(w, producer_quant=producer_quant)
     seen = {}
     y = model(ids, observe=lambda node, v: seen.__setitem__(node.id, (node, _host(v))))
     assert y.shape == (2 * seq, 65)
@@ -167,12 +198,23 @@ def test_small_model_matches_restatement(G, seq):
         ins = [ids if by_id[i].op == "placeholder" else seen[i][1] for i in node.inputs]
         _check_node(node, got, ins)
         checked.add(node.op)
-    # GELU and the residual adds are fused into the int8_linear epilogues.
-    assert checked == {"embedding", "layer_norm", "quantize", "int8_linear", "causal_attention"}
-    acts = {(n.attrs.get("act"), bool(n.attrs.get("residual"))) for n in g.nodes if n.op == "int8_linear"}
-    assert acts == {(None, False), ("gelu", False), (None, True)}
-    assert all(n.attrs.get("absmax") for n in g.nodes
-               if n.op in ("layer_norm", "causal_attention") or (n.op == "int8_linear" and n.attrs.get("act")))
+    # GELU and the residual adds are fused into the int8_linear epilogues;
+    # per-tensor quantizes read absmax partials their producers wrote.  With
+    # producer_quant, every LayerNorm and fc1 (-> GELU) output feeds only a
+    # per-tensor quantize, so those producers emit the codes themselves.
+    acts = {(n.op, n.attrs.get("act"), bool(n.attrs.get("residual"))) for n in g.nodes
+            if n.op in ("int8_linear", "int8_linear_quant")}
+    if producer_quant:
+        assert checked == {"embedding", "layer_norm_quant", "quantize", "int8_linear", "int8_linear_quant",
+                           "causal_attention"}
+        assert acts == {("int8_linear", None, False), ("int8_linear_quant", "gelu", False),
+                        ("int8_linear", None, True)}
+        assert all(n.attrs.get("absmax") for n in g.nodes if n.op == "causal_attention")
+    else:
+        assert checked == {"embedding", "layer_norm", "quantize", "int8_linear", "causal_attention"}
+        assert acts == {("int8_linear", None, False), ("int8_linear", "gelu", False), ("int8_linear", None, True)}
+        assert all(n.attrs.get("absmax") for n in g.nodes
+                   if n.op in ("layer_norm", "causal_attention") or (n.op == "int8_linear" and n.attrs.get("act")))
     np.testing.assert_array_equal(seen[g.output][1].view(np.uint32), y.view(np.uint32))
     # and the int8 model stays near the fp32 one (quantization error)
     fp = R.forward(w, ids, quantized=False)

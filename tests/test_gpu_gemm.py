@@ -277,6 +277,90 @@ def test_gemm_i8_fused_epilogues(hip, M, N, K):
     assert s1.numpy()[0] == s2.numpy()[0]
 
 
+@pytest.mark.parametrize("M,N,K", [(16384, 1536, 384),   # C4 fc1: ping-pong, two passes
+                                   (300, 1152, 384),     # partial tiles
+                                   (1000, 1000, 1536),   # K > 512: the passes still take 128x128 tiles
+                                   (130, 70, 80),        # general kernel (K % 64 != 0): fp32 temporary
+                                   (8, 512, 512)])       # skinny kernel: fp32 temporary
+def test_gemm_i8_quant_matches_unfused(hip, M, N, K):
+    """kh_gemm_i8_quant's codes and scale equal the per-tensor quantize
+    (the oracle's, and kh_quantize_tensor's) of the unfused GEMM's fp32
+    output, for the plain, GELU and residual epilogues and per-row
+    activation scales."""
+    H, D = hip
+    gen = np.random.Generator(np.random.PCG64(M + 5 * N + 11 * K))
+    a = gen.integers(-127, 128, (M, K), dtype=np.int8)
+    bt = gen.integers(-127, 128, (N, K), dtype=np.int8)
+    sb = gen.uniform(1e-4, 1e-3, N)
+    bias = gen.standard_normal(N).astype(np.float32)
+    res = (gen.standard_normal((M, N)) * 4).astype(np.float32)
+    ad, bd, sbd, biasd, resd = D.from_host(a), D.from_host(bt), D.from_host(sb), D.from_host(bias), D.from_host(res)
+    for sa in (np.array([3e-4]), gen.uniform(1e-4, 5e-4, M)):
+        sad = D.from_host(sa)
+        for act, residual in ((None, None), ("gelu", None), (None, resd)):
+            y, _ = H.gemm_i8_fused(ad, bd, sad, sbd, biasd, act=act, residual=residual)
+            yh = y.numpy()
+            oq, os_ = O.ko_quantize_tensor(yh)
+            q2, s2 = H.quantize_tensor(y)
+            q, s = H.gemm_i8_quant(ad, bd, sad, sbd, biasd, act=act, residual=residual)
+            np.testing.assert_array_equal(q.numpy().reshape(-1), oq.reshape(-1))
+            np.testing.assert_array_equal(q.numpy(), q2.numpy())
+            assert s.numpy()[0] == os_ == s2.numpy()[0]
+
+
+def test_gemm_i8_quant_edge_cases(hip):
+    """A zero result quantizes with scale 1.0 (quantize.py:68); an empty one
+    too; a NaN in the residual is reported as ValueError, as the unfused
+    quantize reports it."""
+    from kansaiml_amd import _native as Nn
+    H, D = hip
+    a = np.zeros((256, 384), np.int8)
+    bt = np.ones((512, 384), np.int8)
+    sad, sbd = D.from_host(np.array([0.5])), D.from_host(np.full(512, 0.25))
+    q, s = H.gemm_i8_quant(D.from_host(a), D.from_host(bt), sad, sbd)
+    assert s.numpy()[0] == 1.0 and not q.numpy().any()
+    q, s = H.gemm_i8_quant(D([0, 384], "int8"), D.from_host(bt), sad, sbd)
+    assert s.numpy()[0] == 1.0
+    res = np.zeros((256, 512), np.float32)
+    res[7, 9] = np.nan
+    H.gemm_i8_quant(D.from_host(a), D.from_host(bt), sad, sbd, residual=D.from_host(res))
+    with pytest.raises(ValueError):
+        Nn.synchronize()
+    Nn.synchronize()
+
+
+@pytest.mark.parametrize("rows,d", [(1000, 384), (16384, 384), (37, 100), (1, 1024), (5, 3)])
+def test_layernorm_quant_matches_unfused(hip, rows, d):
+    """kh_layernorm_quant's codes and scale equal the per-tensor quantize of
+    kh_layernorm's output (vector and scalar row paths)."""
+    H, D = hip
+    gen = np.random.Generator(np.random.PCG64(rows * 7 + d))
+    x = (gen.standard_normal((rows, d)) * 3 + 0.5).astype(np.float32)
+    w, b = gen.standard_normal(d).astype(np.float32), gen.standard_normal(d).astype(np.float32)
+    xd, wd, bd = D.from_host(x), D.from_host(w), D.from_host(b)
+    y, _ = H.layer_norm(xd, wd, bd)
+    oq, os_ = O.ko_quantize_tensor(y.numpy())
+    q, s = H.layer_norm_quant(xd, wd, bd)
+    np.testing.assert_array_equal(q.numpy().reshape(-1), oq.reshape(-1))
+    assert s.numpy()[0] == os_
+
+
+def test_layernorm_quant_edge_cases(hip):
+    from kansaiml_amd import _native as Nn
+    H, D = hip
+    w, b = D.from_host(np.ones(384, np.float32)), D.from_host(np.zeros(384, np.float32))
+    q, s = H.layer_norm_quant(D([0, 384]), w, b)
+    assert s.numpy()[0] == 1.0
+    x = np.ones((20, 384), np.float32)  # constant rows normalize to exactly 0
+    q, s = H.layer_norm_quant(D.from_host(x), w, b)
+    assert s.numpy()[0] == 1.0 and not q.numpy().any()
+    x[3, 5] = np.inf
+    H.layer_norm_quant(D.from_host(x), w, b)
+    with pytest.raises(ValueError):
+        Nn.synchronize()
+    Nn.synchronize()
+
+
 def test_layernorm_and_attention_absmax_parts(hip):
     """LayerNorm and attention outputs quantized from the partials their
     kernels wrote equal kh_quantize_tensor of the same outputs; a partials

@@ -103,3 +103,45 @@ def test_plan_memory_matches_liveness_brute_force():
             iv.sort()
             for (a0, a1), (b0, b1) in zip(iv, iv[1:]):
                 assert a1 <= b0, f"slot {sid} reused while live (trial {trial})"
+
+
+def test_quantize_producers_fuse_into_quant_nodes():
+    """A per-tensor quantize whose input is only read by it absorbs its
+    producer: layer_norm -> layer_norm_quant, an int8 Linear chain (here with
+    GELU) -> int8_linear_quant.  A producer with a second reader, or a
+    per-row quantize, keeps the fp32 tensor."""
+    w1 = np.zeros((16, 32), np.float32)
+    w2 = np.zeros((32, 16), np.float32)
+    g1, b1 = np.ones(16, np.float32), np.zeros(16, np.float32)
+    bias = np.zeros(32, np.float32)
+
+    def fn(x):
+        h = x.layer_norm(g1, b1)
+        f = h.quantize().int8_matmul(x._coerce(w1).quantize()).dequantize().add(bias).gelu()
+        return f.quantize().int8_matmul(x._coerce(w2).quantize()).dequantize()
+
+    g = kir.trace(fn, np.zeros((4, 16), np.float32))
+    assert "layer_norm_quant" not in [n.op for n in kir.quant_fusion(g).nodes]  # off by default
+    f = kir.quant_fusion(g, producer_quant=True)
+    ops = [n.op for n in f.nodes if n.op not in ("placeholder", "constant")]
+    assert "layer_norm_quant" in ops and "int8_linear_quant" in ops
+    assert "layer_norm" not in ops and "gelu" not in ops
+    lq = [n for n in f.nodes if n.op == "int8_linear_quant"][0]
+    assert lq.dtype == "int8" and lq.attrs["act"] == "gelu" and lq.attrs["bias"]
+    assert [n for n in f.nodes if n.op == "layer_norm_quant"][0].dtype == "int8"
+
+    def shared(x):
+        h = x.layer_norm(g1, b1)
+        y = h.quantize().int8_matmul(x._coerce(np.zeros((16, 16), np.float32)).quantize()).dequantize()
+        return y.add(h)
+
+    f2 = kir.quant_fusion(kir.trace(shared, np.zeros((4, 16), np.float32)), producer_quant=True)
+    ops2 = [n.op for n in f2.nodes]
+    assert "layer_norm" in ops2 and "layer_norm_quant" not in ops2
+
+    def per_row(x):
+        return x.layer_norm(g1, b1).quantize("row").int8_matmul(x._coerce(w1).quantize()).dequantize()
+
+    ops3 = [n.op for n in kir.quant_fusion(kir.trace(per_row, np.zeros((4, 16), np.float32)),
+                                           producer_quant=True).nodes]
+    assert "layer_norm" in ops3 and "layer_norm_quant" not in ops3
