@@ -589,12 +589,32 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_i8_skinny_kernel(const
     for (int t = 0; t < MT; ++t)
 #pragma unroll
         for (int u = 0; u < NT; ++u) acc[t][u] = i32x4v{0, 0, 0, 0};
+    // The epilogue's operands (scales, bias, residual), loaded by the waves
+    // that finish the tiles while the weights stream in, rather than a
+    // dependent round trip after the reduction.
+    const int et = wave / NT;
+    const int64_t ej = n0 + (wave % NT) * 16 + (lane & 15);
+    const int64_t ejc = min(ej, (int64_t)N - 1);
+    double sbj = 0.0, sai[4] = {0.0, 0.0, 0.0, 0.0};
+    float bj = 0.0f, res[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto prefetch_epilogue = [&]() {
+        if (wave >= MT * NT) return;
+        sbj = ep.sb ? ep.sb[ep.sb_per_col ? ejc : 0] : 0.0;
+        bj = ep.bias ? ep.bias[ejc] : 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t i = min((int64_t)(et * 16 + 4 * (lane >> 4) + r), (int64_t)M - 1);
+            sai[r] = ep.out ? ep.sa[ep.sa_per_row ? i : 0] : 0.0;
+            res[r] = ep.residual ? ep.residual[i * N + ejc] : 0.0f;
+        }
+    };
     auto chunk = [&](int k0) {
         i32x4v b[NT][C];
 #pragma unroll
         for (int u = 0; u < NT; ++u)
 #pragma unroll
             for (int c = 0; c < C; ++c) b[u][c] = __builtin_amdgcn_raw_buffer_load_b128(rb, b_off[u], k0 + 64 * c, 0);
+        if constexpr (ONE) prefetch_epilogue();
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int c0 = 0; c0 < C; c0 += AC) {
@@ -618,6 +638,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_i8_skinny_kernel(const
     if constexpr (ONE) {
         chunk(k_begin);
     } else {
+        prefetch_epilogue();
         for (int k0 = k_begin; k0 < k_begin + kper; k0 += 64 * C) chunk(k0);
     }
 #pragma unroll
@@ -626,24 +647,12 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_i8_skinny_kernel(const
         for (int u = 0; u < NT; ++u) red[wave][t * NT + u][lane] = acc[t][u];
     __syncthreads();
     if (wave >= MT * NT) return;
-    // Wave w finishes row tile w / NT of column tile w % NT.  16x16 MFMA
-    // result layout: register r of lane l holds row 4*(l/16) + r, column l%16.
-    const int t = wave / NT;
-    const int64_t j = n0 + (wave % NT) * 16 + (lane & 15);
+    // Wave w finishes row tile w / NT of column tile w % NT (operands loaded
+    // by prefetch_epilogue).  16x16 MFMA result layout: register r of lane l
+    // holds row 4*(l/16) + r, column l%16.
+    const int t = et;
+    const int64_t j = ej;
     if (j >= N) return;
-    // Every load of the epilogue is issued before its first store (the
-    // output may alias nothing the compiler can prove, so a load left after
-    // a store would wait for it: one memory round trip per row).
-    const double sbj = ep.sb ? ep.sb[ep.sb_per_col ? j : 0] : 0.0;
-    const float bj = ep.bias ? ep.bias[j] : 0.0f;
-    double sai[4];
-    float res[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int64_t i = min((int64_t)(t * 16 + 4 * (lane >> 4) + r), (int64_t)M - 1);
-        sai[r] = ep.out ? ep.sa[ep.sa_per_row ? i : 0] : 0.0;
-        res[r] = ep.residual ? ep.residual[i * N + j] : 0.0f;
-    }
     i32x4v sum = red[0][wave][lane];
 #pragma unroll
     for (int w = 1; w < kSkinnyWaves; ++w) sum += red[w][wave][lane];
@@ -821,6 +830,14 @@ __global__ __launch_bounds__(512) void linear_i8_decode_kernel(const float* __re
     i32x4 b[S];
 #pragma unroll
     for (int s = 0; s < S; ++s) b[s] = __builtin_amdgcn_raw_buffer_load_b128(rb, min(col, N - 1) * K + kb, s * 64, 0);
+    // The epilogue's column scale and bias, in flight with the weights
+    // rather than a dependent round trip after the reduction.
+    double sbj = 0.0;
+    float bj = 0.0f;
+    if (wave == 0) {
+        sbj = sb[sb_per_col ? min(col, N - 1) : 0];
+        if (bias) bj = bias[min(col, N - 1)];
+    }
 
 #pragma unroll
     for (int m = 0; m < MAXM; ++m) {
@@ -885,8 +902,6 @@ __global__ __launch_bounds__(512) void linear_i8_decode_kernel(const float* __re
 #pragma unroll
     for (int w = 1; w < W; ++w) sum += red[w][lane];
     // 16x16 MFMA result layout: register r of lane l holds row 4 * (l / 16) + r, column l % 16.
-    const double sbj = sb[sb_per_col ? col : 0];
-    const float bj = bias ? bias[col] : 0.0f;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int i = 4 * g + r;
