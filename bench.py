@@ -159,22 +159,32 @@ def bench_skinny(steps, warmup):
             q = D([M, K], "int8")
             sx = D([M], "float64")
             out = D([M, N], "float32")
-            call = lambda w: Nn.call("kh_linear_i8", x.ptr, M, K, w.ptr, N, sw.ptr, 1, bias.ptr, q.ptr, sx.ptr,  # noqa: E731
-                                     out.ptr)
+            # The entry point bound once and each call's arguments built
+            # ahead, so the timed loop costs what a native caller's would
+            # (Python's per-call overhead otherwise approaches the kernel's
+            # few microseconds and leaks into the back-to-back figure).
+            fn = getattr(Nn.lib(), "kh_linear_i8")
+            argsets = [(x.ptr, M, K, w.ptr, N, sw.ptr, 1, bias.ptr, q.ptr, sx.ptr, out.ptr) for w in ws]
+
+            def call(i):
+                rc = fn(*argsets[i % copies])
+                if rc:
+                    Nn.check(rc, "kh_linear_i8")
+
             for i in range(max(3, warmup)):
-                call(ws[i % copies])
+                call(i)
             Nn.synchronize()
             e0, e1 = Nn.Event(), Nn.Event()
             e0.record()
             for i in range(steps):
-                call(ws[i % copies])
+                call(i)
             e1.record()
             Nn.synchronize()
             us = e0.elapsed_ms(e1) / steps * 1e3
             evs = [(Nn.Event(), Nn.Event()) for _ in range(steps)]
             for i, (a, b) in enumerate(evs):
                 a.record()
-                call(ws[i % copies])
+                call(i)
                 b.record()
             Nn.synchronize()
             us_single = sum(a.elapsed_ms(b) for a, b in evs) / steps * 1e3
