@@ -280,6 +280,13 @@ int kh_causal_attention_ex(const float* qkv, int B, int T, int H, int dk, float*
  * attainable int8 peak next to the published one. */
 int kh_probe_mfma_i8(const int8_t* operands, int64_t bytes, int64_t iters, double* tops, double* clock_mhz);
 
+/* Reads `bytes` (16-byte aligned, a multiple of 16, below 2 GiB) as the
+ * weight-streaming GEMMs read their weights -- every workgroup issues all of
+ * its 64 KiB of loads up front -- and discards them.  Asynchronous on the
+ * library stream, so it can be timed back to back like kh_linear_i8: the
+ * practical ceiling bench.py states for the decode rows. */
+int kh_probe_stream_read(const void* p, int64_t bytes);
+
 #ifdef __cplusplus
 }
 #endif

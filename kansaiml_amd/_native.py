@@ -78,6 +78,7 @@ _SIGNATURES = {
     "kh_linear_i8": [_vp, _i64, _i64, _vp, _i64, _vp, _int, _vp, _vp, _vp, _vp],
     "kh_matmul_f32": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "kh_probe_mfma_i8": [_vp, _i64, _i64, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)],
+    "kh_probe_stream_read": [_vp, _i64],
     "kh_add": [_vp, _vp, _vp, _i64],
     "kh_add_bias": [_vp, _vp, _vp, _i64, _i64, _int],
     "kh_relu": [_vp, _vp, _i64],

@@ -53,9 +53,40 @@ __global__ __launch_bounds__(kProbeThreads) void mfma_probe_kernel(const int8_t*
     if (s == 0x5eed5eed) sink[threadIdx.x & 63] = s;  // keeps the MFMAs live
 }
 
+// A plain streaming read, the ceiling of the weight-streaming GEMMs: each
+// workgroup of 512 threads issues all of its 64 KiB of 16-byte loads (8 per
+// lane, each instruction covering 8 KiB contiguous) before using any, folds
+// them into one word and keeps them live through an unreachable store.
+// Bytes past `bytes` read as zero (buffer-resource bound).
+__global__ __launch_bounds__(kProbeThreads) void stream_read_kernel(const void* __restrict__ p, uint32_t bytes,
+                                                                    int* __restrict__ sink) {
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+    const uint32_t base = (blockIdx.x * 8u * kProbeThreads + threadIdx.x) * 16u;
+    i32x4 v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = __builtin_amdgcn_raw_buffer_load_b128(r, base + i * kProbeThreads * 16u, 0, 0);
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+    if (s == 0x5eed5eed) sink[threadIdx.x & 63] = s;
+}
+
 }  // namespace
 
 extern "C" {
+
+int kh_probe_stream_read(const void* p, int64_t bytes) {
+    KH_REQUIRE(p && bytes > 0 && bytes % 16 == 0 && bytes < (1LL << 31) && kh::aligned(p, 16),
+               "kh_probe_stream_read: 16-byte aligned buffer of 16 B .. 2 GiB (a multiple of 16) required");
+    KH_DEVICE_OR_RETURN(d);
+    int* sink = static_cast<int*>(kh::scratch(d, 256));
+    if (!sink) return KH_ERR_OOM;
+    const int64_t per_block = 8LL * kProbeThreads * 16;
+    const unsigned blocks = (unsigned)((bytes + per_block - 1) / per_block);
+    stream_read_kernel<<<blocks, kProbeThreads, 0, d->stream>>>(p, (uint32_t)bytes, sink);
+    return kh::launch_status("stream_read");
+}
 
 int kh_probe_mfma_i8(const int8_t* operands, int64_t bytes, int64_t iters, double* tops, double* clock_mhz) {
     KH_REQUIRE(iters > 0 && tops && clock_mhz, "kh_probe_mfma_i8: bad arguments");

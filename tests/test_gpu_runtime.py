@@ -86,3 +86,15 @@ def test_mfma_probe_reports_rate_and_clock():
     assert 0.0 < mhz.value <= 2500.0
     with pytest.raises(RuntimeError):
         N.call("kh_probe_mfma_i8", ops.ptr, nbytes - 16, 200, ctypes.byref(tops), ctypes.byref(mhz))
+
+
+def test_stream_read_probe_runs_and_checks_arguments():
+    from kansaiml_amd import _native as N
+    from kansaiml_amd.device import DeviceTensor as D
+    buf = D([5 * 65536 + 48], "int8")  # a partial last workgroup
+    N.call("kh_probe_stream_read", buf.ptr, buf.nbytes)
+    N.synchronize()
+    with pytest.raises(RuntimeError):
+        N.call("kh_probe_stream_read", buf.ptr, 7)
+    with pytest.raises(RuntimeError):
+        N.call("kh_probe_stream_read", None, 4096)
