@@ -780,19 +780,26 @@ int launch_gemm(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, int6
 
 // ---------------------------------------------------------------------------
 // Decode Linear for one or two tokens (kh_linear_i8 with M <= 2): the per-token
-// quantize of the fp32 activations is fused into the weight-streaming GEMM,
+// quantize of the fp32 activations is fused into the weight-streaming GEMV,
 // so a decode step is one launch instead of two dependent ones.
 //
-// A workgroup (8 waves) owns 16 output columns for all M rows; wave w covers
-// k in [w * K/8, (w+1) * K/8) as S = K/512 steps of v_mfma_i32_16x16x64_i8.
-// Each workgroup reads the activations first (M x K fp32, L2-resident after
-// the first workgroup touches them), then issues all its weight loads, so
-// the in-order vmcnt wait for the activations does not wait for the weights;
-// while the weights stream in it reduces each row's absmax (wave shuffles and
-// an LDS table), quantizes the row with the reference's arithmetic into LDS
-// codes (workgroup 0 also writes the codes and scales to q_out / sx_out, the
-// outputs kh_linear_i8 documents), then multiplies.  Groups with an
-// undecided element take the exact path out of line, from memory.
+// A workgroup (8 waves) owns 16 consecutive weight rows (output columns), 16K
+// contiguous bytes, and reads them 8 KiB per load instruction -- the fastest
+// streaming pattern measured (an MFMA operand layout, 16 rows x 64 B per
+// wave instruction, read the same bytes ~20 % slower).  So lane t of
+// instruction i holds 16 bytes of row i * (8192 / K) + t / (K / 16) at the
+// k offset 16 * (t % (K / 16)), the same offset in every instruction; the
+// products are VALU v_dot4_i32_i8 against the lane's 16 activation codes
+// (read once from LDS), exact in int32 in any order.  Each row's lanes are
+// whole waves: a wave sums its lanes by shuffles, the row's waves through
+// LDS.  Each workgroup loads the fp32 activations first (L2-resident after
+// the first workgroup), then issues all of its weight loads, so the
+// in-order vmcnt wait for the activations does not wait for the weights;
+// while the weights stream in it reduces each row's absmax (wave shuffles
+// and an LDS table) and quantizes the row with the reference's arithmetic
+// into LDS codes (workgroup 0 also writes the codes and scales to q_out /
+// sx_out, the outputs kh_linear_i8 documents).  Groups with an undecided
+// element take the exact path out of line, from memory.
 // ---------------------------------------------------------------------------
 template <int S, int MAXM>
 __global__ __launch_bounds__(512) void linear_i8_decode_kernel(const float* __restrict__ x, int M,
@@ -805,14 +812,17 @@ __global__ __launch_bounds__(512) void linear_i8_decode_kernel(const float* __re
     using namespace kh::quant;
     constexpr int W = 8, T = W * 64;
     constexpr int K = 512 * S;
-    constexpr int XH = K / 4 / T;  // float4 of each row per thread
-    constexpr int kRow = K + 16;   // padded LDS code row: 16 rows at one k hit distinct banks
-    static_assert(XH >= 1 && MAXM * XH <= 32, "shape");
-    __shared__ __attribute__((aligned(16))) int8_t codes[MAXM * kRow];
+    constexpr int XH = K / 4 / T;         // float4 of each activation row per thread
+    constexpr int kLanesPerRow = K / 16;  // 16 weight bytes per lane
+    constexpr int kRowsPerInst = T / kLanesPerRow;
+    constexpr int kWavesPerRow = kLanesPerRow / 64;
+    static_assert(XH >= 1 && MAXM * XH <= 32 && kRowsPerInst * S == 16 && kWavesPerRow >= 1, "shape");
+    __shared__ __attribute__((aligned(16))) int8_t codes[MAXM * K];
     __shared__ unsigned rmax[W][MAXM];
-    __shared__ i32x4 red[W][64];
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    __shared__ int red[W][MAXM][S];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)M * (uint32_t)K * 4u);
     f32x4 xv[MAXM][XH];
@@ -821,23 +831,24 @@ __global__ __launch_bounds__(512) void linear_i8_decode_kernel(const float* __re
 #pragma unroll
         for (int h = 0; h < XH; ++h)
             xv[m][h] = __builtin_bit_cast(
-                f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (m * K + (threadIdx.x + h * T) * 4) * 4, 0, 0));
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (m * K + (tid + h * T) * 4) * 4, 0, 0));
 
-    const int cl = lane & 15, g = lane >> 4;
-    const int kb = wave * (S * 64) + g * 16;
-    const int col = blockIdx.x * 16 + cl;
+    // The epilogue's column scale and bias (thread j < 16 * MAXM finishes
+    // row j % 16 of token j / 16), in flight with the weights.  Every thread
+    // loads them (16 addresses per workgroup), unconditionally and before the
+    // weights: the in-order vmcnt wait for the activations then counts
+    // exactly and does not wait for any weight load.
+    const int erow = tid & 15;
+    const int ecol = min((int)blockIdx.x * 16 + erow, N - 1);
+    const double sbj = sb[sb_per_col ? ecol : 0];
+    const float bj = bias ? bias[ecol] : 0.0f;
+    // Rows past N read zeros (buffer-resource bound; the launch keeps
+    // (N + 16) * K within 32 bits).
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(B, (uint32_t)N * (uint32_t)K);
+    const uint32_t wbase = (uint32_t)blockIdx.x * 16u * (uint32_t)K + (uint32_t)tid * 16u;
     i32x4 b[S];
 #pragma unroll
-    for (int s = 0; s < S; ++s) b[s] = __builtin_amdgcn_raw_buffer_load_b128(rb, min(col, N - 1) * K + kb, s * 64, 0);
-    // The epilogue's column scale and bias, in flight with the weights
-    // rather than a dependent round trip after the reduction.
-    double sbj = 0.0;
-    float bj = 0.0f;
-    if (wave == 0) {
-        sbj = sb[sb_per_col ? min(col, N - 1) : 0];
-        if (bias) bj = bias[min(col, N - 1)];
-    }
+    for (int i = 0; i < S; ++i) b[i] = __builtin_amdgcn_raw_buffer_load_b128(rb, wbase, i * 8192, 0);
 
 #pragma unroll
     for (int m = 0; m < MAXM; ++m) {
@@ -858,17 +869,17 @@ __global__ __launch_bounds__(512) void linear_i8_decode_kernel(const float* __re
 #pragma unroll
         for (int w = 1; w < W; ++w) mb = max(mb, rmax[w][m]);
         const Scale sc = make_scale(mb);
-        if (blockIdx.x == 0 && threadIdx.x == 0) {
+        if (blockIdx.x == 0 && tid == 0) {
             sx_out[m] = sc.s;
             if (sc.bad) flag_nonfinite(fault);
         }
 #pragma unroll
         for (int h = 0; h < XH; ++h) {
-            const int e4 = threadIdx.x + h * T;
+            const int e4 = tid + h * T;
             bool ok = sc.fast;
             const unsigned w4 = pack4_fast(xv[m][h], sc.rf, ok);
             if (!ok) redo |= 1u << (m * XH + h);
-            *reinterpret_cast<unsigned*>(codes + m * kRow + e4 * 4) = w4;
+            *reinterpret_cast<unsigned*>(codes + m * K + e4 * 4) = w4;
             if (blockIdx.x == 0) *reinterpret_cast<unsigned*>(q_out + (int64_t)m * K + e4 * 4) = w4;
         }
     }
@@ -879,40 +890,64 @@ __global__ __launch_bounds__(512) void linear_i8_decode_kernel(const float* __re
         unsigned mb = rmax[0][m];
         for (int w = 1; w < W; ++w) mb = max(mb, rmax[w][m]);
         const Scale sc = make_scale(mb);
-        const int e4 = threadIdx.x + h * T;
+        const int e4 = tid + h * T;
         const f32x4 vv =
             __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (m * K + e4 * 4) * 4, 0, 0));
         const unsigned w4 = pack4(vv, sc);
-        *reinterpret_cast<unsigned*>(codes + m * kRow + e4 * 4) = w4;
+        *reinterpret_cast<unsigned*>(codes + m * K + e4 * 4) = w4;
         if (blockIdx.x == 0) *reinterpret_cast<unsigned*>(q_out + (int64_t)m * K + e4 * 4) = w4;
     }
     __builtin_amdgcn_s_waitcnt(wait_imm(63, 0));
     __builtin_amdgcn_s_barrier();
 
-    i32x4 acc = {0, 0, 0, 0};
+    // Partial dot products: the lane's 16 codes of each token against its
+    // 16 bytes of every row it loaded.
+    const int kk = (tid % kLanesPerRow) * 16;
+    i32x4 a[MAXM];
 #pragma unroll
-    for (int s = 0; s < S; ++s) {
-        const i32x4 af = (cl < M) ? *reinterpret_cast<const i32x4*>(codes + cl * kRow + kb + s * 64) : i32x4{0, 0, 0, 0};
-        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, b[s], acc, 0, 0, 0);
+    for (int m = 0; m < MAXM; ++m)
+        a[m] = (m < M) ? *reinterpret_cast<const i32x4*>(codes + m * K + kk) : i32x4{0, 0, 0, 0};
+    int p[MAXM][S];
+#pragma unroll
+    for (int i = 0; i < S; ++i)
+#pragma unroll
+        for (int m = 0; m < MAXM; ++m) {
+            p[m][i] = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) p[m][i] = __builtin_amdgcn_sdot4(a[m][e], b[i][e], p[m][i], false);
+        }
+    // Wave sums of all S * MAXM partials in lockstep: each shuffle round is
+    // S * MAXM independent exchanges and one wait, not S * MAXM dependent
+    // chains one after another.
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+        for (int m = 0; m < MAXM; ++m)
+#pragma unroll
+            for (int i = 0; i < S; ++i) p[m][i] += __shfl_xor(p[m][i], off, 64);
+    if (lane == 0) {
+#pragma unroll
+        for (int m = 0; m < MAXM; ++m)
+#pragma unroll
+            for (int i = 0; i < S; ++i) red[wave][m][i] = p[m][i];
     }
-    red[wave][lane] = acc;
     __syncthreads();
-    if (wave != 0 || col >= N) return;
-    i32x4 sum = red[0][lane];
+    if (tid >= 16 * MAXM) return;
+    // Row erow of the workgroup came from instruction erow / kRowsPerInst,
+    // waves [sub * kWavesPerRow, (sub + 1) * kWavesPerRow).
+    const int m = tid >> 4;
+    const int n = (int)blockIdx.x * 16 + erow;
+    if (m >= M || n >= N) return;
+    const int i = erow / kRowsPerInst, sub = erow % kRowsPerInst;
+    int sum = 0;
 #pragma unroll
-    for (int w = 1; w < W; ++w) sum += red[w][lane];
-    // 16x16 MFMA result layout: register r of lane l holds row 4 * (l / 16) + r, column l % 16.
+    for (int w = 0; w < kWavesPerRow; ++w) sum += red[sub * kWavesPerRow + w][m][i];
+    unsigned mb = rmax[0][m];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int i = 4 * g + r;
-        if (i >= M) continue;
-        unsigned mb = rmax[0][i];
-#pragma unroll
-        for (int w = 1; w < W; ++w) mb = max(mb, rmax[w][i]);
-        float y = (float)((double)sum[r] * (make_scale(mb).s * sbj));
-        if (bias) y = y + bj;
-        out[(int64_t)i * N + col] = y;
-    }
+    for (int w = 1; w < W; ++w) mb = max(mb, rmax[w][m]);
+    float y = (float)((double)sum * (make_scale(mb).s * sbj));
+    if (bias) y = y + bj;
+    out[(int64_t)m * N + n] = y;
 }
 
 template <int S>
@@ -931,8 +966,7 @@ int launch_decode(kh::Device* d, const float* x, int64_t M, const int8_t* B, int
 // True when the fused decode kernel covers this call.
 bool decode_fits(const float* x, int64_t M, int64_t K, const int8_t* B, int64_t N, const int8_t* q) {
     return M >= 1 && M <= 2 && (K == 2048 || K == 4096 || K == 8192) && N >= 1 &&
-           N * K <= 0xFFFFFFFFLL && (N + 15) / 16 <= 0x7FFFFFFFLL && kh::aligned(x, 16) && kh::aligned(B, 16) &&
-           kh::aligned(q, 4);
+           (N + 16) * K <= 0xFFFFFFFFLL && kh::aligned(x, 16) && kh::aligned(B, 16) && kh::aligned(q, 4);
 }
 
 }  // namespace
