@@ -205,7 +205,8 @@ def _f32_bound(a, b):
 
 @pytest.mark.parametrize("M,K,N", [(17, 19, 15), (100, 77, 50), (1, 1, 1), (64, 512, 512), (16, 32, 24),
                                    (257, 129, 131), (512, 1024, 768), (1024, 1024, 1024),
-                                   (4100, 68, 4000), (4097, 33, 4001)])  # 256x256 tiles, partial; K % 4 != 0
+                                   (4100, 68, 4000), (4097, 33, 4001),  # 256x256 tiles, partial; K % 4 != 0
+                                   (4100, 64, 4004), (3000, 2048, 5000)])  # ping-pong kernel, partial tiles
 def test_matmul_f32_vs_reference(hip, M, K, N):
     H, D = hip
     gen = np.random.Generator(np.random.PCG64(M + 7 * K + 13 * N))
