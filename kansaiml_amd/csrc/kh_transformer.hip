@@ -20,6 +20,7 @@
 
 #include "kh_common.h"
 #include "kh_act.h"
+#include "kh_pipeline.h"
 #include "kh_quant_math.h"
 // kh_quant_math.h turns FP contraction off for the exact quantize arithmetic
 // it defines; the fp32 kernels of this file keep the compiler's default.
@@ -206,8 +207,13 @@ __global__ __launch_bounds__(256) void gelu_kernel(const float* __restrict__ x, 
 //
 // A workgroup owns 64 queries of one (batch, head); wave w owns queries
 // 16w .. 16w+15 of them, lane l query 16w + l % 16.  Keys go through LDS 64
-// at a time: K as [key][d] and V transposed as [d][key] (4-key groups
-// XOR-swizzled), rows padded to 68 floats.  Both products run on
+// at a time, K and V each as [key][d] (256-byte rows whose 16-byte chunk c sits
+// at position c ^ (key % 16), so the column reads below touch 16 distinct
+// chunks), brought in by LDS-DMA from a buffer resource spanning the batch's
+// rows (keys past T read as 0).  Each has one buffer and its own point in the
+// iteration: V of tile i is loaded while S of tile i is computed and
+// softmaxed, K of tile i+1 while P V of tile i is computed, so no wave waits
+// on HBM once the pipeline runs.  Both products run on
 // v_mfma_f32_16x16x4_f32 (D[i][j] += sum over k of A[i][k] B[k][j]; lane l
 // supplies A[l % 16][l / 16] and B[l / 16][l % 16]; result register r of lane
 // l is D[4 * (l / 16) + r][l % 16]).  The reduction index of each product is
@@ -216,23 +222,22 @@ __global__ __launch_bounds__(256) void gelu_kernel(const float* __restrict__ x, 
 //   d = 16g + s): lane l ends up holding, for its own query, the scores of
 //   keys 16t + 4g + r (t, r = 0..3) of the tile;
 //   O^T = V^T P^T (k = key; step (t, r) of lane group g takes key
-//   16t + 4g + r): P^T's operand is exactly the probabilities lane l holds, so
-//   P never leaves registers, and V^T's operand is a 16-byte LDS read.
+//   16t + 4g + r; product j's row i is d = 4i + j): P^T's operand is exactly
+//   the probabilities lane l holds, so P never leaves registers, V^T's
+//   operands for the four products are one 16-byte read of V's row, and lane
+//   l ends up holding d = 16g .. 16g+15 of its query's output.
 // The softmax of a query reduces over its lane's 16 scores and the 4 lanes
 // l % 16 + 16g.  The 1/sqrt(dk) = 1/8 scale is applied to Q (exact).
+//
+// Workgroups are ordered so that the query blocks of one (batch, head) run on
+// one XCD (its L2 holds their shared K and V; workgroup i runs on XCD i % 8)
+// and, within an XCD, the blocks with the most key tiles go first.
 // ---------------------------------------------------------------------------
 constexpr int kDk = 64;
-constexpr int kAttQ = 64;      // queries per workgroup (16 per wave)
-constexpr int kAttK = 64;      // keys per LDS tile
-constexpr int kAttPad = 68;    // padded LDS row, floats
+constexpr int kAttQ = 64;  // queries per workgroup (16 per wave)
+constexpr int kAttK = 64;  // keys per LDS tile
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
-
-// Column of key kk in row d of the transposed V tile: groups of 4 keys are
-// XOR-swizzled by (d / 16) % 4, so the transposing stores (64 lanes: 16
-// values of d / 4, 4 keys) hit 64 distinct banks; a 4-key group stays
-// contiguous for the 16-byte operand reads.
-__device__ __forceinline__ int vt_col(int d, int kk) { return ((((kk >> 2) ^ (d >> 4)) & 15) << 2) | (kk & 3); }
 
 // max / sum over the 4 lanes l % 16 + 16g holding one query's scores.
 __device__ __forceinline__ float query4_max(float v) {
@@ -244,24 +249,50 @@ __device__ __forceinline__ float query4_sum(float v) {
     return v + __shfl_xor(v, 32, 64);
 }
 
+// One 64-key tile of K or V (rows of the batch's qkv at byte offset `col`)
+// into `tile` by LDS-DMA: wave w's instruction i fills rows 16i + 4w .. +3,
+// lane l row 16i + 4w + l / 16 at position l % 16, loading the chunk that
+// belongs there.
+__device__ __forceinline__ void attention_tile_dma(__amdgpu_buffer_rsrc_t r, float* tile, int k0, int row_bytes,
+                                                   int col, int wave, int lane) {
+    const int row = 4 * wave + (lane >> 4);  // 16i + row, i = 0..3
+    const int voff = (k0 + row) * row_bytes + col + 16 * ((lane & 15) ^ row);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        kh::pipe::lds_dma16(r, reinterpret_cast<char*>(tile) + (16 * i + 4 * wave) * kDk * 4,
+                            voff + 16 * i * row_bytes, 0);
+}
+
 __global__ __launch_bounds__(256) void attention_mfma_kernel(const float* __restrict__ qkv, int B, int T, int H,
                                                              float* __restrict__ out, unsigned* __restrict__ parts) {
-    __shared__ __attribute__((aligned(16))) float ks[kAttK][kAttPad];
-    __shared__ __attribute__((aligned(16))) float vt[kDk][kAttPad];
+    __shared__ __attribute__((aligned(1024))) float ks[kAttK * kDk];
+    __shared__ __attribute__((aligned(1024))) float vs[kAttK * kDk];
+    using kh::pipe::wait_imm;
     const int D = H * kDk;
-    // Query blocks in reverse: the workgroups with the most key tiles (the
-    // last queries of the causal triangle) are dispatched first.
-    const int qb = gridDim.x - 1 - blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int nq = (T + kAttQ - 1) / kAttQ, pairs = B * H;
+    int qb, pair;
+    if (pairs % kh::pipe::kXcds == 0) {
+        const int per = pairs / kh::pipe::kXcds, s = blockIdx.x / kh::pipe::kXcds;
+        qb = nq - 1 - s / per;
+        pair = (blockIdx.x % kh::pipe::kXcds) * per + s % per;
+    } else {
+        qb = nq - 1 - blockIdx.x / pairs;
+        pair = blockIdx.x % pairs;
+    }
+    const int b = pair / H, h = pair - b * H;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, g = lane >> 4;
-    const int64_t row0 = (int64_t)b * T;
+    const float* bq = qkv + (int64_t)b * T * 3 * D;
     const int q0 = qb * kAttQ + wave * 16;  // this wave's first query
     const int q = q0 + li;                  // this lane's query
+    const int row_bytes = 3 * D * 4;
+    const __amdgpu_buffer_rsrc_t rsrc = kh::pipe::make_rsrc(bq, (uint32_t)(T * row_bytes));
+    const int kcol = (D + h * kDk) * 4, vcol = kcol + D * 4;
 
     // Q operand: query q, d = 16g .. 16g+15, scaled by 1/8.
     float qf[16];
     {
-        const f32x4v* qr = reinterpret_cast<const f32x4v*>(qkv + (row0 + min(q, T - 1)) * 3 * D + h * kDk + 16 * g);
+        const f32x4v* qr = reinterpret_cast<const f32x4v*>(bq + (int64_t)min(q, T - 1) * 3 * D + h * kDk + 16 * g);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const f32x4v v = qr[c];
@@ -269,30 +300,19 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(const float* __rest
             for (int e = 0; e < 4; ++e) qf[4 * c + e] = q < T ? v[e] * 0.125f : 0.0f;
         }
     }
-    f32x4v o[4];  // O^T: register r of o[j] is O[q][16j + 4g + r]
+    attention_tile_dma(rsrc, ks, 0, row_bytes, kcol, wave, lane);
+    f32x4v o[4];  // O^T: register r of o[j] is O[q][16g + 4r + j]
 #pragma unroll
     for (int j = 0; j < 4; ++j) o[j] = f32x4v{0.f, 0.f, 0.f, 0.f};
     float m = -3.0e38f, l = 0.0f;
 
-    const int q_hi = min(T, (qb + 1) * kAttQ) - 1;  // last query of the workgroup
-    for (int k0 = 0; k0 <= q_hi; k0 += kAttK) {
-        __syncthreads();  // previous tile's readers are done
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int e = tid + i * 256;
-            const int kk = e >> 4, d4 = e & 15;
-            const int key = k0 + kk;
-            f32x4v kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
-            if (key < T) {
-                const float* kr = qkv + (row0 + key) * 3 * D + h * kDk;
-                kv = reinterpret_cast<const f32x4v*>(kr + D)[d4];
-                vv = reinterpret_cast<const f32x4v*>(kr + 2 * D)[d4];
-            }
-            *reinterpret_cast<f32x4v*>(&ks[kk][4 * d4]) = kv;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) vt[4 * d4 + c][vt_col(4 * d4 + c, kk)] = vv[c];
-        }
+    const int tiles = (min(T, (qb + 1) * kAttQ) - 1) / kAttK + 1;  // through the workgroup's last query
+    for (int it = 0; it < tiles; ++it) {
+        const int k0 = it * kAttK;
+        // K(it) has landed for every wave, and every wave is done with V(it-1).
+        __builtin_amdgcn_s_waitcnt(wait_imm(0, 15));
         __syncthreads();
+        attention_tile_dma(rsrc, vs, k0, row_bytes, vcol, wave, lane);
 
         // S^T = K Q^T, 4 subtiles of 16 keys: st[t][r] = score of key 16t + 4g + r.
         f32x4v st[4];
@@ -302,7 +322,8 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(const float* __rest
         for (int c = 0; c < 4; ++c) {
             f32x4v kv[4];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) kv[t] = reinterpret_cast<const f32x4v*>(&ks[16 * t + li][16 * g])[c];
+            for (int t = 0; t < 4; ++t)
+                kv[t] = *reinterpret_cast<const f32x4v*>(&ks[(16 * t + li) * kDk + 4 * ((4 * g + c) ^ li)]);
 #pragma unroll
             for (int e = 0; e < 4; ++e)
 #pragma unroll
@@ -311,16 +332,20 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(const float* __rest
         }
         // Causal mask (key > query) and keys past T -- only where the tile
         // reaches this wave's diagonal or the sequence end.
-        const bool full = k0 + kAttK - 1 <= q0 && k0 + kAttK <= T;
+        if (!(k0 + kAttK - 1 <= q0 && k0 + kAttK <= T)) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int key = k0 + 16 * t + 4 * g + r;
+                    st[t][r] = (key > q || key >= T) ? -3.0e38f : st[t][r];
+                }
+        }
         float mx = -3.0e38f;
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int key = k0 + 16 * t + 4 * g + r;
-                if (!full && (key > q || key >= T)) st[t][r] = -3.0e38f;
-                mx = fmaxf(mx, st[t][r]);
-            }
+            for (int r = 0; r < 4; ++r) mx = fmaxf(mx, st[t][r]);
         mx = query4_max(mx);
         const float m_new = fmaxf(m, mx);
         const float corr = __expf(m - m_new);
@@ -329,8 +354,8 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(const float* __rest
         for (int t = 0; t < 4; ++t)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int key = k0 + 16 * t + 4 * g + r;
-                const float p = (!full && (key > q || key >= T)) ? 0.0f : __expf(st[t][r] - m_new);
+                // A masked score (-3e38) gives exactly 0: m_new is a real score.
+                const float p = st[t][r] == -3.0e38f ? 0.0f : __expf(st[t][r] - m_new);
                 st[t][r] = p;
                 sum += p;
             }
@@ -338,37 +363,43 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(const float* __rest
         m = m_new;
 #pragma unroll
         for (int j = 0; j < 4; ++j) o[j] *= corr;
-        // O^T += V^T P^T: A = V^T (d 16j + li, key 16t + 4g + r), B = P^T (in registers).
+
+        // V(it) has landed for every wave, and every wave is done with K(it).
+        __builtin_amdgcn_s_waitcnt(wait_imm(0, 15));
+        __syncthreads();
+        if (it + 1 < tiles) attention_tile_dma(rsrc, ks, k0 + kAttK, row_bytes, kcol, wave, lane);
+
+        // O^T += V^T P^T: product j, A = V^T (d 4 li + j, key 16t + 4g + r), B = P^T (in registers).
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             f32x4v va[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                va[j] = *reinterpret_cast<const f32x4v*>(&vt[16 * j + li][vt_col(16 * j + li, 16 * t + 4 * g)]);
+            for (int r = 0; r < 4; ++r)
+                va[r] = *reinterpret_cast<const f32x4v*>(&vs[(16 * t + 4 * g + r) * kDk + 4 * (li ^ (4 * g + r))]);
 #pragma unroll
             for (int r = 0; r < 4; ++r)
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-                    o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(va[j][r], st[t][r], o[j], 0, 0, 0);
+                    o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(va[r][j], st[t][r], o[j], 0, 0, 0);
         }
     }
     unsigned mxo = 0;
     if (q < T) {
         const float inv = 1.0f / l;
-        float* orow = out + (row0 + q) * D + h * kDk + 4 * g;
+        float* orow = out + ((int64_t)b * T + q) * D + h * kDk + 16 * g;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const f32x4v y = o[j] * inv;
-            *reinterpret_cast<f32x4v*>(orow + 16 * j) = y;
+        for (int r = 0; r < 4; ++r) {
+            const f32x4v y = f32x4v{o[0][r], o[1][r], o[2][r], o[3][r]} * inv;
+            *reinterpret_cast<f32x4v*>(orow + 4 * r) = y;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) mxo = max(mxo, kh::abs_bits32(y[r]));
+            for (int e = 0; e < 4; ++e) mxo = max(mxo, kh::abs_bits32(y[e]));
         }
     }
     if (parts) {
         // Per-workgroup max |out| bits, for a following per-tensor quantize.
         __shared__ unsigned wmax[4];
         mxo = block4_max(mxo, wmax);
-        if (tid == 0) parts[((int64_t)b * gridDim.y + h) * gridDim.x + blockIdx.x] = mxo;
+        if (tid == 0) parts[blockIdx.x] = mxo;
     }
 }
 
@@ -474,19 +505,23 @@ int kh_causal_attention_ex(const float* qkv, int B, int T, int H, int dk, float*
                            int max_parts, int* nparts) {
     KH_REQUIRE(B > 0 && T > 0 && H > 0, "kh_causal_attention: bad shape");
     KH_REQUIRE(dk == kDk, "kh_causal_attention: only head dimension 64 is supported");
-    KH_REQUIRE(B <= 65535 && H <= 65535, "kh_causal_attention: too many batches or heads");
     KH_REQUIRE(qkv && out, "kh_causal_attention: null pointer");
     KH_REQUIRE(!absmax_parts || (max_parts > 0 && nparts), "kh_causal_attention_ex: partials need max_parts and nparts");
     if (nparts) *nparts = 0;
     KH_DEVICE_OR_RETURN(d);
     KH_REQUIRE(kh::aligned(qkv, 16) && kh::aligned(out, 16), "kh_causal_attention: 16-byte aligned buffers required");
-    dim3 grid((unsigned)((T + kAttQ - 1) / kAttQ), (unsigned)H, (unsigned)B);
-    const int64_t blocks = (int64_t)grid.x * grid.y * grid.z;
+    // Key offsets within a batch's rows, up to the last tile's padding, are
+    // 32-bit buffer offsets.
+    const int64_t nq = (T + kAttQ - 1) / kAttQ;
+    KH_REQUIRE((nq * kAttQ) * 3 * (int64_t)H * kDk * 4 <= 0x7FFFFFFFLL,
+               "kh_causal_attention: one batch's qkv rows must stay under 2 GiB");
+    const int64_t blocks = nq * H * B;
+    KH_REQUIRE(blocks <= 0x7FFFFFFFLL, "kh_causal_attention: too many query blocks");
     const bool fused = absmax_parts && blocks <= max_parts;
     // 1/sqrt(d_k) = 1/8 for dk = 64 (the reference's binary64 Python float,
     // nn.py:413, is exactly representable in binary32); the kernel applies it
     // to Q.
-    attention_mfma_kernel<<<grid, 256, 0, d->stream>>>(qkv, B, T, H, out, fused ? absmax_parts : nullptr);
+    attention_mfma_kernel<<<(unsigned)blocks, 256, 0, d->stream>>>(qkv, B, T, H, out, fused ? absmax_parts : nullptr);
     int rc = kh::launch_status("attention");
     if (rc || !absmax_parts) return rc;
     if (fused) {
