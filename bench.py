@@ -231,16 +231,23 @@ def bench_c4(steps, warmup):
     """Config C4: the int8 char-LM forward (vocab 65, d 384, 6 heads, 6 layers,
     FFN 1536, seq 256, batch 64; int8 per-channel weights ~N(0, 0.02),
     per-tensor dynamic activation scales, fp32 softmax / LayerNorm / GELU).
-    Token ids and weights resident on the device; logits stay on the device."""
+    Token ids and weights resident on the device; logits stay on the device.
+    Timed two ways: replaying the forward recorded as a HIP graph (one host
+    call per forward; the headline figure) and the eager planned run (one
+    Python dispatch per graph node)."""
     from kansaiml_amd.charlm import CharLM, CharLMWeights, attention_flops, int8_linear_ops
     from kansaiml_amd.device import DeviceTensor as D
     w = CharLMWeights(seed=0)
     model = CharLM(w)
     ids = D.from_host(np.random.Generator(np.random.PCG64(9)).integers(0, 65, (64, 256)).astype(np.int32))
-    ms = time_kernel(lambda: model.forward(ids, to_host=False), steps, warmup)
+    eager = time_kernel(lambda: model.forward(ids, to_host=False), steps, warmup)
+    g = model.capture(64, 256)
+    ms = time_kernel(lambda: g(ids, to_host=False), steps, warmup)
+    g.close()
     ops = int8_linear_ops(w, 64, 256)
     return {"workload": "C4 int8 char-LM forward, batch 64 x seq 256 (16384 tokens), 6 layers, d 384",
             "ms_per_forward": round(ms, 4), "tokens_per_s": round(64 * 256 / (ms * 1e-3), 1),
+            "ms_per_forward_eager": round(eager, 4),
             "int8_linear_ops": ops, "int8_linear_TOPS_over_forward": round(ops / (ms * 1e-3) / 1e12, 2),
             "attention_fp32_flops_full_square": attention_flops(w, 64, 256)}
 
@@ -443,7 +450,8 @@ def main():
     if "c4" in only:
         log("C4 int8 char-LM forward ...")
         c4 = bench_c4(max(5, args.steps // 4), max(2, args.warmup // 10))
-        log(f"C4 forward: {c4['ms_per_forward']:.3f} ms ({c4['tokens_per_s']:.0f} tokens/s)")
+        log(f"C4 forward: {c4['ms_per_forward']:.3f} ms as a HIP graph ({c4['tokens_per_s']:.0f} tokens/s), "
+            f"{c4['ms_per_forward_eager']:.3f} ms eager")
         Nn.call("kh_pool_trim")
     if "copy" in only:
         c_ms, c_gbs = bench_copy(args.steps, args.warmup)

@@ -102,6 +102,29 @@ int kh_event_record(void* event);
 int kh_event_elapsed_ms(void* start, void* end, float* ms);
 int kh_event_destroy(void* event);
 
+/* ---- graphs (HIP graph capture of the library stream) ------------------- */
+
+/* Records the library calls made between kh_graph_capture_begin and
+ * kh_graph_capture_end into a HIP graph instead of running them, and
+ * instantiates it; kh_graph_launch replays the recorded kernels and copies
+ * on the library stream with one host call.  Stands where the reference
+ * re-interprets a cached traced graph on every call (python/kansai/kir.py:
+ * 536-555 jit cache, 957-1068 run_planned): the planned run is recorded once
+ * and replayed.  The graph reads and writes the very buffers the captured
+ * calls named, so inputs are refreshed in place before a launch, and outputs
+ * are overwritten by the next launch.  Pool blocks freed during the capture
+ * belong to the graph (they return to the pool at kh_graph_destroy), and a
+ * block still held at capture end stays the graph's when it is freed later,
+ * so no other work is handed memory a launch writes.  Work needing a larger
+ * scratch area or a host synchronisation cannot be captured (run it once
+ * first); kh_synchronize, the host copies and kh_pool_trim fail while a
+ * capture is open.  kh_graph_capture_end(NULL) discards the capture.
+ * kh_graph_destroy waits for the stream first. */
+int kh_graph_capture_begin(void);
+int kh_graph_capture_end(void** graph);
+int kh_graph_launch(void* graph);
+int kh_graph_destroy(void* graph);
+
 /* ---- quantize / dequantize -------------------------------------------- */
 
 /* quantize_symmetric (python/kansai/quantize.py:50-70) over a whole

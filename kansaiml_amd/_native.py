@@ -58,6 +58,10 @@ _SIGNATURES = {
     "kh_event_record": [_vp],
     "kh_event_elapsed_ms": [_vp, _vp, ctypes.POINTER(ctypes.c_float)],
     "kh_event_destroy": [_vp],
+    "kh_graph_capture_begin": [],
+    "kh_graph_capture_end": [ctypes.POINTER(_vp)],
+    "kh_graph_launch": [_vp],
+    "kh_graph_destroy": [_vp],
     "kh_quantize_tensor": [_vp, _i64, _vp, _vp],
     "kh_quantize_rows": [_vp, _i64, _i64, _vp, _vp],
     "kh_quantize_cols_packed": [_vp, _i64, _i64, _vp, _vp],

@@ -194,6 +194,18 @@ class CharLM:
 
     __call__ = forward
 
+    def capture(self, batch: int, seq: int) -> "kir.HipGraph":
+        """The forward for [batch, seq] token ids recorded as a HIP graph:
+        g(ids, to_host=True) replays it on new ids with one launch (the
+        returned device logits, with to_host=False, are overwritten by the
+        next replay).  The graph reads this model's device weights in place;
+        set_parameter and checkpoint loads overwrite those same buffers, so
+        the next replay sees the loaded values."""
+        if seq > self.w.seq:
+            raise ValueError(f"sequence length {seq} exceeds the position table ({self.w.seq})")
+        g, plan = self.graph(batch, seq)
+        return kir.capture_hip_planned(g, plan, DeviceTensor.from_host(np.zeros((batch, seq), np.int32)))
+
 
 def int8_linear_ops(w: CharLMWeights, batch: int, seq: int) -> float:
     """Integer ops (2*M*N*K) of the model's int8 Linear layers per forward."""

@@ -26,6 +26,8 @@ thread_local int t_device = -1;
 
 constexpr int kMaxDevices = 16;
 
+struct Graph;
+
 struct Pool {
     std::mutex mu;
     std::unordered_map<size_t, std::vector<void*>> free_lists;  // size class -> blocks
@@ -33,6 +35,16 @@ struct Pool {
     size_t in_use = 0;
     size_t cached = 0;
     size_t driver_allocs = 0;
+    // Graph capture (kh_graph_capture_begin .. _end).  Blocks freed while
+    // capturing go to cap_free, not to free_lists: the captured nodes keep
+    // using them at every launch, so no later work may be handed them.
+    bool capturing = false;
+    std::unordered_map<size_t, std::vector<void*>> cap_free;
+    std::vector<void*> cap_used;  // every block handed out while capturing
+    // Blocks a live graph's nodes use that were still handed out when its
+    // capture ended (its output, for one): kh_free gives them to the graph.
+    std::unordered_map<void*, Graph*> pinned;
+    int graphs_alive = 0;
 };
 
 struct DeviceSlot {
@@ -41,7 +53,16 @@ struct DeviceSlot {
     std::mutex scratch_mu;
     void* scratch = nullptr;
     size_t scratch_bytes = 0;
+    std::vector<void*> retired_scratch;  // outgrown while graphs that use it were alive
     bool ready = false;
+};
+
+// An instantiated capture and the pool blocks its nodes use.
+struct Graph {
+    hipGraphExec_t exec = nullptr;
+    int device = -1;
+    std::vector<std::pair<void*, size_t>> owned;  // back to the pool at destroy
+    std::vector<void*> pinned;                    // entries of Pool::pinned for this graph
 };
 
 std::mutex g_init_mu;
@@ -133,7 +154,24 @@ void* scratch(Device* d, size_t bytes) {
     std::lock_guard<std::mutex> lk(s.scratch_mu);
     if (bytes <= s.scratch_bytes) return s.scratch;
     size_t want = bytes < (1u << 20) ? (1u << 20) : size_class(bytes);
-    if (s.scratch) {
+    bool capturing, graphs;
+    {
+        std::lock_guard<std::mutex> plk(s.pool.mu);
+        capturing = s.pool.capturing;
+        graphs = s.pool.graphs_alive > 0;
+    }
+    if (capturing) {
+        fail(KH_ERR_INVALID_ARG,
+             "scratch area would grow during graph capture: run the work once on the stream before capturing it");
+        return nullptr;
+    }
+    if (s.scratch && graphs) {
+        // Captured graphs hold the old area's address: keep it until the
+        // last of them is destroyed.
+        s.retired_scratch.push_back(s.scratch);
+        s.scratch = nullptr;
+        s.scratch_bytes = 0;
+    } else if (s.scratch) {
         // The old area may still be read by queued work.
         if (hipStreamSynchronize(d->stream) != hipSuccess) {
             fail(KH_ERR_HIP, "hipStreamSynchronize before growing scratch");
@@ -150,10 +188,20 @@ void* scratch(Device* d, size_t bytes) {
     return p;
 }
 
+bool capturing(Device* d) {
+    Pool& pool = g_slots[d->id].pool;
+    std::lock_guard<std::mutex> lk(pool.mu);
+    return pool.capturing;
+}
+
 }  // namespace kh
 
 using kh::fail;
 using kh::hip_status;
+
+// Host-synchronous calls cannot be recorded into a graph.
+#define KH_NOT_CAPTURING(d, what) \
+    KH_REQUIRE(!::kh::capturing(d), what ": not allowed while a graph is being captured")
 
 extern "C" {
 
@@ -197,6 +245,7 @@ int kh_device_info(char* name, size_t name_len, int* cus, int* clock_khz, int* m
 
 int kh_synchronize(void) {
     KH_DEVICE_OR_RETURN(d);
+    KH_NOT_CAPTURING(d, "kh_synchronize");
     int rc = hip_status(hipStreamSynchronize(d->stream), "hipStreamSynchronize");
     if (rc) return rc;
     unsigned fault = 0;
@@ -228,17 +277,25 @@ int kh_alloc(size_t bytes, void** dptr) {
     KH_DEVICE_OR_RETURN(d);
     kh::Pool& pool = kh::g_slots[d->id].pool;
     const size_t cls = kh::size_class(bytes);
+    bool capturing;
     {
         std::lock_guard<std::mutex> lk(pool.mu);
-        auto it = pool.free_lists.find(cls);
-        if (it != pool.free_lists.end() && !it->second.empty()) {
-            void* p = it->second.back();
-            it->second.pop_back();
-            pool.live[p] = cls;
-            pool.cached -= cls;
-            pool.in_use += cls;
-            *dptr = p;
-            return KH_OK;
+        capturing = pool.capturing;
+        // While capturing, blocks freed by the capture come back first (the
+        // same last-freed-first order as outside a capture).
+        for (auto* lists : {capturing ? &pool.cap_free : nullptr, &pool.free_lists}) {
+            if (!lists) continue;
+            auto it = lists->find(cls);
+            if (it != lists->end() && !it->second.empty()) {
+                void* p = it->second.back();
+                it->second.pop_back();
+                pool.live[p] = cls;
+                pool.cached -= cls;
+                pool.in_use += cls;
+                if (capturing) pool.cap_used.push_back(p);
+                *dptr = p;
+                return KH_OK;
+            }
         }
     }
     void* p = nullptr;
@@ -256,6 +313,7 @@ int kh_alloc(size_t bytes, void** dptr) {
     pool.live[p] = cls;
     pool.in_use += cls;
     pool.driver_allocs += 1;
+    if (pool.capturing) pool.cap_used.push_back(p);
     *dptr = p;
     return KH_OK;
 }
@@ -269,14 +327,23 @@ int kh_free(void* dptr) {
     if (it == pool.live.end()) return fail(KH_ERR_INVALID_ARG, "kh_free: pointer was not allocated by kh_alloc");
     const size_t cls = it->second;
     pool.live.erase(it);
-    pool.free_lists[cls].push_back(dptr);
     pool.in_use -= cls;
     pool.cached += cls;
+    auto pin = pool.pinned.find(dptr);
+    if (pin != pool.pinned.end()) {
+        pin->second->owned.emplace_back(dptr, cls);  // the graph still writes it
+        pool.pinned.erase(pin);
+    } else if (pool.capturing) {
+        pool.cap_free[cls].push_back(dptr);
+    } else {
+        pool.free_lists[cls].push_back(dptr);
+    }
     return KH_OK;
 }
 
 int kh_pool_trim(void) {
     KH_DEVICE_OR_RETURN(d);
+    KH_NOT_CAPTURING(d, "kh_pool_trim");
     int rc = hip_status(hipStreamSynchronize(d->stream), "hipStreamSynchronize");
     if (rc) return rc;
     kh::Pool& pool = kh::g_slots[d->id].pool;
@@ -304,6 +371,7 @@ int kh_memcpy_h2d(void* dst, const void* host_src, size_t bytes) {
     if (bytes == 0) return KH_OK;
     KH_REQUIRE(dst && host_src, "kh_memcpy_h2d: null pointer");
     KH_DEVICE_OR_RETURN(d);
+    KH_NOT_CAPTURING(d, "kh_memcpy_h2d");
     int rc = hip_status(hipMemcpyAsync(dst, host_src, bytes, hipMemcpyHostToDevice, d->stream), "hipMemcpyAsync(H2D)");
     if (rc) return rc;
     return hip_status(hipStreamSynchronize(d->stream), "hipStreamSynchronize");
@@ -313,6 +381,7 @@ int kh_memcpy_d2h(void* host_dst, const void* src, size_t bytes) {
     if (bytes == 0) return KH_OK;
     KH_REQUIRE(host_dst && src, "kh_memcpy_d2h: null pointer");
     KH_DEVICE_OR_RETURN(d);
+    KH_NOT_CAPTURING(d, "kh_memcpy_d2h");
     int rc = hip_status(hipMemcpyAsync(host_dst, src, bytes, hipMemcpyDeviceToHost, d->stream), "hipMemcpyAsync(D2H)");
     if (rc) return rc;
     return hip_status(hipStreamSynchronize(d->stream), "hipStreamSynchronize");
@@ -338,6 +407,8 @@ int kh_event_record(void* event) {
 
 int kh_event_elapsed_ms(void* start, void* end, float* ms) {
     KH_REQUIRE(start && end && ms, "kh_event_elapsed_ms: null argument");
+    KH_DEVICE_OR_RETURN(d);
+    KH_NOT_CAPTURING(d, "kh_event_elapsed_ms");
     int rc = hip_status(hipEventSynchronize(static_cast<hipEvent_t>(end)), "hipEventSynchronize");
     if (rc) return rc;
     return hip_status(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(end)),
@@ -347,6 +418,105 @@ int kh_event_elapsed_ms(void* start, void* end, float* ms) {
 int kh_event_destroy(void* event) {
     if (!event) return KH_OK;
     return hip_status(hipEventDestroy(static_cast<hipEvent_t>(event)), "hipEventDestroy");
+}
+
+// ---- graphs ---------------------------------------------------------------------
+
+int kh_graph_capture_begin(void) {
+    KH_DEVICE_OR_RETURN(d);
+    kh::Pool& pool = kh::g_slots[d->id].pool;
+    {
+        std::lock_guard<std::mutex> lk(pool.mu);
+        KH_REQUIRE(!pool.capturing, "kh_graph_capture_begin: a capture is already in progress");
+        pool.capturing = true;
+        pool.cap_used.clear();
+    }
+    int rc = hip_status(hipStreamBeginCapture(d->stream, hipStreamCaptureModeRelaxed), "hipStreamBeginCapture");
+    if (rc) {
+        std::lock_guard<std::mutex> lk(pool.mu);
+        pool.capturing = false;
+    }
+    return rc;
+}
+
+int kh_graph_capture_end(void** graph) {
+    KH_DEVICE_OR_RETURN(d);
+    kh::Pool& pool = kh::g_slots[d->id].pool;
+    {
+        std::lock_guard<std::mutex> lk(pool.mu);
+        KH_REQUIRE(pool.capturing, "kh_graph_capture_end: no capture in progress");
+    }
+    if (graph) *graph = nullptr;
+    hipGraph_t g = nullptr;
+    int rc = hip_status(hipStreamEndCapture(d->stream, &g), "hipStreamEndCapture");
+    hipGraphExec_t exec = nullptr;
+    if (!rc && graph) rc = hip_status(hipGraphInstantiate(&exec, g, nullptr, nullptr, 0), "hipGraphInstantiate");
+    if (g) (void)hipGraphDestroy(g);
+    std::lock_guard<std::mutex> lk(pool.mu);
+    pool.capturing = false;
+    if (rc || !graph) {
+        // Nothing captured will run: the capture's blocks are ordinary again.
+        for (auto& kv : pool.cap_free)
+            for (void* p : kv.second) pool.free_lists[kv.first].push_back(p);
+        pool.cap_free.clear();
+        pool.cap_used.clear();
+        if (exec) (void)hipGraphExecDestroy(exec);
+        return rc;
+    }
+    auto* gr = new kh::Graph;
+    gr->exec = exec;
+    gr->device = d->id;
+    for (auto& kv : pool.cap_free)
+        for (void* p : kv.second) gr->owned.emplace_back(p, kv.first);
+    pool.cap_free.clear();
+    for (void* p : pool.cap_used)
+        if (pool.live.count(p) && !pool.pinned.count(p)) {
+            pool.pinned[p] = gr;
+            gr->pinned.push_back(p);
+        }
+    pool.cap_used.clear();
+    pool.graphs_alive += 1;
+    *graph = gr;
+    return KH_OK;
+}
+
+int kh_graph_launch(void* graph) {
+    KH_REQUIRE(graph, "kh_graph_launch: null graph");
+    KH_DEVICE_OR_RETURN(d);
+    auto* gr = static_cast<kh::Graph*>(graph);
+    KH_REQUIRE(gr->device == d->id, "kh_graph_launch: graph was captured on another device");
+    KH_NOT_CAPTURING(d, "kh_graph_launch");
+    return hip_status(hipGraphLaunch(gr->exec, d->stream), "hipGraphLaunch");
+}
+
+int kh_graph_destroy(void* graph) {
+    if (!graph) return KH_OK;
+    KH_DEVICE_OR_RETURN(d);
+    auto* gr = static_cast<kh::Graph*>(graph);
+    KH_REQUIRE(gr->device == d->id, "kh_graph_destroy: graph was captured on another device");
+    KH_NOT_CAPTURING(d, "kh_graph_destroy");
+    // A launch may still be running.
+    int rc = hip_status(hipStreamSynchronize(d->stream), "hipStreamSynchronize");
+    if (rc) return rc;
+    (void)hipGraphExecDestroy(gr->exec);
+    kh::DeviceSlot& slot = kh::g_slots[d->id];
+    bool last;
+    {
+        std::lock_guard<std::mutex> lk(slot.pool.mu);
+        for (auto& b : gr->owned) slot.pool.free_lists[b.second].push_back(b.first);
+        for (void* p : gr->pinned) {
+            auto it = slot.pool.pinned.find(p);
+            if (it != slot.pool.pinned.end() && it->second == gr) slot.pool.pinned.erase(it);
+        }
+        last = --slot.pool.graphs_alive == 0;
+    }
+    delete gr;
+    if (last) {
+        std::lock_guard<std::mutex> lk(slot.scratch_mu);
+        for (void* p : slot.retired_scratch) (void)hipFree(p);
+        slot.retired_scratch.clear();
+    }
+    return KH_OK;
 }
 
 }  // extern "C"

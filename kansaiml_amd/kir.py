@@ -33,6 +33,7 @@ fused Q|K|V projection, heads merged in place).
 
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass, field
 from typing import Any
 
@@ -567,7 +568,7 @@ def _to_host(v):
     return v
 
 
-def _run(graph, args, plan, to_host, observe=None):
+def _run(graph, args, plan, to_host, observe=None, capturing=False):
     if not N.available():
         raise RuntimeError("run_hip: no gfx950 (MI355X) device available on this system")
     by_id = {n.id: n for n in graph.nodes}
@@ -595,6 +596,8 @@ def _run(graph, args, plan, to_host, observe=None):
                 if plan.last_use.get(i) == idx and i in vals:
                     _release(vals.pop(i))
     out = vals[graph.output]
+    if capturing:
+        return out
     N.synchronize()  # reports a non-finite quantizer input as ValueError
     return _to_host(out) if to_host else out
 
@@ -620,6 +623,100 @@ def run_hip_planned(graph, plan: MemoryPlan, pool: DevicePool | None, *args, to_
     released; the output's ownership passes to the caller.  `observe` is
     run_hip's per-node hook."""
     return _run(graph, args, plan, to_host, observe)
+
+
+class HipGraph:
+    """A planned run recorded once as a HIP graph and replayed with one host
+    call per run (hipGraphLaunch), where the reference re-interprets its
+    cached traced graph on every call (kir.py:536-555, 957-1068): the same
+    kernels on the same buffers, without the per-node Python dispatch.
+
+    The graph owns private input buffers (filled from the capture's
+    arguments) and writes one output buffer: launch(*args) copies its
+    arguments into the input buffers on the library stream, replays, and
+    returns the output -- a host array, or with to_host=False the output
+    DeviceTensor itself, which the next launch overwrites.  The graph reads
+    the constants' device copies (the model's weights) in place, so it is
+    only valid while they are.  close() (or garbage collection) destroys the
+    graph and returns its buffers to the pool.  Errors the kernels record
+    (non-finite quantizer input, token id out of range) surface on the next
+    synchronize, as for an eager run."""
+
+    def __init__(self, graph, plan: MemoryPlan, *args):
+        if not N.available():
+            raise RuntimeError("HipGraph: no gfx950 (MI355X) device available on this system")
+        by_id = {n.id: n for n in graph.nodes}
+        self._dtypes = [by_id[nid].dtype if by_id[nid].dtype in ("float32", "int32") else "float32"
+                        for nid in graph.inputs]
+        self.inputs = []
+        for a, dt in zip(args, self._dtypes):
+            if isinstance(a, DeviceTensor):
+                buf = DeviceTensor(a.shape, a.dtype)
+                N.call("kh_memcpy_d2d", buf.ptr, a.ptr, a.nbytes)
+            else:
+                buf = DeviceTensor.from_host(as_host_array(a, dt))
+            self.inputs.append(buf)
+        self.handle = None
+        self._graph = graph  # holds the constants' device buffers the nodes read
+        # One eager run first: it uploads the constants, sizes the scratch
+        # area and warms the pool, none of which can happen inside a capture.
+        _release(_run(graph, self.inputs, plan, to_host=False))
+        N.call("kh_graph_capture_begin")
+        try:
+            out = _run(graph, self.inputs, plan, to_host=False, capturing=True)
+        except BaseException:
+            N.lib().kh_graph_capture_end(None)
+            raise
+        h = ctypes.c_void_p()
+        N.call("kh_graph_capture_end", ctypes.byref(h))
+        self.handle = h
+        self.output = out
+
+    def launch(self, *args, to_host: bool = True):
+        if self.handle is None:
+            raise RuntimeError("HipGraph: the graph has been closed")
+        if len(args) != len(self.inputs):
+            raise ValueError(f"HipGraph: expected {len(self.inputs)} inputs, got {len(args)}")
+        for buf, a, dt in zip(self.inputs, args, self._dtypes):
+            if a is buf:
+                continue
+            if isinstance(a, DeviceTensor):
+                if tuple(a.shape) != tuple(buf.shape) or a.dtype != buf.dtype:
+                    raise ValueError(f"HipGraph: input {a.dtype}{list(a.shape)} does not match the captured "
+                                     f"{buf.dtype}{list(buf.shape)}")
+                N.call("kh_memcpy_d2d", buf.ptr, a.ptr, buf.nbytes)
+            else:
+                arr = np.ascontiguousarray(as_host_array(a, dt))
+                if tuple(arr.shape) != tuple(buf.shape):
+                    raise ValueError(f"HipGraph: input shape {list(arr.shape)} does not match the captured "
+                                     f"{list(buf.shape)}")
+                N.call("kh_memcpy_h2d", buf.ptr, arr.ctypes.data, buf.nbytes)
+        N.call("kh_graph_launch", self.handle)
+        if not to_host:
+            return self.output
+        N.synchronize()
+        return _to_host(self.output)
+
+    __call__ = launch
+
+    def close(self):
+        if self.handle is not None:
+            h, self.handle = self.handle, None
+            N.call("kh_graph_destroy", h)
+            _release(self.output)
+            for buf in self.inputs:
+                buf.release()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def capture_hip_planned(graph, plan: MemoryPlan, *args) -> HipGraph:
+    """run_hip_planned's work recorded as a HipGraph (see there)."""
+    return HipGraph(graph, plan, *args)
 
 
 def jit(fn):
