@@ -155,6 +155,64 @@ __device__ __forceinline__ unsigned store_block32_masked(const Epilogue& ep, int
     return store_block32_impl<FUSED, RG, true, MODE>(ep, i0, j, M, N, v, sc);
 }
 
+// store_block32 for a block inside the matrix in the common configuration --
+// fp32 output only (or one of the quantize passes), per-tensor activation
+// scale -- with the uniform choices (bias, activation, residual) taken once
+// per block instead of per element, and raw buffer accesses whose row offsets
+// are scalar (8*(r/4) + r%4 rows of N floats), so no element needs address
+// arithmetic.  Same arithmetic, in the same order, as store_block32_impl.
+// (rowblk, colblk): the block's first row and column; N <= 2^24.
+template <bool FUSED, int MODE>
+__device__ __forceinline__ unsigned store_block32_full(const Epilogue& ep, int64_t rowblk, int64_t colblk, int N,
+                                                       int lane, double sa, const i32x16& v,
+                                                       const kh::quant::Scale& sc) {
+    const int fr = lane & 31, fh = lane >> 5;
+    const int64_t j = colblk + fr;
+    const double sbj = ep.sb ? ep.sb[ep.sb_per_col ? j : 0] : 0.0;
+    const double s = sa * sbj;
+    const int64_t base = rowblk * N + colblk;
+    const uint32_t span = (uint32_t)N * 32u * 4u;  // the block's 32 rows, in bytes
+    const int voff = (4 * fh * N + fr) * 4;
+    auto row_off = [&](int r) { return (8 * (r >> 2) + (r & 3)) * N * 4; };
+    float res[16];
+    if (FUSED && ep.residual) {
+        const __amdgpu_buffer_rsrc_t rr = kh::pipe::make_rsrc(ep.residual + base, span);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) res[r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rr, voff, row_off(r), 0));
+    }
+    float y[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) y[r] = (float)((double)v[r] * s);
+    if (ep.bias) {
+        const float bj = ep.bias[j];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) y[r] = y[r] + bj;
+    }
+    if (FUSED && ep.act == kActGelu) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) y[r] = kh::gelu_exact(y[r]);
+    }
+    if (FUSED && ep.residual) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) y[r] = res[r] + y[r];
+    }
+    unsigned mx = 0;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = max(mx, kh::abs_bits32(y[r]));
+    if (MODE == kh::quant::kOutStore) {
+        const __amdgpu_buffer_rsrc_t ro = kh::pipe::make_rsrc(ep.out + base, span);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y[r]), ro, voff, row_off(r), 0);
+    } else if (MODE == kh::quant::kOutQuant) {
+        const __amdgpu_buffer_rsrc_t rq = kh::pipe::make_rsrc(ep.q + base, span / 4u);
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            __builtin_amdgcn_raw_buffer_store_b8((unsigned char)kh::quant::quant_one(y[r], sc), rq, voff / 4,
+                                                 row_off(r) / 4, 0);
+    }
+    return mx;
+}
+
 template <int BM, int BN, int BK, int WM, int WN>
 struct GemmCfg {
     static constexpr int kThreads = WM * WN * 64;
@@ -464,7 +522,19 @@ __global__ __launch_bounds__(512, BN == 256 ? 2 : 4) void gemm_i8_pingpong_kerne
     const int64_t row_base = (int64_t)tm * BM + wm * kWaveM + 4 * fh;
     const int64_t col_base = (int64_t)tn * BN + wn * kWaveN + fr;
     unsigned mx = 0;
-    if (rows_a == BM && rows_b == BN) {
+    const bool full = rows_a == BM && rows_b == BN;
+    if (full && !ep.acc && !ep.sa_per_row && (MODE != kh::quant::kOutStore || ep.out) && N <= (1 << 24)) {
+        const double sa = ep.sa[0];
+#pragma unroll
+        for (int a = 0; a < kTM; ++a)
+#pragma unroll
+            for (int b = 0; b < kTN; ++b) {
+                mx = max(mx, store_block32_full<FUSED, MODE>(ep, (int64_t)tm * BM + wm * kWaveM + a * 32,
+                                                             (int64_t)tn * BN + wn * kWaveN + b * 32, N, lane, sa,
+                                                             acc[a][b], sc));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+    } else if (full) {
 #pragma unroll
         for (int a = 0; a < kTM; ++a)
 #pragma unroll
