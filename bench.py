@@ -288,7 +288,7 @@ KERNELS = {
     "gemm_i8_8192": "gemm_i8_pingpong_kernel",
     "quant_rows_16384": "quant_rows_reg_kernel<4, 16>",
     "dequant_rows_16384": "dequant_vec_kernel",
-    "fp32_matmul_4096": "gemm_f32_kernel",
+    "fp32_matmul_4096": "gemm_f32_",
     "copy_1GiB": "copy16_kernel",
 }
 ALGO_BYTES = {"gemm_i8_8192": 2 * 8192 * 8192 + 4 * 8192 * 8192, "quant_rows_16384": 5 * 16384 * 16384,

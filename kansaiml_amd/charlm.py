@@ -111,10 +111,11 @@ class CharLM:
     one (or a float32 checkpoint, quantized per output channel on the way)
     into it in place.  `w` stays the construction-time weights."""
 
-    def __init__(self, w: CharLMWeights, producer_quant: bool = False):
-        """producer_quant: LayerNorm and fc1 (-> GELU) emit their int8 codes
-        directly instead of fp32 (kir.quant_fusion's option; less memory,
-        not faster)."""
+    def __init__(self, w: CharLMWeights, producer_quant: bool | str = "layer_norm"):
+        """producer_quant (kir.quant_fusion's option): "layer_norm" (the
+        default) -- each LayerNorm emits its int8 codes directly instead of
+        fp32 (two passes over its input; the fastest on MI355X); True -- fc1
+        (-> GELU) as well (less memory, slower); False -- neither."""
         self.w = w
         self.producer_quant = producer_quant
         up = DeviceTensor.from_host

@@ -15,8 +15,11 @@
 //                  in binary32, so masked keys are skipped; every row keeps
 //                  its diagonal key.
 // All fp32 (float accumulation order differs from the reference's CPU loops,
-// so results agree to rounding, not bit for bit).
+// and LayerNorm multiplies by 1 / sqrt(var + eps) rather than dividing, so
+// results agree to rounding, not bit for bit).
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 
 #include "kh_common.h"
 #include "kh_act.h"
@@ -68,59 +71,21 @@ __device__ __forceinline__ unsigned block4_max(unsigned v, unsigned* wmax) {
     return max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
 }
 
-// One row of LayerNorm by one wave; returns this lane's largest |out| bits.
-// VEC: D % 4 == 0 and 16-byte aligned rows, lanes hold float4s (D <= 1024).
-// MODE (kh::quant::kOut*): store the fp32 row to `out`, only reduce its
-// absmax, or store its int8 codes under scale `sc` to `q`.
-template <bool VEC, int MODE>
+// One row of LayerNorm by one wave (any D <= 1024; the scalar path for rows
+// that are not float4-aligned); returns this lane's largest |out| bits.  MODE
+// (kh::quant::kOut*): store the fp32 row to `out`, only reduce its absmax, or
+// store its int8 codes under scale `sc` to `q`.  The centred values are
+// multiplied by the row's 1 / sqrt(var + eps), as in layernorm_rows_vec.
+template <int MODE>
 __device__ __forceinline__ unsigned layernorm_row(const float* __restrict__ x, int64_t row, int D,
                                                   const float* __restrict__ w, const float* __restrict__ b, float eps,
                                                   float* __restrict__ out, int8_t* __restrict__ q,
                                                   const kh::quant::Scale& sc, int lane) {
     using namespace kh::quant;
-    typedef float f4 __attribute__((ext_vector_type(4)));
     const float* xr = x + row * D;
     float* orow = out + row * D;
     int8_t* qrow = q + row * D;
     unsigned mx = 0;
-    if (VEC) {
-        constexpr int kV = kLnMaxPerLane / 4;  // float4 per lane
-        f4 v[kV];
-        float s = 0.0f;
-#pragma unroll
-        for (int i = 0; i < kV; ++i) {
-            const int c4 = lane + i * 64;
-            v[i] = c4 * 4 < D ? reinterpret_cast<const f4*>(xr)[c4] : f4{0.f, 0.f, 0.f, 0.f};
-            s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
-        }
-        const float mean = wave_sum(s) / (float)D;
-        float ss = 0.0f;
-#pragma unroll
-        for (int i = 0; i < kV; ++i) {
-            if ((lane + i * 64) * 4 < D) {
-                v[i] -= mean;
-                ss += (v[i].x * v[i].x + v[i].y * v[i].y) + (v[i].z * v[i].z + v[i].w * v[i].w);
-            }
-        }
-        const float var = wave_sum(ss) / (float)D;
-        const float denom = sqrtf(var + eps);
-#pragma unroll
-        for (int i = 0; i < kV; ++i) {
-            const int c4 = lane + i * 64;
-            if (c4 * 4 < D) {
-                const f4 wv = reinterpret_cast<const f4*>(w)[c4], bv = reinterpret_cast<const f4*>(b)[c4];
-                f4 y;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    y[e] = v[i][e] / denom * wv[e] + bv[e];
-                    mx = max(mx, kh::abs_bits32(y[e]));
-                }
-                if (MODE == kOutStore) reinterpret_cast<f4*>(orow)[c4] = y;
-                if (MODE == kOutQuant) reinterpret_cast<unsigned*>(qrow)[c4] = pack4(y, sc);
-            }
-        }
-        return mx;
-    }
     float v[kLnMaxPerLane];
     float s = 0.0f;
 #pragma unroll
@@ -138,16 +103,99 @@ __device__ __forceinline__ unsigned layernorm_row(const float* __restrict__ x, i
         v[i] = cv;
         ss += cv * cv;
     }
-    const float var = wave_sum(ss) / (float)D;
-    const float denom = sqrtf(var + eps);
+    const float inv = 1.0f / sqrtf(wave_sum(ss) / (float)D + eps);
 #pragma unroll
     for (int i = 0; i < kLnMaxPerLane; ++i) {
         const int c = lane + i * 64;
         if (c < D) {
-            const float y = v[i] / denom * w[c] + b[c];
+            const float y = v[i] * inv * w[c] + b[c];
             if (MODE == kOutStore) orow[c] = y;
             if (MODE == kOutQuant) qrow[c] = (int8_t)quant_one(y, sc);
             mx = max(mx, kh::abs_bits32(y));
+        }
+    }
+    return mx;
+}
+
+// The vectorized LayerNorm of kLnRowsPerWave consecutive rows by one wave
+// (D % 4 == 0, D <= 256 * KV, 16-byte aligned rows): every row's loads are
+// issued before any arithmetic and the weight and bias once, so the wave
+// waits one memory round trip for all of its rows.  Mean and variance as in
+// layernorm_row; the centred values are multiplied by the row's correctly
+// rounded 1 / sqrt(var + eps) instead of divided by sqrt(var + eps) (within
+// 1 ulp of the quotient; the division's ~10-instruction sequence per element
+// made the kernel compute-bound).  Rows >= `rows` are computed on zeros and
+// not stored.
+constexpr int kLnRowsPerWave = 4;
+
+template <int KV, int MODE>
+__device__ __forceinline__ unsigned layernorm_rows_vec(const float* __restrict__ x, int64_t row0, int64_t rows,
+                                                       int D, const float* __restrict__ w,
+                                                       const float* __restrict__ b, float eps,
+                                                       float* __restrict__ out, int8_t* __restrict__ q,
+                                                       const kh::quant::Scale& sc, int lane) {
+    using namespace kh::quant;
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    constexpr int R = kLnRowsPerWave;
+    const int D4 = D / 4;
+    f4 v[R][KV];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < KV; ++i) {
+            const int c4 = lane + i * 64;
+            v[r][i] = (row0 + r < rows && c4 < D4) ? reinterpret_cast<const f4*>(x + (row0 + r) * D)[c4]
+                                                   : f4{0.f, 0.f, 0.f, 0.f};
+        }
+    f4 wv[KV], bv[KV];
+#pragma unroll
+    for (int i = 0; i < KV; ++i) {
+        const int c4 = lane + i * 64;
+        wv[i] = c4 < D4 ? reinterpret_cast<const f4*>(w)[c4] : f4{0.f, 0.f, 0.f, 0.f};
+        bv[i] = c4 < D4 ? reinterpret_cast<const f4*>(b)[c4] : f4{0.f, 0.f, 0.f, 0.f};
+    }
+    float mean[R], sumsq[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < KV; ++i) s += (v[r][i].x + v[r][i].y) + (v[r][i].z + v[r][i].w);
+        mean[r] = s;
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) mean[r] = wave_sum(mean[r]) / (float)D;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < KV; ++i) {
+            if (lane + i * 64 < D4) {
+                v[r][i] -= mean[r];
+                ss += (v[r][i].x * v[r][i].x + v[r][i].y * v[r][i].y) + (v[r][i].z * v[r][i].z + v[r][i].w * v[r][i].w);
+            }
+        }
+        sumsq[r] = ss;
+    }
+    float inv[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) inv[r] = 1.0f / sqrtf(wave_sum(sumsq[r]) / (float)D + eps);
+    unsigned mx = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        if (row0 + r >= rows) continue;
+#pragma unroll
+        for (int i = 0; i < KV; ++i) {
+            const int c4 = lane + i * 64;
+            if (c4 < D4) {
+                f4 y;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    y[e] = v[r][i][e] * inv[r] * wv[i][e] + bv[i][e];
+                    mx = max(mx, kh::abs_bits32(y[e]));
+                }
+                if (MODE == kOutStore) reinterpret_cast<f4*>(out + (row0 + r) * D)[c4] = y;
+                if (MODE == kOutQuant) reinterpret_cast<unsigned*>(q + (row0 + r) * D)[c4] = pack4(y, sc);
+            }
         }
     }
     return mx;
@@ -159,7 +207,9 @@ __device__ __forceinline__ unsigned layernorm_row(const float* __restrict__ x, i
 // tensor's scale (workgroup 0 stores it to *qscale).
 constexpr int kLnRowsPerBlock = 16;
 
-template <bool VEC, int MODE>
+// KV: 0 for the scalar path, else float4 columns per lane of the vectorized
+// path (2 for D <= 512, 4 for D <= 1024).
+template <int KV, int MODE>
 __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict__ x, int64_t rows, int D,
                                                         const float* __restrict__ w, const float* __restrict__ b,
                                                         float eps, float* __restrict__ out,
@@ -178,10 +228,16 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict_
         }
     }
     unsigned mx = 0;
+    if constexpr (KV > 0) {
+        static_assert(kLnRowsPerBlock == 4 * kLnRowsPerWave, "four waves");
+        const int64_t row0 = (int64_t)blockIdx.x * kLnRowsPerBlock + (threadIdx.x >> 6) * kLnRowsPerWave;
+        mx = layernorm_rows_vec<KV, MODE>(x, row0, rows, D, w, b, eps, out, q, sc, lane);
+    } else {
 #pragma unroll 1
-    for (int k = threadIdx.x >> 6; k < kLnRowsPerBlock; k += 4) {
-        const int64_t row = (int64_t)blockIdx.x * kLnRowsPerBlock + k;
-        if (row < rows) mx = max(mx, layernorm_row<VEC, MODE>(x, row, D, w, b, eps, out, q, sc, lane));
+        for (int k = threadIdx.x >> 6; k < kLnRowsPerBlock; k += 4) {
+            const int64_t row = (int64_t)blockIdx.x * kLnRowsPerBlock + k;
+            if (row < rows) mx = max(mx, layernorm_row<MODE>(x, row, D, w, b, eps, out, q, sc, lane));
+        }
     }
     if (MODE != kOutQuant && parts) {
         // Per-workgroup max |out| bits, for a following per-tensor quantize.
@@ -434,11 +490,14 @@ int kh_layernorm_ex(const float* x, int64_t rows, int D, const float* weight, co
                      kh::aligned(bias, 16);
     using kh::quant::kOutStore;
     unsigned* parts = fused ? absmax_parts : nullptr;
-    if (vec)
-        layernorm_kernel<true, kOutStore><<<(unsigned)blocks, 256, 0, d->stream>>>(
+    if (vec && D <= 512)
+        layernorm_kernel<2, kOutStore><<<(unsigned)blocks, 256, 0, d->stream>>>(
+            x, rows, D, weight, bias, eps, out, parts, nullptr, nullptr, 0, nullptr, d->fault);
+    else if (vec)
+        layernorm_kernel<4, kOutStore><<<(unsigned)blocks, 256, 0, d->stream>>>(
             x, rows, D, weight, bias, eps, out, parts, nullptr, nullptr, 0, nullptr, d->fault);
     else
-        layernorm_kernel<false, kOutStore><<<(unsigned)blocks, 256, 0, d->stream>>>(
+        layernorm_kernel<0, kOutStore><<<(unsigned)blocks, 256, 0, d->stream>>>(
             x, rows, D, weight, bias, eps, out, parts, nullptr, nullptr, 0, nullptr, d->fault);
     int rc = kh::launch_status("layernorm");
     if (rc || !absmax_parts) return rc;
@@ -476,17 +535,16 @@ int kh_layernorm_quant(const float* x, int64_t rows, int D, const float* weight,
     // Pass 1 reduces the normalized values' absmax into one partial per
     // workgroup without storing them; pass 2 recomputes them (the same
     // arithmetic, so the same values) and stores their codes.
-    if (vec) {
-        layernorm_kernel<true, kOutMaxOnly><<<(unsigned)blocks, 256, 0, d->stream>>>(
+    auto passes = [&](auto kv) {
+        constexpr int KV = decltype(kv)::value;
+        layernorm_kernel<KV, kOutMaxOnly><<<(unsigned)blocks, 256, 0, d->stream>>>(
             x, rows, D, weight, bias, eps, nullptr, parts, nullptr, nullptr, 0, nullptr, d->fault);
-        layernorm_kernel<true, kOutQuant><<<(unsigned)blocks, 256, 0, d->stream>>>(
+        layernorm_kernel<KV, kOutQuant><<<(unsigned)blocks, 256, 0, d->stream>>>(
             x, rows, D, weight, bias, eps, nullptr, nullptr, q, parts, (int)blocks, scale, d->fault);
-    } else {
-        layernorm_kernel<false, kOutMaxOnly><<<(unsigned)blocks, 256, 0, d->stream>>>(
-            x, rows, D, weight, bias, eps, nullptr, parts, nullptr, nullptr, 0, nullptr, d->fault);
-        layernorm_kernel<false, kOutQuant><<<(unsigned)blocks, 256, 0, d->stream>>>(
-            x, rows, D, weight, bias, eps, nullptr, nullptr, q, parts, (int)blocks, scale, d->fault);
-    }
+    };
+    if (vec && D <= 512) passes(std::integral_constant<int, 2>{});
+    else if (vec) passes(std::integral_constant<int, 4>{});
+    else passes(std::integral_constant<int, 0>{});
     return kh::launch_status("layernorm_quant");
 }
 

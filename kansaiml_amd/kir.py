@@ -226,23 +226,24 @@ def _is_bias(graph, by_id, x_id, b_id) -> bool:
     return len(xs) == 2 and len(bs) == 1 and xs[1] == bs[0]
 
 
-def quant_fusion(graph, producer_quant: bool = False) -> Graph:
+def quant_fusion(graph, producer_quant: bool | str = False) -> Graph:
     """Fuses, where the intermediate has no other user:
       int8_matmul -> dequantize [-> add(bias)] [-> gelu] [-> add(x, .)]
                                                  =>  int8_linear
       matmul -> add(bias)                        =>  matmul_bias
       add(bias) -> relu                          =>  fused_bias_relu
-    and, with producer_quant=True,
+    and, with producer_quant=True (both) or "layer_norm" (the second only),
       ... the int8_linear chain -> quantize (per tensor) => int8_linear_quant
       layer_norm -> quantize (per tensor)        =>  layer_norm_quant
     int8_linear's attrs record what it absorbed: bias (bool), act ("gelu" or
     None) and residual (bool; the residual operand comes last).  The *_quant
     nodes produce the quantized tensor directly: their kernels run the
     producer twice (absmax, then codes) and never write the fp32 values.
-    That saves the fp32 intermediate's memory but not time on MI355X (the
-    GELU epilogue and LayerNorm are VALU- and latency-bound, so a second
-    pass costs more than the fp32 round trip it replaces), hence off by
-    default.  Then every int8_linear, layer_norm or causal_attention whose
+    That saves the fp32 intermediate's memory; on MI355X it saves time for
+    LayerNorm (two passes over its input cost less than writing the fp32
+    values and reading them back) but not for the GEMM, whose VALU-bound
+    epilogue (binary64 dequantize, exact-erf GELU) the second pass repeats.
+    Then every int8_linear, layer_norm or causal_attention whose
     output feeds a per-tensor quantize is marked absmax=True: its kernel
     writes the absmax partials that quantize needs, so the quantize reads
     its input once.
@@ -260,10 +261,13 @@ def quant_fusion(graph, producer_quant: bool = False) -> Graph:
     # absorbed nodes are dropped.
     fused, absorbed = {}, set()
 
+    if producer_quant not in (False, True, "layer_norm"):
+        raise ValueError(f"producer_quant must be False, True or 'layer_norm', not {producer_quant!r}")
+
     def tensor_quantize(nid):
         """The per-tensor quantize that is the only user of nid, if any (and
-        producer fusion is on)."""
-        if not producer_quant:
+        producer fusion is on for nid's kind of node)."""
+        if producer_quant is not True and producer_quant != by_id[nid].op:
             return None
         q = only_user(nid)
         if q is not None and by_id[q].op == "quantize" and by_id[q].attrs.get("granularity", "tensor") == "tensor":

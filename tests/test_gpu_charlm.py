@@ -172,7 +172,7 @@ def _check_node(node, got, ins):
         raise AssertionError(f"unchecked node kind {op}")
 
 
-@pytest.mark.parametrize("seq,producer_quant", [(64, False), (100, False), (100, True)])
+@pytest.mark.parametrize("seq,producer_quant", [(64, False), (100, False), (100, True), (100, "layer_norm")])
 def test_small_model_matches_restatement(G, seq, producer_quant):
     """Two layers of the C4 architecture (d 384, 6 heads, FFN 1536, vocab 65)
     with nonzero biases, checked node by node: every node's GPU output
@@ -203,10 +203,16 @@ def test_small_model_matches_restatement(G, seq, producer_quant):
     # GELU and the residual adds are fused into the int8_linear epilogues;
     # per-tensor quantizes read absmax partials their producers wrote.  With
     # producer_quant, every LayerNorm and fc1 (-> GELU) output feeds only a
-    # per-tensor quantize, so those producers emit the codes themselves.
+    # per-tensor quantize, so those producers emit the codes themselves
+    # ("layer_norm": the LayerNorms only).
     acts = {(n.op, n.attrs.get("act"), bool(n.attrs.get("residual"))) for n in g.nodes
             if n.op in ("int8_linear", "int8_linear_quant")}
-    if producer_quant:
+    if producer_quant == "layer_norm":
+        assert checked == {"embedding", "layer_norm_quant", "quantize", "int8_linear", "causal_attention"}
+        assert acts == {("int8_linear", None, False), ("int8_linear", "gelu", False), ("int8_linear", None, True)}
+        assert all(n.attrs.get("absmax") for n in g.nodes
+                   if n.op == "causal_attention" or (n.op == "int8_linear" and n.attrs.get("act")))
+    elif producer_quant:
         assert checked == {"embedding", "layer_norm_quant", "quantize", "int8_linear", "int8_linear_quant",
                            "causal_attention"}
         assert acts == {("int8_linear", None, False), ("int8_linear_quant", "gelu", False),

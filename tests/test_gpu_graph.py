@@ -31,7 +31,7 @@ def _bits(a):
     return np.ascontiguousarray(a).view(np.uint32)
 
 
-@pytest.mark.parametrize("producer_quant", [False, True])
+@pytest.mark.parametrize("producer_quant", [False, "layer_norm", True])
 def test_replays_equal_eager_runs(G, producer_quant):
     N, D = G
     from kansaiml_amd.charlm import CharLM, CharLMWeights

@@ -129,6 +129,14 @@ def test_quantize_producers_fuse_into_quant_nodes():
     lq = [n for n in f.nodes if n.op == "int8_linear_quant"][0]
     assert lq.dtype == "int8" and lq.attrs["act"] == "gelu" and lq.attrs["bias"]
     assert [n for n in f.nodes if n.op == "layer_norm_quant"][0].dtype == "int8"
+    # "layer_norm": the LayerNorm emits codes, the GEMM chain keeps its fp32
+    # output (and absmax partials for the separate quantize).
+    fl = kir.quant_fusion(g, producer_quant="layer_norm")
+    opsl = [n.op for n in fl.nodes if n.op not in ("placeholder", "constant")]
+    assert "layer_norm_quant" in opsl and "int8_linear_quant" not in opsl and "layer_norm" not in opsl
+    assert [n for n in fl.nodes if n.op == "int8_linear" and n.attrs.get("act") == "gelu"][0].attrs["absmax"]
+    with pytest.raises(ValueError, match="producer_quant"):
+        kir.quant_fusion(g, producer_quant="gelu")
 
     def shared(x):
         h = x.layer_norm(g1, b1)
