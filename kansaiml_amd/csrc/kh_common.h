@@ -46,6 +46,10 @@ Device* current();
 // reuse it safely.  Returns nullptr (and sets the last error) on OOM.
 void* scratch(Device* d, size_t bytes);
 
+// True while a graph capture (kh_graph_capture_begin .. _end) is open on the
+// device's library stream: host-synchronous work must refuse to run.
+bool capturing(Device* d);
+
 // ---- argument checks ---------------------------------------------------------
 
 __host__ __device__ inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
@@ -60,6 +64,10 @@ __host__ __device__ inline bool aligned(const void* p, size_t a) { return (reint
 #define KH_DEVICE_OR_RETURN(d)                                       \
     ::kh::Device* d = ::kh::current();                               \
     if (!d) return KH_ERR_NO_DEVICE
+
+// Host-synchronous calls cannot be recorded into a graph.
+#define KH_NOT_CAPTURING(d, what) \
+    KH_REQUIRE(!::kh::capturing(d), what ": not allowed while a graph is being captured")
 
 // Non-finite detection uses the IEEE bit pattern: for |v| (sign cleared) the
 // unsigned order of the bits is the numeric order, and every NaN/inf pattern

@@ -91,6 +91,7 @@ int kh_probe_stream_read(const void* p, int64_t bytes) {
 int kh_probe_mfma_i8(const int8_t* operands, int64_t bytes, int64_t iters, double* tops, double* clock_mhz) {
     KH_REQUIRE(iters > 0 && tops && clock_mhz, "kh_probe_mfma_i8: bad arguments");
     KH_DEVICE_OR_RETURN(d);
+    KH_NOT_CAPTURING(d, "kh_probe_mfma_i8");
     const int64_t need = (int64_t)d->cus * kProbeThreads * 8 * 16;
     KH_REQUIRE(operands && bytes >= need && kh::aligned(operands, 16),
                "kh_probe_mfma_i8: operands must be 16-byte aligned and hold cus * 64 KiB");
@@ -102,19 +103,24 @@ int kh_probe_mfma_i8(const int8_t* operands, int64_t bytes, int64_t iters, doubl
     rc = kh::hip_status(hipEventCreate(&e0), "hipEventCreate");
     if (rc) return rc;
     rc = kh::hip_status(hipEventCreate(&e1), "hipEventCreate");
-    if (rc) return rc;
-    hipEventRecord(e0, d->stream);
-    mfma_probe_kernel<<<(unsigned)d->cus, kProbeThreads, 0, d->stream>>>(operands, iters, clocks,
-                                                                        reinterpret_cast<int*>(clocks + 4));
-    rc = kh::launch_status("mfma_probe");
-    hipEventRecord(e1, d->stream);
+    if (rc) {
+        (void)hipEventDestroy(e0);
+        return rc;
+    }
+    rc = kh::hip_status(hipEventRecord(e0, d->stream), "hipEventRecord(probe)");
+    if (!rc) {
+        mfma_probe_kernel<<<(unsigned)d->cus, kProbeThreads, 0, d->stream>>>(operands, iters, clocks,
+                                                                            reinterpret_cast<int*>(clocks + 4));
+        rc = kh::launch_status("mfma_probe");
+    }
+    if (!rc) rc = kh::hip_status(hipEventRecord(e1, d->stream), "hipEventRecord(probe)");
     if (!rc) rc = kh::hip_status(hipEventSynchronize(e1), "hipEventSynchronize(probe)");
     float ms = 0.0f;
     if (!rc) rc = kh::hip_status(hipEventElapsedTime(&ms, e0, e1), "hipEventElapsedTime(probe)");
     unsigned long long h[2] = {0, 0};
     if (!rc) rc = kh::hip_status(hipMemcpy(h, clocks, sizeof h, hipMemcpyDeviceToHost), "read probe clocks");
-    hipEventDestroy(e0);
-    hipEventDestroy(e1);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
     if (rc) return rc;
     const double ops = (double)d->cus * (kProbeThreads / 64) * (double)iters * 16.0 * 65536.0;
     *tops = ops / (ms * 1e-3) / 1e12;

@@ -199,9 +199,6 @@ bool capturing(Device* d) {
 using kh::fail;
 using kh::hip_status;
 
-// Host-synchronous calls cannot be recorded into a graph.
-#define KH_NOT_CAPTURING(d, what) \
-    KH_REQUIRE(!::kh::capturing(d), what ": not allowed while a graph is being captured")
 
 extern "C" {
 
