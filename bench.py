@@ -17,7 +17,7 @@ CPU baseline: the reference's own compiled backend/cpu/src/Ops.cpp matmul
 dequantizing the weight (python/kansai/quantize.py:115-122) -- on one core,
 over a time-bounded slab of rows of the same workload.
 
-    python bench.py [--gpus 1] [--steps 50] [--warmup 50] [--no-cpu] [--only gemm,probe,quant,f32,skinny,c4,copy]
+    python bench.py [--gpus 1] [--steps 50] [--warmup 50] [--no-cpu] [--only gemm,probe,quant,f32,c1,skinny,c4,copy]
 
 Profiling (the summaries under profiles/ are made this way):
     rocprofv3 --kernel-trace --stats -d OUT/trace -o run --output-format csv -- python3 bench.py --no-cpu
@@ -227,6 +227,56 @@ def bench_skinny(steps, warmup):
     return rows
 
 
+class _Linear:
+    """An nn.Linear-like holder (.weight [in, out], .bias [out])."""
+
+    def __init__(self, weight, bias):
+        self.weight, self.bias = weight, bias
+
+
+def _c1_inputs():
+    gen = np.random.Generator(np.random.PCG64(0))
+    x = gen.standard_normal((64, 512), dtype=np.float32)
+    w = gen.standard_normal((512, 512), dtype=np.float32) * np.float32(0.02)
+    return x, w, np.zeros(512, np.float32)
+
+
+def bench_c1(steps, warmup):
+    """Config C1, the reference's CPU-runnable case: an int8 quantized Linear,
+    x fp32 [64, 512] ~N(0,1), W fp32 [512, 512] ~N(0, 0.02), bias zeros,
+    per-tensor scales for x and W (seed 0; W quantized once at construction).
+    Latency-bound, so reported as microseconds per call two ways: the two
+    kernels back to back (one-launch per-tensor quantize of x; the skinny
+    int8 GEMM with the dequantize and bias fused) and the eager QLinear call
+    (Python dispatch and output allocation included)."""
+    from kansaiml_amd import _native as Nn
+    from kansaiml_amd.device import DeviceTensor as D
+    from kansaiml_amd.quantize import QLinear
+    x, w, b = _c1_inputs()
+    layer = QLinear(_Linear(w, b), mode="int8", act_granularity="tensor", weight_granularity="tensor")
+    xd = D.from_host(x)
+    q, s, out = D([64, 512], "int8"), D([1], "float64"), D([64, 512])
+    wq, ws, bd = layer.qweight.codes, layer.qweight.scales, layer.bias
+    quant = Nn.lib().kh_quantize_tensor
+    gemm = Nn.lib().kh_gemm_i8
+    qargs = (xd.ptr, 64 * 512, q.ptr, s.ptr)
+    gargs = (q.ptr, wq.ptr, 64, 512, 512, s.ptr, 0, ws.ptr, 0, bd.ptr, out.ptr, None)
+
+    def kernels():
+        quant(*qargs)
+        gemm(*gargs)
+
+    Nn.call("kh_quantize_tensor", *qargs)  # checked once; the timed calls skip the status check
+    Nn.call("kh_gemm_i8", *gargs)
+
+    us_kernels = time_kernel(kernels, steps, warmup) * 1e3
+    us_eager = time_kernel(lambda: layer(xd), steps, warmup) * 1e3
+    ops = 2 * 64 * 512 * 512
+    return {"workload": "C1 int8 quantized Linear x[64,512] @ W[512,512] + b, per-tensor scales (seed 0)",
+            "us_kernels_back_to_back": round(us_kernels, 2), "us_eager_call": round(us_eager, 2), "ops": ops,
+            "TOPS_kernels": round(ops / (us_kernels * 1e-6) / 1e12, 3), "bound": "latency"}
+
+
 def bench_c4(steps, warmup):
     """Config C4: the int8 char-LM forward (vocab 65, d 384, 6 heads, 6 layers,
     FFN 1536, seq 256, batch 64; int8 per-channel weights ~N(0, 0.02),
@@ -357,6 +407,27 @@ def summarize(root):
     return lines, traffic
 
 
+def cpu_c1(reps=200):
+    """C1 on the host as the reference runs it (quantize.py:115-122 with the
+    weight quantized once): x @ dequantize(W) + b through the reference's
+    compiled fp32 i-k-j matmul and bias add (backend/cpu/src/Ops.cpp:322-339,
+    34-38; oracle/_ref), one core, microseconds per call."""
+    from oracle import oracle as O
+    x, w, b = _c1_inputs()
+    qw, sw = O.ko_quantize_tensor(w)
+    wdeq = O.ko_dequantize_tensor(qw, sw).reshape(w.shape)  # dequantize(W), once
+    use_ref = O.ref_available()
+    mm = O.ref_matmul if use_ref else O.ko_matmul_f32
+    add = O.ref_add_bias if use_ref else (lambda y, bb: (y + bb).astype(np.float32))
+    add(mm(x, wdeq), b)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        add(mm(x, wdeq), b)
+    us = (time.perf_counter() - t0) / reps * 1e6
+    return {"us_per_call": round(us, 1), "cores": 1, "kind": "reference" if use_ref else "port",
+            "sample": f"{reps} calls of x @ dequantize(W) + b on C1's inputs (the reference's weight-only qlinear)"}
+
+
 def cpu_baseline(budget_s=12.0):
     """The reference's compiled fp32 i-k-j matmul (oracle/_ref, built from
     backend/cpu/src/Ops.cpp) on dequantized operands of the C3a workload,
@@ -397,8 +468,8 @@ def main():
     # steps let every leg reach its sustained rate before timing.
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", default="gemm,probe,quant,f32,skinny,c4",
-                    help="comma list of gemm,probe,quant,f32,skinny,c4,copy")
+    ap.add_argument("--only", default="gemm,probe,quant,f32,c1,skinny,c4",
+                    help="comma list of gemm,probe,quant,f32,c1,skinny,c4,copy")
     ap.add_argument("--summarize", metavar="DIR", help="summarize rocprofv3 CSV output and exit")
     args = ap.parse_args()
     if args.summarize:
@@ -442,6 +513,12 @@ def main():
         f_ms, f_tflops = bench_f32(H, D, max(5, args.steps // 2), max(2, args.warmup // 2))
         log(f"fp32 matmul: {f_ms:.4f} ms, {f_tflops:.1f} TFLOP/s")
         Nn.call("kh_pool_trim")
+    c1 = None
+    if "c1" in only:
+        log("C1 int8 quantized Linear ...")
+        c1 = bench_c1(max(50, args.steps), args.warmup)
+        log(f"C1: {c1['us_kernels_back_to_back']:.2f} us per call (kernels back to back), "
+            f"{c1['us_eager_call']:.2f} us eager")
     skinny = None
     if "skinny" in only:
         log("skinny decode GEMMs C5 ...")
@@ -463,6 +540,9 @@ def main():
         log("CPU baseline ...")
         cpu = cpu_baseline()
         log(f"CPU baseline {cpu['value']:.6f} TOPS")
+        if c1 is not None:
+            c1["cpu"] = cpu_c1()
+            log(f"C1 on the CPU: {c1['cpu']['us_per_call']:.1f} us per call")
 
     result = {
         "metric": "int8 GEMM TOPS @8192^3 (% of i8 MFMA peak); quant/dequant GB/s (% HBM)",
@@ -499,6 +579,7 @@ def main():
                                      "traffic": None}},
         "skinny_decode": {"workload": "C5 kh_linear_i8: per-token quantize + int8 GEMM, per-channel weights",
                           "bytes": "N*K + 8N + 4MK + 2MK + 4MN", "rows": skinny},
+        "c1_linear": c1,
         "c4_forward": c4,
         "cpu_baseline": cpu,
         "device": info,

@@ -569,7 +569,7 @@ __global__ __launch_bounds__(512, BN == 256 ? 2 : 4) void gemm_i8_pingpong_kerne
 }
 
 // ---------------------------------------------------------------------------
-// Skinny GEMM for decode-style shapes (M <= 32): weight streaming.
+// Skinny GEMM for decode-style and small shapes (M <= 64): weight streaming.
 //
 // A workgroup owns 16 output columns for all M rows; its SKW waves split K,
 // each streaming its slice of those 16 packed weight rows (16 B per lane per
@@ -696,7 +696,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_i8_skinny_kernel(const
 }
 
 bool skinny_fits(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K) {
-    return M >= 1 && M <= 32 && K > 0 && K % (64 * kSkinnyWaves) == 0 && kh::aligned(A, 16) &&
+    return M >= 1 && M <= 64 && K > 0 && K % (64 * kSkinnyWaves) == 0 && kh::aligned(A, 16) &&
            kh::aligned(B, 16) && M * K <= 0xFFFFFFFFLL && N * K <= 0xFFFFFFFFLL && N <= 0x7FFFFFFF;
 }
 
@@ -738,7 +738,8 @@ int launch_skinny(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, in
         else go(mt, N1(), std::integral_constant<int, 1>(), F());
     };
     if (M <= 16) pick(std::integral_constant<int, 1>());
-    else pick(std::integral_constant<int, 2>());
+    else if (M <= 32) pick(std::integral_constant<int, 2>());
+    else pick(std::integral_constant<int, 4>());
     return kh::launch_status("gemm_i8_skinny");
 }
 

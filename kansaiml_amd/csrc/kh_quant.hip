@@ -188,6 +188,53 @@ __global__ __launch_bounds__(256) void quant_tensor_kernel(const float* __restri
     }
 }
 
+// Per-tensor quantize of a small tensor (n <= kSmallPer * 4 * 1024, x 16-byte
+// and q 4-byte aligned) in one launch: one 1024-thread workgroup holds the
+// values in registers, reduces the absmax, and stores the codes -- the same
+// arithmetic as the two-pass path, without the second launch (latency-bound
+// sizes such as a Linear's activations).
+constexpr int kSmallThreads = 1024;
+constexpr int kSmallPer = 16;  // float4 per thread
+constexpr int64_t kSmallTensor = (int64_t)kSmallPer * 4 * kSmallThreads;
+
+__global__ __launch_bounds__(kSmallThreads) void quant_tensor_small_kernel(const float* __restrict__ x, int64_t n,
+                                                                           int8_t* __restrict__ q,
+                                                                           double* __restrict__ scale,
+                                                                           unsigned* __restrict__ fault) {
+    __shared__ unsigned red[kSmallThreads / 64];
+    const int tid = threadIdx.x;
+    const int n4 = (int)(n >> 2), tail = (int)(n - 4 * (int64_t)n4);
+    const f32x4* x4 = reinterpret_cast<const f32x4*>(x);
+    f32x4 v[kSmallPer];
+    AbsMax am;
+#pragma unroll
+    for (int i = 0; i < kSmallPer; ++i) {
+        const int idx = tid + i * kSmallThreads;
+        v[i] = idx < n4 ? x4[idx] : f32x4{0.f, 0.f, 0.f, 0.f};
+        if (idx < n4) am.add4(v[i]);
+    }
+    const float xt = tid < tail ? x[4 * (int64_t)n4 + tid] : 0.0f;
+    if (tid < tail) am.add1(xt);
+    unsigned mb = wave_max(am.bits());
+    if ((tid & 63) == 0) red[tid >> 6] = mb;
+    __syncthreads();
+    mb = red[0];
+#pragma unroll
+    for (int w = 1; w < kSmallThreads / 64; ++w) mb = max(mb, red[w]);
+    const Scale sc = make_scale(mb);
+    if (tid == 0) {
+        scale[0] = sc.s;
+        if (sc.bad) flag_nonfinite(fault);
+    }
+    unsigned* q4 = reinterpret_cast<unsigned*>(q);
+#pragma unroll
+    for (int i = 0; i < kSmallPer; ++i) {
+        const int idx = tid + i * kSmallThreads;
+        if (idx < n4) q4[idx] = pack4(v[i], sc);
+    }
+    if (tid < tail) q[4 * (int64_t)n4 + tid] = (int8_t)quant_one(xt, sc);
+}
+
 // ---------------------------------------------------------------------------
 // Per-column (per output channel) absmax of a [k, n] weight, and the
 // transpose-quantize that packs codes K-contiguous ([n, k]).
@@ -415,6 +462,10 @@ int kh_quantize_tensor(const float* x, int64_t n, int8_t* q, double* scale) {
     KH_DEVICE_OR_RETURN(d);
     if (n == 0) return fill_scales_one(d, scale, 1);
     const bool vec = kh::aligned(x, 16) && kh::aligned(q, 4);
+    if (vec && n <= kSmallTensor) {
+        quant_tensor_small_kernel<<<1, kSmallThreads, 0, d->stream>>>(x, n, q, scale, d->fault);
+        return kh::launch_status("quant_tensor_small");
+    }
     unsigned* partials = nullptr;
     int nparts = 0;
     int rc = tensor_absmax(d, x, n, vec, &partials, &nparts);

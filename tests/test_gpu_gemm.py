@@ -116,7 +116,7 @@ def test_gemm_i8_c3a_full_size(hip):
     np.testing.assert_array_equal(acc[::97][:, cols], eacc_c)
 
 
-@pytest.mark.parametrize("M", [1, 3, 8, 16, 17, 32])
+@pytest.mark.parametrize("M", [1, 3, 8, 16, 17, 32, 33, 48, 64])
 def test_skinny_per_token_and_per_channel(hip, M):
     """Config C5 shapes through kh_linear_i8: per-token activations, per-output-
     channel weights with 0.5% outlier columns x20, K=4096, N=11008."""

@@ -86,7 +86,9 @@ def test_quantize_rows_vs_oracle(hip, rows, cols):
     np.testing.assert_array_equal(bits32(H.dequantize_rows(q, s).numpy()), bits32(O.ko_dequantize_rows(eq, es)))
 
 
-@pytest.mark.parametrize("n", [1, 3, 4, 5, 1023, 65536, 1_000_003, 16_777_216])
+# n <= 65536 (float4-aligned buffers) takes the one-launch kernel, larger n the
+# two-pass path.
+@pytest.mark.parametrize("n", [1, 3, 4, 5, 1023, 32768, 65535, 65536, 65537, 1_000_003, 16_777_216])
 def test_quantize_tensor_vs_oracle(hip, n):
     H, D = hip
     gen = np.random.Generator(np.random.PCG64(n))
