@@ -129,3 +129,31 @@ def test_capture_rules_and_recorded_errors(G):
     with pytest.raises(ValueError, match="does not match"):
         g(_ids(1, 8, 20, 1))
     g.close()
+
+
+def test_any_planned_graph_replays(G):
+    """kir.HipGraph on a graph other than the char-LM: the fused C1 Linear
+    (per-tensor quantize of x, int8 GEMM with dequantize and bias), replayed
+    on new inputs with eager work between the replays, equals run_hip bit for
+    bit each time."""
+    N, D = G
+    from kansaiml_amd import kir
+    from kansaiml_amd.quantize import QLinear
+
+    class _Lin:
+        def __init__(self, w, b):
+            self.weight, self.bias = w, b
+
+    gen = np.random.Generator(np.random.PCG64(21))
+    w = gen.standard_normal((512, 384), dtype=np.float32) * np.float32(0.02)
+    b = gen.standard_normal(384).astype(np.float32)
+    layer = QLinear(_Lin(w, b), mode="int8", act_granularity="tensor", weight_granularity="col")
+    x0 = gen.standard_normal((64, 512), dtype=np.float32)
+    g = kir.quant_fusion(kir.trace(layer, x0))
+    hg = kir.HipGraph(g, kir.plan_memory(g), x0)
+    for k in range(3):
+        x = gen.standard_normal((64, 512), dtype=np.float32) * np.float32(1 + k)
+        want = kir.run_hip(g, x)
+        N.synchronize()
+        np.testing.assert_array_equal(_bits(hg(x)), _bits(want))
+    hg.close()
