@@ -128,7 +128,9 @@ int kh_graph_destroy(void* graph);
 /* ---- quantize / dequantize -------------------------------------------- */
 
 /* quantize_symmetric (python/kansai/quantize.py:50-70) over a whole
- * tensor of n fp32 values: one scale, written to scale[0]. */
+ * tensor of n fp32 values: one scale, written to scale[0].  Up to 64 K
+ * elements (x 16-byte and q 4-byte aligned) in one launch, larger tensors in
+ * two passes (absmax partials, then the codes). */
 int kh_quantize_tensor(const float* x, int64_t n, int8_t* q, double* scale);
 
 /* The two passes of kh_quantize_tensor taken apart, so the absmax pass can
