@@ -277,6 +277,40 @@ def bench_c1(steps, warmup):
             "TOPS_kernels": round(ops / (us_kernels * 1e-6) / 1e12, 3), "bound": "latency"}
 
 
+def c4_gemm_breakdown(model, ids, ms_forward, steps):
+    """The C4 forward's int8 Linear layers one by one, on the activations
+    the model itself produces: one unplanned run keeps every node's device
+    value, then each int8_linear node is re-executed on its own inputs and
+    timed with HIP events.  Returns per-shape microseconds and TOPS and the
+    int8 GEMMs' share of the forward's time."""
+    from kansaiml_amd import kir
+    g, _ = model.graph(*ids.shape)
+    vals = {g.inputs[0]: ids}
+    out = kir.run_hip(g, ids, to_host=False, observe=lambda n, v: vals.__setitem__(n.id, v))
+    del out
+    M = ids.shape[0] * ids.shape[1]
+    shapes = {}
+    for node in g.nodes:
+        if node.op != "int8_linear":
+            continue
+        w = vals[node.inputs[1]]
+        N, K = int(node.shape[-1]), int(w.shape[0])
+        epi = "+".join(e for e, on in (("bias", node.attrs.get("bias")), (node.attrs.get("act") or "", node.attrs.get("act")),
+                                        ("residual", node.attrs.get("residual"))) if on) or "none"
+        us = time_kernel(lambda: kir._release(kir._exec(node, vals)), steps, 3) * 1e3
+        key = (N, K, epi)
+        shapes.setdefault(key, []).append(us)
+    rows, total = [], 0.0
+    for (N, K, epi), t in sorted(shapes.items(), key=lambda kv: -sum(kv[1])):
+        us = float(np.median(t))
+        total += us * len(t)
+        rows.append({"M": M, "N": N, "K": K, "epilogue": epi, "count": len(t), "us": round(us, 2),
+                     "TOPS": round(2.0 * M * N * K / (us * 1e-6) / 1e12, 1)})
+    vals.clear()
+    return {"gemms": rows, "int8_gemm_us_per_forward": round(total, 1),
+            "int8_gemm_fraction_of_forward": round(total / (ms_forward * 1e3), 3)}
+
+
 def bench_c4(steps, warmup):
     """Config C4: the int8 char-LM forward (vocab 65, d 384, 6 heads, 6 layers,
     FFN 1536, seq 256, batch 64; int8 per-channel weights ~N(0, 0.02),
@@ -294,12 +328,13 @@ def bench_c4(steps, warmup):
     g = model.capture(64, 256)
     ms = time_kernel(lambda: g(ids, to_host=False), steps, warmup)
     g.close()
+    breakdown = c4_gemm_breakdown(model, ids, ms, steps)
     ops = int8_linear_ops(w, 64, 256)
     return {"workload": "C4 int8 char-LM forward, batch 64 x seq 256 (16384 tokens), 6 layers, d 384",
             "ms_per_forward": round(ms, 4), "tokens_per_s": round(64 * 256 / (ms * 1e-3), 1),
             "ms_per_forward_eager": round(eager, 4),
             "int8_linear_ops": ops, "int8_linear_TOPS_over_forward": round(ops / (ms * 1e-3) / 1e12, 2),
-            "attention_fp32_flops_full_square": attention_flops(w, 64, 256)}
+            "attention_fp32_flops_full_square": attention_flops(w, 64, 256), **breakdown}
 
 
 COPY_BYTES = 1 << 30
