@@ -32,7 +32,8 @@
 namespace {
 
 // ---------------------------------------------------------------------------
-// Embedding: one thread per output element.
+// Embedding: one thread per output element (embedding_kernel), or per four
+// (embedding4_kernel: D % 4 == 0, 16-byte aligned tables and output).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void embedding_kernel(const int32_t* __restrict__ ids,
                                                         const float* __restrict__ tok, const float* __restrict__ pos,
@@ -49,6 +50,24 @@ __global__ __launch_bounds__(256) void embedding_kernel(const int32_t* __restric
         return;
     }
     out[e] = tok[(int64_t)id * D + c] + pos[(int64_t)(r % T) * D + c];
+}
+
+__global__ __launch_bounds__(256) void embedding4_kernel(const int32_t* __restrict__ ids,
+                                                         const float* __restrict__ tok, const float* __restrict__ pos,
+                                                         int rows, int T, int D4, int V, float* __restrict__ out,
+                                                         unsigned* __restrict__ fault) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= (int64_t)rows * D4) return;
+    const int r = (int)(e / D4), c = (int)(e - (int64_t)r * D4);
+    const int id = ids[r];
+    f4* o = reinterpret_cast<f4*>(out) + e;
+    if (id < 0 || id >= V) {
+        atomicOr(fault, kh::kFaultBadIndex);
+        *o = f4{0.f, 0.f, 0.f, 0.f};
+        return;
+    }
+    *o = reinterpret_cast<const f4*>(tok)[(int64_t)id * D4 + c] + reinterpret_cast<const f4*>(pos)[(int64_t)(r % T) * D4 + c];
 }
 
 // ---------------------------------------------------------------------------
@@ -470,6 +489,12 @@ int kh_embedding(const int32_t* ids, int64_t rows, int T, const float* tok, int 
     KH_REQUIRE(ids && tok && pos && out, "kh_embedding: null pointer");
     KH_DEVICE_OR_RETURN(d);
     const int64_t n = rows * D;
+    if (D % 4 == 0 && rows <= 0x7FFFFFFF && n / 4 <= 0xFFFFFFFFLL * 256 && kh::aligned(tok, 16) &&
+        kh::aligned(pos, 16) && kh::aligned(out, 16)) {
+        embedding4_kernel<<<(unsigned)((n / 4 + 255) / 256), 256, 0, d->stream>>>(ids, tok, pos, (int)rows, T, D / 4,
+                                                                                  V, out, d->fault);
+        return kh::launch_status("embedding");
+    }
     embedding_kernel<<<(unsigned)((n + 255) / 256), 256, 0, d->stream>>>(ids, tok, pos, rows, T, D, V, out, d->fault);
     return kh::launch_status("embedding");
 }

@@ -46,26 +46,26 @@ def test_gelu(G):
     assert np.abs(out.numpy() - ref).max() < 4e-6 * max(1.0, np.abs(ref).max())
 
 
-def test_embedding_exact_and_bad_id(G):
+@pytest.mark.parametrize("d", [48, 50])  # float4 path, scalar path
+def test_embedding_exact_and_bad_id(G, d):
     N, D = G
     gen = np.random.Generator(np.random.PCG64(3))
-    tok = gen.standard_normal((65, 48)).astype(np.float32)
-    pos = gen.standard_normal((20, 48)).astype(np.float32)
+    tok = gen.standard_normal((65, d)).astype(np.float32)
+    pos = gen.standard_normal((20, d)).astype(np.float32)
     ids = gen.integers(0, 65, (3, 20)).astype(np.int32)
-    out = D([60, 48])
+    out = D([60, d])
     idd, td, pd = D.from_host(ids), D.from_host(tok), D.from_host(pos)
-    N.call("kh_embedding", idd.ptr, 60, 20, td.ptr, 65, pd.ptr, 48, out.ptr)
+    N.call("kh_embedding", idd.ptr, 60, 20, td.ptr, 65, pd.ptr, d, out.ptr)
     ref = tok[ids.reshape(-1)] + np.tile(pos, (3, 1))
     np.testing.assert_array_equal(out.numpy().view(np.uint32), ref.astype(np.float32).view(np.uint32))
     ids[1, 4] = 65
     idd = D.from_host(ids)
-    N.call("kh_embedding", idd.ptr, 60, 20, td.ptr, 65, pd.ptr, 48, out.ptr)
+    N.call("kh_embedding", idd.ptr, 60, 20, td.ptr, 65, pd.ptr, d, out.ptr)
     with pytest.raises(RuntimeError):
         N.synchronize()
     N.synchronize()
 
 
-# batch * heads a multiple of 8 takes the kernel's XCD-grouped workgroup order.
 @pytest.mark.parametrize("batch,seq,heads", [(2, 1, 2), (2, 5, 3), (1, 64, 2), (2, 100, 2), (2, 256, 6), (4, 200, 2),
                                              (8, 130, 3)])
 def test_causal_attention(G, batch, seq, heads):
