@@ -13,6 +13,10 @@ Every Linear goes through the oracle's int8 path (per-tensor activation
 quantize, per-output-channel weight quantize, exact int32 GEMM, binary64
 epilogue) so the int8 arithmetic is the C restatement's; the fp32 parts are
 numpy float32.  `quantized=False` gives the plain fp32 model (x @ W + b).
+
+Pinned on the CPU by tests/test_charlm_oracle.py: the reference tests' known
+answers, closed forms, binary64 brute force of attention and of the whole
+forward, causality invariants and planted mutants.
 """
 
 from __future__ import annotations
