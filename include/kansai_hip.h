@@ -294,6 +294,11 @@ int kh_causal_attention(const float* qkv, int B, int T, int H, int dk, float* ou
 /* ... also writing absmax partials of out (see kh_absmax_parts). */
 int kh_causal_attention_ex(const float* qkv, int B, int T, int H, int dk, float* out, unsigned* absmax_parts,
                            int max_parts, int* nparts);
+/* The same with the mask chosen by the caller: causal = 1 as above, causal = 0
+ * attends over all T keys -- BigGPT.forward passes no mask when the sequence
+ * is shorter than its position table (train_shakespeare_large.py:86). */
+int kh_attention_ex(const float* qkv, int B, int T, int H, int dk, int causal, float* out, unsigned* absmax_parts,
+                    int max_parts, int* nparts);
 
 /* ---- measurement utility (no reference counterpart) ------------------- */
 

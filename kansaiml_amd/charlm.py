@@ -5,7 +5,9 @@ The architecture is the reference's BigGPT
 nn modules (python/kansai/nn.py): token + learned position embedding,
 N pre-LN TransformerBlocks (nn.py:430-478: x + attn(LN1 x), then
 x + fc2(GELU(fc1(LN2 x)))) under one causal mask, a final LayerNorm and the
-vocabulary head.  MultiHeadAttention (nn.py:334-427) has no projection bias;
+vocabulary head.  As in BigGPT.forward (:86), the mask applies when the
+sequence fills the position table (seq == block size); a shorter sequence
+attends over all of its keys.  MultiHeadAttention (nn.py:334-427) has no projection bias;
 the FFN Linears and the head do.
 
 Every Linear is int8 here: weights quantized once per output channel
@@ -168,7 +170,7 @@ class CharLM:
             x = ids.embedding(self.tok, self.pos)
             for p in self.blocks:
                 h = x.layer_norm(p["ln1_w"], p["ln1_b"])
-                a = linear(h, p["w_qkv"]).causal_attention(batch, seq, self.w.heads)
+                a = linear(h, p["w_qkv"]).attention(batch, seq, self.w.heads, causal=seq == self.w.seq)
                 x = x.add(linear(a, p["w_o"]))
                 h = x.layer_norm(p["ln2_w"], p["ln2_b"])
                 x = x.add(linear(linear(h, p["fc1"], p["fc1_b"]).gelu(), p["fc2"], p["fc2_b"]))

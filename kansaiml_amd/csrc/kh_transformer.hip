@@ -1,6 +1,6 @@
 // kh_transformer.hip -- the fp32 pieces of a decoder block around the int8
 // Linear layers (config C4): token + position embedding, LayerNorm, exact-erf
-// GELU, and causal multi-head attention.
+// GELU, and multi-head attention (causal or unmasked).
 //
 // Semantics follow the reference's modules (python/kansai/nn.py):
 //   Embedding      out[r] = tok[id[r]] + pos[r % T]        (nn.py:624-646, the
@@ -13,7 +13,9 @@
 //                  train_shakespeare_large.py:69-70); the softmax subtracts the
 //                  row max (Tensor.cpp:906-913).  exp(-1e9 - max) is exactly 0
 //                  in binary32, so masked keys are skipped; every row keeps
-//                  its diagonal key.
+//                  its diagonal key.  BigGPT adds the mask only when the
+//                  sequence fills its position table (:86); shorter
+//                  sequences attend over all T keys (causal = 0).
 // All fp32 (float accumulation order differs from the reference's CPU loops,
 // and LayerNorm multiplies by 1 / sqrt(var + eps) rather than dividing, so
 // results agree to rounding, not bit for bit).
@@ -274,7 +276,8 @@ __global__ __launch_bounds__(256) void gelu_kernel(const float* __restrict__ x, 
 }
 
 // ---------------------------------------------------------------------------
-// Causal attention, fp32, flash-style (online softmax) on fp32 MFMA.
+// Attention, fp32, flash-style (online softmax) on fp32 MFMA; CAUSAL masks
+// keys after the query, otherwise only keys past T are left out.
 //
 // qkv: [B*T, 3*D] row-major, the fused Q|K|V projection output (head h of Q
 // at columns h*dk .. h*dk+dk-1, K at D + h*dk, V at 2D + h*dk).  out: [B*T, D],
@@ -338,6 +341,7 @@ __device__ __forceinline__ void attention_tile_dma(__amdgpu_buffer_rsrc_t r, flo
                             voff + 16 * i * row_bytes, 0);
 }
 
+template <bool CAUSAL>
 __global__ __launch_bounds__(256) void attention_mfma_kernel(const float* __restrict__ qkv, int B, int T, int H,
                                                              float* __restrict__ out, unsigned* __restrict__ parts) {
     __shared__ __attribute__((aligned(1024))) float ks[kAttK * kDk];
@@ -381,7 +385,8 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(const float* __rest
     for (int j = 0; j < 4; ++j) o[j] = f32x4v{0.f, 0.f, 0.f, 0.f};
     float m = -3.0e38f, l = 0.0f;
 
-    const int tiles = (min(T, (qb + 1) * kAttQ) - 1) / kAttK + 1;  // through the workgroup's last query
+    // Causal: key tiles through the workgroup's last query; otherwise all of them.
+    const int tiles = ((CAUSAL ? min(T, (qb + 1) * kAttQ) : T) - 1) / kAttK + 1;
     for (int it = 0; it < tiles; ++it) {
         const int k0 = it * kAttK;
         // K(it) has landed for every wave, and every wave is done with V(it-1).
@@ -407,13 +412,13 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(const float* __rest
         }
         // Causal mask (key > query) and keys past T -- only where the tile
         // reaches this wave's diagonal or the sequence end.
-        if (!(k0 + kAttK - 1 <= q0 && k0 + kAttK <= T)) {
+        if (!((!CAUSAL || k0 + kAttK - 1 <= q0) && k0 + kAttK <= T)) {
 #pragma unroll
             for (int t = 0; t < 4; ++t)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int key = k0 + 16 * t + 4 * g + r;
-                    st[t][r] = (key > q || key >= T) ? -3.0e38f : st[t][r];
+                    st[t][r] = ((CAUSAL && key > q) || key >= T) ? -3.0e38f : st[t][r];
                 }
         }
         float mx = -3.0e38f;
@@ -584,27 +589,33 @@ int kh_gelu(const float* x, float* out, int64_t n) {
     return kh::launch_status("gelu");
 }
 
-int kh_causal_attention_ex(const float* qkv, int B, int T, int H, int dk, float* out, unsigned* absmax_parts,
-                           int max_parts, int* nparts) {
-    KH_REQUIRE(B > 0 && T > 0 && H > 0, "kh_causal_attention: bad shape");
-    KH_REQUIRE(dk == kDk, "kh_causal_attention: only head dimension 64 is supported");
-    KH_REQUIRE(qkv && out, "kh_causal_attention: null pointer");
-    KH_REQUIRE(!absmax_parts || (max_parts > 0 && nparts), "kh_causal_attention_ex: partials need max_parts and nparts");
+int kh_attention_ex(const float* qkv, int B, int T, int H, int dk, int causal, float* out, unsigned* absmax_parts,
+                    int max_parts, int* nparts) {
+    KH_REQUIRE(B > 0 && T > 0 && H > 0, "kh_attention: bad shape");
+    KH_REQUIRE(dk == kDk, "kh_attention: only head dimension 64 is supported");
+    KH_REQUIRE(causal == 0 || causal == 1, "kh_attention: causal must be 0 or 1");
+    KH_REQUIRE(qkv && out, "kh_attention: null pointer");
+    KH_REQUIRE(!absmax_parts || (max_parts > 0 && nparts), "kh_attention_ex: partials need max_parts and nparts");
     if (nparts) *nparts = 0;
     KH_DEVICE_OR_RETURN(d);
-    KH_REQUIRE(kh::aligned(qkv, 16) && kh::aligned(out, 16), "kh_causal_attention: 16-byte aligned buffers required");
+    KH_REQUIRE(kh::aligned(qkv, 16) && kh::aligned(out, 16), "kh_attention: 16-byte aligned buffers required");
     // Key offsets within a batch's rows, up to the last tile's padding, are
     // 32-bit buffer offsets.
     const int64_t nq = (T + kAttQ - 1) / kAttQ;
     KH_REQUIRE((nq * kAttQ) * 3 * (int64_t)H * kDk * 4 <= 0x7FFFFFFFLL,
-               "kh_causal_attention: one batch's qkv rows must stay under 2 GiB");
+               "kh_attention: one batch's qkv rows must stay under 2 GiB");
     const int64_t blocks = nq * H * B;
-    KH_REQUIRE(blocks <= 0x7FFFFFFFLL, "kh_causal_attention: too many query blocks");
+    KH_REQUIRE(blocks <= 0x7FFFFFFFLL, "kh_attention: too many query blocks");
     const bool fused = absmax_parts && blocks <= max_parts;
     // 1/sqrt(d_k) = 1/8 for dk = 64 (the reference's binary64 Python float,
     // nn.py:413, is exactly representable in binary32); the kernel applies it
     // to Q.
-    attention_mfma_kernel<<<(unsigned)blocks, 256, 0, d->stream>>>(qkv, B, T, H, out, fused ? absmax_parts : nullptr);
+    if (causal)
+        attention_mfma_kernel<true><<<(unsigned)blocks, 256, 0, d->stream>>>(qkv, B, T, H, out,
+                                                                          fused ? absmax_parts : nullptr);
+    else
+        attention_mfma_kernel<false><<<(unsigned)blocks, 256, 0, d->stream>>>(qkv, B, T, H, out,
+                                                                           fused ? absmax_parts : nullptr);
     int rc = kh::launch_status("attention");
     if (rc || !absmax_parts) return rc;
     if (fused) {
@@ -614,8 +625,13 @@ int kh_causal_attention_ex(const float* qkv, int B, int T, int H, int dk, float*
     return kh_absmax_parts(out, (int64_t)B * T * H * kDk, absmax_parts, max_parts, nparts);
 }
 
+int kh_causal_attention_ex(const float* qkv, int B, int T, int H, int dk, float* out, unsigned* absmax_parts,
+                           int max_parts, int* nparts) {
+    return kh_attention_ex(qkv, B, T, H, dk, 1, out, absmax_parts, max_parts, nparts);
+}
+
 int kh_causal_attention(const float* qkv, int B, int T, int H, int dk, float* out) {
-    return kh_causal_attention_ex(qkv, B, T, H, dk, out, nullptr, 0, nullptr);
+    return kh_attention_ex(qkv, B, T, H, dk, 1, out, nullptr, 0, nullptr);
 }
 
 }  // extern "C"

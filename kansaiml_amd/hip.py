@@ -331,14 +331,21 @@ def layer_norm(x: DeviceTensor, w: DeviceTensor, b: DeviceTensor, eps: float = 1
     return out, parts
 
 
-def causal_attention(qkv: DeviceTensor, batch: int, seq: int, heads: int, d_model: int, *, absmax: bool = False):
-    """Causal multi-head attention core (nn.py:381-427).  Returns (out, AbsmaxParts | None)."""
-    _need(qkv, "float32", 2, "causal_attention(qkv)")
+def attention(qkv: DeviceTensor, batch: int, seq: int, heads: int, d_model: int, *, causal: bool = True,
+              absmax: bool = False):
+    """Multi-head attention core (nn.py:381-427), with the causal mask or none.
+    Returns (out, AbsmaxParts | None)."""
+    _need(qkv, "float32", 2, "attention(qkv)")
     out = DeviceTensor([batch * seq, d_model], "float32")
     parts = AbsmaxParts() if absmax else None
-    N.call("kh_causal_attention_ex", qkv.ptr, batch, seq, heads, d_model // heads, out.ptr,
+    N.call("kh_attention_ex", qkv.ptr, batch, seq, heads, d_model // heads, int(bool(causal)), out.ptr,
            parts.buf.ptr if parts else None, ABSMAX_PARTS if parts else 0, ctypes.byref(parts._n) if parts else None)
     return out, parts
+
+
+def causal_attention(qkv: DeviceTensor, batch: int, seq: int, heads: int, d_model: int, *, absmax: bool = False):
+    """attention() under the causal mask."""
+    return attention(qkv, batch, seq, heads, d_model, causal=True, absmax=absmax)
 
 
 def quantize_tensor_parts(x: DeviceTensor, parts: AbsmaxParts):

@@ -26,7 +26,7 @@ at trace time, kir.py:129-136):
 
 and, for a decoder block (config C4), fused forms of what the reference
 composes from generic ops (nn.py:308-478): embedding (token + position
-lookup on int32 ids), layer_norm, gelu, causal_attention (the per-head
+lookup on int32 ids), layer_norm, gelu, attention (the per-head
 softmax(Q K^T / sqrt(d_k) + causal mask) V core of MultiHeadAttention on a
 fused Q|K|V projection, heads merged in place).
 """
@@ -178,12 +178,17 @@ class TraceValue:
     def gelu(self):
         return self._emit("gelu", [self], self.shape)
 
-    def causal_attention(self, batch: int, seq: int, heads: int):
-        """self: fused Q|K|V projection [batch*seq, 3*D] -> [batch*seq, D]."""
+    def attention(self, batch: int, seq: int, heads: int, causal: bool = True):
+        """self: fused Q|K|V projection [batch*seq, 3*D] -> [batch*seq, D];
+        causal adds the mask that hides later keys, otherwise every query
+        attends over all seq keys of its sequence."""
         if len(self.shape) != 2 or self.shape[0] != batch * seq or self.shape[1] % (3 * heads):
-            raise ValueError(f"causal_attention: {self.shape} is not [batch*seq, 3*D] for {heads} heads")
-        return self._emit("causal_attention", [self], [self.shape[0], self.shape[1] // 3], batch=batch, seq=seq,
-                          heads=heads)
+            raise ValueError(f"attention: {self.shape} is not [batch*seq, 3*D] for {heads} heads")
+        return self._emit("attention", [self], [self.shape[0], self.shape[1] // 3], batch=batch, seq=seq,
+                          heads=heads, causal=bool(causal))
+
+    def causal_attention(self, batch: int, seq: int, heads: int):
+        return self.attention(batch, seq, heads, causal=True)
 
 
 def _example_dtype(x) -> str:
@@ -243,7 +248,7 @@ def quant_fusion(graph, producer_quant: bool | str = False) -> Graph:
     LayerNorm (two passes over its input cost less than writing the fp32
     values and reading them back) but not for the GEMM, whose VALU-bound
     epilogue (binary64 dequantize, exact-erf GELU) the second pass repeats.
-    Then every int8_linear, layer_norm or causal_attention whose
+    Then every int8_linear, layer_norm or attention whose
     output feeds a per-tensor quantize is marked absmax=True: its kernel
     writes the absmax partials that quantize needs, so the quantize reads
     its input once.
@@ -354,7 +359,7 @@ def quant_fusion(graph, producer_quant: bool | str = False) -> Graph:
     return out
 
 
-_ABSMAX_PRODUCERS = ("int8_linear", "layer_norm", "causal_attention")
+_ABSMAX_PRODUCERS = ("int8_linear", "layer_norm", "attention")
 
 
 # ---------------------------------------------------------------------------
@@ -541,9 +546,9 @@ def _exec(node, vals):
         out = DeviceTensor(ins[0].shape, "float32")
         N.call("kh_gelu", ins[0].ptr, out.ptr, ins[0].numel())
         return out
-    if op == "causal_attention":
-        out, parts = H.causal_attention(ins[0], node.attrs["batch"], node.attrs["seq"], node.attrs["heads"],
-                                        node.shape[1], absmax=bool(node.attrs.get("absmax")))
+    if op == "attention":
+        out, parts = H.attention(ins[0], node.attrs["batch"], node.attrs["seq"], node.attrs["heads"], node.shape[1],
+                                 causal=node.attrs["causal"], absmax=bool(node.attrs.get("absmax")))
         return _with_parts(out, parts)
     if op == "tuple":
         return tuple(ins)

@@ -6,7 +6,8 @@ LayerNorm (308-331: biased variance, eps 1e-5, centered / sqrt(var + eps) *
 w + b), MultiHeadAttention (381-427: no projection bias, scores * 1/sqrt(d_k)
 + additive causal mask of -1e9 above the diagonal, softmax by max-subtract
 (core/src/Tensor.cpp:906-913), merged heads @ w_o), TransformerBlock
-(466-478: pre-LN, two residual adds), exact-erf GELU
+(466-478: pre-LN, two residual adds; BigGPT passes the mask only when the
+sequence fills the position table, :86), exact-erf GELU
 (backend/cpu/src/Ops.cpp:250-256).
 
 Every Linear goes through the oracle's int8 path (per-tensor activation
@@ -42,7 +43,7 @@ def gelu(x):
     return (x * (f32(0.5) * (f32(1.0) + erf(x * f32(0.70710678118654752440)).astype(f32)))).astype(f32)
 
 
-def causal_attention(qkv, batch, seq, heads):
+def attention(qkv, batch, seq, heads, causal=True):
     D = qkv.shape[1] // 3
     dk = D // heads
     q = qkv[:, :D].reshape(batch, seq, heads, dk).transpose(0, 2, 1, 3)
@@ -50,13 +51,18 @@ def causal_attention(qkv, batch, seq, heads):
     v = qkv[:, 2 * D:].reshape(batch, seq, heads, dk).transpose(0, 2, 1, 3)
     scale = f32(1.0 / math.sqrt(dk))
     s = (q @ k.transpose(0, 1, 3, 2)).astype(f32) * scale
-    mask = np.where(np.arange(seq)[None, :] <= np.arange(seq)[:, None], f32(0.0), f32(-1e9))
-    s = (s + mask).astype(f32)
+    if causal:
+        mask = np.where(np.arange(seq)[None, :] <= np.arange(seq)[:, None], f32(0.0), f32(-1e9))
+        s = (s + mask).astype(f32)
     s = s - s.max(axis=-1, keepdims=True)
     e = np.exp(s).astype(f32)
     p = (e / e.sum(axis=-1, keepdims=True, dtype=f32)).astype(f32)
     o = (p @ v).astype(f32)
     return o.transpose(0, 2, 1, 3).reshape(batch * seq, D)
+
+
+def causal_attention(qkv, batch, seq, heads):
+    return attention(qkv, batch, seq, heads, causal=True)
 
 
 def linear(x, w, b=None, quantized=True):
@@ -77,7 +83,9 @@ def forward(w, ids, quantized=True):
     for p in w.blocks:
         h = layer_norm(x, p["ln1_w"], p["ln1_b"])
         qkv = linear(h, np.concatenate([p["w_q"], p["w_k"], p["w_v"]], axis=1), None, quantized)
-        a = causal_attention(qkv, batch, seq, w.heads)
+        # BigGPT adds its causal mask only at seq == BLOCK_SIZE
+        # (train_shakespeare_large.py:86)
+        a = attention(qkv, batch, seq, w.heads, causal=seq == w.seq)
         x = (x + linear(a, p["w_o"], None, quantized)).astype(f32)
         h = layer_norm(x, p["ln2_w"], p["ln2_b"])
         f = gelu(linear(h, p["fc1_w"], p["fc1_b"], quantized))

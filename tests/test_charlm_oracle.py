@@ -60,10 +60,11 @@ def _gelu64(x):
     return np.vectorize(lambda v: v * 0.5 * (1.0 + math.erf(v / math.sqrt(2.0))))(np.asarray(x, f64))
 
 
-def _attn64(q, k, v, batch, seq, heads):
+def _attn64(q, k, v, batch, seq, heads, causal=True):
     """softmax(q k^T / sqrt(dk) + causal mask) v, one (batch, head, query) at a
     time; head h owns columns h*dk .. h*dk+dk-1 (a row-major reshape of
-    d_model into (heads, dk), nn.py:393-402)."""
+    d_model into (heads, dk), nn.py:393-402).  Unmasked: every query sees all
+    seq keys."""
     D = q.shape[1]
     dk = D // heads
     out = np.zeros((batch * seq, D), f64)
@@ -72,24 +73,28 @@ def _attn64(q, k, v, batch, seq, heads):
             cols = slice(h * dk, (h + 1) * dk)
             for i in range(seq):
                 qi = q[b * seq + i, cols].astype(f64)
-                s = [float(qi @ k[b * seq + j, cols].astype(f64)) / math.sqrt(dk) for j in range(i + 1)]
+                keys = i + 1 if causal else seq
+                s = [float(qi @ k[b * seq + j, cols].astype(f64)) / math.sqrt(dk) for j in range(keys)]
                 m = max(s)
                 e = [math.exp(t - m) for t in s]
                 tot = sum(e)
-                for j in range(i + 1):
+                for j in range(keys):
                     out[b * seq + i, cols] += (e[j] / tot) * v[b * seq + j, cols].astype(f64)
     return out
 
 
 def _forward64(w, ids):
     """BigGPT's forward in binary64: token + position embedding, pre-LN
-    blocks (x + attn(LN1 x); x + fc2(GELU(fc1(LN2 x)))), final LN, head."""
+    blocks (x + attn(LN1 x); x + fc2(GELU(fc1(LN2 x)))), final LN, head;
+    the causal mask only when seq fills the position table
+    (train_shakespeare_large.py:86)."""
     batch, seq = ids.shape
+    causal = seq == w.seq
     x = np.stack([w.tok[ids[b, t]].astype(f64) + w.pos[t].astype(f64) for b in range(batch) for t in range(seq)])
     for p in w.blocks:
         h = _ln64(x, p["ln1_w"], p["ln1_b"])
         q, k, v = (h @ p[n].astype(f64) for n in ("w_q", "w_k", "w_v"))
-        x = x + _attn64(q, k, v, batch, seq, w.heads) @ p["w_o"].astype(f64)
+        x = x + _attn64(q, k, v, batch, seq, w.heads, causal) @ p["w_o"].astype(f64)
         h = _ln64(x, p["ln2_w"], p["ln2_b"])
         f = _gelu64(h @ p["fc1_w"].astype(f64) + p["fc1_b"].astype(f64))
         x = x + f @ p["fc2_w"].astype(f64) + p["fc2_b"].astype(f64)
@@ -227,6 +232,24 @@ def test_attention_vs_binary64_loops(batch, seq, heads, dk):
     np.testing.assert_allclose(got, want, rtol=0, atol=2e-6)
 
 
+@pytest.mark.parametrize("batch,seq,heads,dk", [(1, 1, 1, 4), (2, 7, 3, 4), (1, 33, 2, 16)])
+def test_unmasked_attention_vs_binary64_loops(batch, seq, heads, dk):
+    qkv = _qkv(batch, seq, heads, dk, seed=seq * 37 + heads)
+    D = heads * dk
+    got = R.attention(qkv, batch, seq, heads, causal=False)
+    want = _attn64(qkv[:, :D], qkv[:, D:2 * D], qkv[:, 2 * D:], batch, seq, heads, causal=False)
+    np.testing.assert_allclose(got, want, rtol=0, atol=2e-6)
+    # zero queries: every position gets the mean of all its sequence's values
+    z = qkv.copy()
+    z[:, :D] = 0
+    v = z[:, 2 * D:].astype(f64).reshape(batch, seq, D)
+    mean = np.broadcast_to(v.mean(axis=1, keepdims=True), v.shape).reshape(batch * seq, D)
+    np.testing.assert_allclose(R.attention(z, batch, seq, heads, causal=False), mean, rtol=0, atol=1e-6)
+    # and the unmasked form is not the causal one
+    if seq > 1:
+        assert not np.allclose(got, R.causal_attention(qkv, batch, seq, heads), rtol=0, atol=2e-6)
+
+
 def test_attention_closed_forms():
     batch, seq, heads, dk = 2, 9, 3, 8
     D = heads * dk
@@ -322,9 +345,11 @@ def _tiny_weights(seed):
     return w
 
 
-def test_fp32_forward_vs_binary64_composition():
+@pytest.mark.parametrize("seq", [6, 4])
+def test_fp32_forward_vs_binary64_composition(seq):
+    """seq 6 fills the position table (causal mask); seq 4 runs unmasked."""
     w = _tiny_weights(3)
-    ids = _gen(4).integers(0, 11, (2, 6))
+    ids = _gen(4).integers(0, 11, (2, seq))
     got = R.forward(w, ids, quantized=False).astype(f64)
     want = _forward64(w, ids)
     assert np.max(np.abs(got - want)) <= 2e-5 * (1.0 + np.max(np.abs(want)))
@@ -338,7 +363,7 @@ def test_forward_mutants_are_caught(mutant, monkeypatch):
         monkeypatch.setattr(R, "gelu", lambda x: (0.5 * x * (1 + np.tanh(math.sqrt(2 / math.pi) *
                                                                           (x + 0.044715 * x ** 3)))).astype(f32))
     elif mutant == "attention_scale_dk":
-        monkeypatch.setattr(R, "causal_attention", lambda qkv, b, s, h: _attn_mutant(qkv, b, s, h, "scale_dk"))
+        monkeypatch.setattr(R, "attention", lambda qkv, b, s, h, causal=True: _attn_mutant(qkv, b, s, h, "scale_dk"))
     elif mutant == "ln_affine_dropped":
         ln = R.layer_norm
         monkeypatch.setattr(R, "layer_norm", lambda x, a, b: ln(x, np.ones_like(a), np.zeros_like(b)))

@@ -68,15 +68,19 @@ def test_embedding_exact_and_bad_id(G, d):
 
 @pytest.mark.parametrize("batch,seq,heads", [(2, 1, 2), (2, 5, 3), (1, 64, 2), (2, 100, 2), (2, 256, 6), (4, 200, 2),
                                              (8, 130, 3)])
-def test_causal_attention(G, batch, seq, heads):
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention(G, batch, seq, heads, causal):
     N, D = G
     gen = np.random.Generator(np.random.PCG64(batch * 1000 + seq * 10 + heads))
     dm = heads * 64
     qkv = (gen.standard_normal((batch * seq, 3 * dm)) * 1.5).astype(np.float32)
     out = D([batch * seq, dm])
     qd = D.from_host(qkv)
-    N.call("kh_causal_attention", qd.ptr, batch, seq, heads, 64, out.ptr)
-    ref = R.causal_attention(qkv.astype(np.float64), batch, seq, heads)
+    if causal:
+        N.call("kh_causal_attention", qd.ptr, batch, seq, heads, 64, out.ptr)
+    else:
+        N.call("kh_attention_ex", qd.ptr, batch, seq, heads, 64, 0, out.ptr, None, 0, None)
+    ref = R.attention(qkv.astype(np.float64), batch, seq, heads, causal=causal)
     assert np.abs(out.numpy() - ref).max() < 2e-5
 
 
@@ -164,15 +168,16 @@ def _check_node(node, got, ins):
         x = ins[0].astype(np.float64)
         ref = x * 0.5 * (1 + erf(x / np.sqrt(2)))
         assert np.abs(got - ref).max() < 4e-6 * max(1.0, np.abs(ref).max())
-    elif op == "causal_attention":
-        ref = R.causal_attention(ins[0].astype(np.float64), node.attrs["batch"], node.attrs["seq"],
-                                 node.attrs["heads"])
+    elif op == "attention":
+        ref = R.attention(ins[0].astype(np.float64), node.attrs["batch"], node.attrs["seq"], node.attrs["heads"],
+                          causal=node.attrs["causal"])
         assert np.abs(got - ref).max() < 2e-5
     else:
         raise AssertionError(f"unchecked node kind {op}")
 
 
-@pytest.mark.parametrize("seq,producer_quant", [(64, False), (100, False), (100, True), (100, "layer_norm")])
+@pytest.mark.parametrize("seq,producer_quant", [(64, False), (100, False), (128, False), (100, True), (128, True),
+                                                (128, "layer_norm")])
 def test_small_model_matches_restatement(G, seq, producer_quant):
     """Two layers of the C4 architecture (d 384, 6 heads, FFN 1536, vocab 65)
     with nonzero biases, checked node by node: every node's GPU output
@@ -183,7 +188,9 @@ def test_small_model_matches_restatement(G, seq, producer_quant):
     the attention output (below any fp32 kernel's rounding bound) re-rounds
     enough codes downstream to move logits by 2.5e-2 at seq 100.  So the
     whole-model comparison is against the fp32 model, at the quantization
-    error's scale, and exactness is asserted per node."""
+    error's scale, and exactness is asserted per node.  The position table
+    holds 128 rows: seq 128 runs under the causal mask, shorter sequences
+    without it (BigGPT.forward, train_shakespeare_large.py:86)."""
     from kansaiml_amd.charlm import CharLM, CharLMWeights
     w = CharLMWeights(layers=2, seq=128, seed=1, bias_std=0.02)
     ids = np.random.Generator(np.random.PCG64(2)).integers(0, 65, (2, seq)).astype(np.int32)
@@ -192,6 +199,7 @@ def test_small_model_matches_restatement(G, seq, producer_quant):
     y = model(ids, observe=lambda node, v: seen.__setitem__(node.id, (node, _host(v))))
     assert y.shape == (2 * seq, 65)
     g, _ = model.graph(2, seq)
+    assert {n.attrs["causal"] for n in g.nodes if n.op == "attention"} == {seq == 128}
     by_id = {n.id: n for n in g.nodes}
     checked = set()
     for nid, (node, got) in seen.items():
@@ -208,21 +216,21 @@ def test_small_model_matches_restatement(G, seq, producer_quant):
     acts = {(n.op, n.attrs.get("act"), bool(n.attrs.get("residual"))) for n in g.nodes
             if n.op in ("int8_linear", "int8_linear_quant")}
     if producer_quant == "layer_norm":
-        assert checked == {"embedding", "layer_norm_quant", "quantize", "int8_linear", "causal_attention"}
+        assert checked == {"embedding", "layer_norm_quant", "quantize", "int8_linear", "attention"}
         assert acts == {("int8_linear", None, False), ("int8_linear", "gelu", False), ("int8_linear", None, True)}
         assert all(n.attrs.get("absmax") for n in g.nodes
-                   if n.op == "causal_attention" or (n.op == "int8_linear" and n.attrs.get("act")))
+                   if n.op == "attention" or (n.op == "int8_linear" and n.attrs.get("act")))
     elif producer_quant:
         assert checked == {"embedding", "layer_norm_quant", "quantize", "int8_linear", "int8_linear_quant",
-                           "causal_attention"}
+                           "attention"}
         assert acts == {("int8_linear", None, False), ("int8_linear_quant", "gelu", False),
                         ("int8_linear", None, True)}
-        assert all(n.attrs.get("absmax") for n in g.nodes if n.op == "causal_attention")
+        assert all(n.attrs.get("absmax") for n in g.nodes if n.op == "attention")
     else:
-        assert checked == {"embedding", "layer_norm", "quantize", "int8_linear", "causal_attention"}
+        assert checked == {"embedding", "layer_norm", "quantize", "int8_linear", "attention"}
         assert acts == {("int8_linear", None, False), ("int8_linear", "gelu", False), ("int8_linear", None, True)}
         assert all(n.attrs.get("absmax") for n in g.nodes
-                   if n.op in ("layer_norm", "causal_attention") or (n.op == "int8_linear" and n.attrs.get("act")))
+                   if n.op in ("layer_norm", "attention") or (n.op == "int8_linear" and n.attrs.get("act")))
     np.testing.assert_array_equal(seen[g.output][1].view(np.uint32), y.view(np.uint32))
     # and the int8 model stays near the fp32 one (quantization error)
     fp = R.forward(w, ids, quantized=False)

@@ -46,6 +46,7 @@ def test_invalid_arguments_are_reported(G):
         (("kh_layernorm", x.ptr, 4, 2048, w.ptr, w.ptr, 1e-5, out.ptr), "longer than 1024"),
         (("kh_causal_attention", x.ptr, 1, 8, 2, 32, out.ptr), "head dimension 64"),
         (("kh_causal_attention", x.ptr, 0, 8, 2, 64, out.ptr), "bad shape"),
+        (("kh_attention_ex", x.ptr, 1, 8, 2, 64, 2, out.ptr, None, 0, None), "causal must be 0 or 1"),
         (("kh_linear_i8", x.ptr, 1, 512, b.ptr, 512, sb.ptr, 1, None, q.ptr, sa.ptr, None), "null out"),
         (("kh_graph_launch", None), "null graph"),
         (("kh_graph_capture_end", ctypes.byref(ctypes.c_void_p())), "no capture"),
