@@ -68,6 +68,18 @@ class DeviceTensor:
             N.call("kh_memcpy_h2d", t.ptr, ctypes.c_void_p(a.ctypes.data), t.nbytes)
         return t
 
+    @classmethod
+    def from_flat(cls, values, shape) -> "DeviceTensor":
+        """A float32 tensor of `shape` from a flat sequence of numbers, as the
+        reference's kansai.from_flat (core/src/Tensor.cpp:94-100): each value
+        rounded to binary32, and RuntimeError when the length does not match
+        the shape (checked before anything is allocated)."""
+        shape = [int(s) for s in shape]
+        flat = np.asarray(values, dtype=np.float64).reshape(-1)
+        if any(s < 0 for s in shape) or flat.size != math.prod(shape):
+            raise RuntimeError("from_flat: data length does not match shape")
+        return cls.from_host(flat.astype(np.float32).reshape(shape))
+
     # -- access -------------------------------------------------------------
     def numel(self) -> int:
         return math.prod(self.shape)

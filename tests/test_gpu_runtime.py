@@ -98,3 +98,19 @@ def test_stream_read_probe_runs_and_checks_arguments():
         N.call("kh_probe_stream_read", buf.ptr, 7)
     with pytest.raises(RuntimeError):
         N.call("kh_probe_stream_read", None, 4096)
+
+
+def test_from_flat_and_tolist(rt):
+    """kansai.from_flat / Tensor.tolist (core/src/Tensor.cpp:94-100, 133-137;
+    python/bindings.cpp:44, 133-134): values rounded to binary32 on the way
+    in, widened exactly on the way out, shape kept, empty tensors allowed."""
+    N, D = rt
+    vals = [0.1, -2.5, 1e-40, 3.4e38, 1.0 / 3.0, -0.0, 7.0]
+    t = D.from_flat(vals, [7])
+    assert t.shape == [7] and t.dtype == "float32"
+    got = t.tolist()
+    assert got == [float(np.float32(v)) for v in vals]
+    assert all(type(v) is float for v in got)
+    m = D.from_flat(range(6), (2, 3))
+    assert m.shape == [2, 3] and m.tolist() == [0.0, 1.0, 2.0, 3.0, 4.0, 5.0]
+    assert D.from_flat([], [0, 4]).tolist() == []

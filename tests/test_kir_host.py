@@ -153,3 +153,13 @@ def test_quantize_producers_fuse_into_quant_nodes():
     ops3 = [n.op for n in kir.quant_fusion(kir.trace(per_row, np.zeros((4, 16), np.float32)),
                                            producer_quant=True).nodes]
     assert "layer_norm" in ops3 and "layer_norm_quant" not in ops3
+
+
+@pytest.mark.parametrize("values,shape", [([1.0, 2.0, 3.0], [2, 2]), ([], [1]), ([1.0], [-1]), ([1.0, 2.0], [1])])
+def test_from_flat_length_mismatch_raises(values, shape):
+    """kansai.from_flat throws runtime_error("from_flat: data length does not
+    match shape") (core/src/Tensor.cpp:96-97); the check runs before any
+    device allocation, so it needs no GPU."""
+    from kansaiml_amd.device import DeviceTensor
+    with pytest.raises(RuntimeError, match="data length does not match shape"):
+        DeviceTensor.from_flat(values, shape)
