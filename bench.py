@@ -17,7 +17,7 @@ CPU baseline: the reference's own compiled backend/cpu/src/Ops.cpp matmul
 dequantizing the weight (python/kansai/quantize.py:115-122) -- on one core,
 over a time-bounded slab of rows of the same workload.
 
-    python bench.py [--gpus 1] [--steps 50] [--warmup 50] [--no-cpu] [--only gemm,probe,quant,f32,c1,skinny,c4,copy]
+    python bench.py [--gpus 1] [--steps 50] [--warmup 50] [--no-cpu] [--only gemm,probe,quant,f32,c1,skinny,c4,copy,pcie]
 
 Profiling (the summaries under profiles/ are made this way):
     rocprofv3 --kernel-trace --stats -d OUT/trace -o run --output-format csv -- python3 bench.py --no-cpu
@@ -277,6 +277,56 @@ def bench_c1(steps, warmup):
             "TOPS_kernels": round(ops / (us_kernels * 1e-6) / 1e12, 3), "bound": "latency"}
 
 
+def bench_host_buffers(reps=3):
+    """C2 and C3a handed over as host (pageable numpy) buffers: upload, the
+    kernel and the download, each between host synchronisations, best of
+    `reps`.  Reported beside `value`, never as it: the PCIe-inclusive rate
+    a caller holding host arrays sees."""
+    from kansaiml_amd import _native as Nn
+    from kansaiml_amd import hip as H
+    from kansaiml_amd.device import DeviceTensor as D
+
+    def timed(fn):
+        Nn.synchronize()
+        t0 = time.perf_counter()
+        r = fn()
+        Nn.synchronize()
+        return time.perf_counter() - t0, r
+
+    gen = np.random.Generator(np.random.PCG64(0))
+    R = 16384
+    x = gen.standard_normal((R, R), dtype=np.float32)
+    runs = []
+    for _ in range(reps):
+        tu, xd = timed(lambda: D.from_host(x))
+        tk, (q, s) = timed(lambda: H.quantize_rows(xd))
+        td, _ = timed(lambda: (q.numpy(), s.numpy()))
+        runs.append((tu, tk, td))
+        del xd, q, s
+    del x
+    tu, tk, td = min(runs, key=sum)
+    c2 = {"workload": "C2 per-row quantize, fp32 [16384,16384] in, int8 codes + fp64 scales out",
+          "upload_ms": round(tu * 1e3, 2), "kernel_ms": round(tk * 1e3, 3), "download_ms": round(td * 1e3, 2),
+          "GB/s_pcie_inclusive": round(5.0 * R * R / (tu + tk + td) / 1e9, 2),
+          "h2d_GB/s": round(4.0 * R * R / tu / 1e9, 2), "d2h_GB/s": round((R * R + 8 * R) / td / 1e9, 2)}
+    M = 8192
+    a = gen.integers(-127, 128, (M, M), dtype=np.int8)
+    b = gen.integers(-127, 128, (M, M), dtype=np.int8)
+    sa, sb = np.array([0.01], np.float64), np.full(M, 0.02, np.float64)
+    runs = []
+    for _ in range(reps):
+        tu, ops = timed(lambda: (D.from_host(a), D.from_host(b), D.from_host(sa), D.from_host(sb)))
+        tk, (out, _) = timed(lambda: H.gemm_i8(*ops))
+        td, _ = timed(lambda: out.numpy())
+        runs.append((tu, tk, td))
+        del ops, out
+    tu, tk, td = min(runs, key=sum)
+    c3a = {"workload": "C3a int8 GEMM 8192^3, int8 operands in, fp32 [8192,8192] out",
+           "upload_ms": round(tu * 1e3, 2), "kernel_ms": round(tk * 1e3, 3), "download_ms": round(td * 1e3, 2),
+           "TOPS_pcie_inclusive": round(2.0 * M ** 3 / (tu + tk + td) / 1e12, 2)}
+    return {"note": "pageable host buffers; timed on the host around synchronised calls", "c2": c2, "c3a": c3a}
+
+
 def c4_gemm_breakdown(model, ids, ms_forward, steps):
     """The C4 forward's int8 Linear layers one by one, on the activations
     the model itself produces: one unplanned run keeps every node's device
@@ -504,7 +554,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="gemm,probe,quant,f32,c1,skinny,c4",
-                    help="comma list of gemm,probe,quant,f32,c1,skinny,c4,copy")
+                    help="comma list of gemm,probe,quant,f32,c1,skinny,c4,copy,pcie (pcie: host-buffer rates)")
     ap.add_argument("--summarize", metavar="DIR", help="summarize rocprofv3 CSV output and exit")
     args = ap.parse_args()
     if args.summarize:
@@ -565,6 +615,13 @@ def main():
         log(f"C4 forward: {c4['ms_per_forward']:.3f} ms as a HIP graph ({c4['tokens_per_s']:.0f} tokens/s), "
             f"{c4['ms_per_forward_eager']:.3f} ms eager")
         Nn.call("kh_pool_trim")
+    host_buffers = None
+    if "pcie" in only:
+        log("C2 and C3a from host buffers ...")
+        host_buffers = bench_host_buffers()
+        log(f"host buffers: C2 {host_buffers['c2']['GB/s_pcie_inclusive']} GB/s, "
+            f"C3a {host_buffers['c3a']['TOPS_pcie_inclusive']} TOPS")
+        Nn.call("kh_pool_trim")
     if "copy" in only:
         c_ms, c_gbs = bench_copy(args.steps, args.warmup)
         log(f"1 GiB d2d copy: {c_ms:.4f} ms, {c_gbs:.0f} GB/s")
@@ -616,6 +673,7 @@ def main():
                           "bytes": "N*K + 8N + 4MK + 2MK + 4MN", "rows": skinny},
         "c1_linear": c1,
         "c4_forward": c4,
+        "host_buffers": host_buffers,
         "cpu_baseline": cpu,
         "device": info,
     }
