@@ -297,6 +297,16 @@ int kh_causal_attention_ex(const float* qkv, int B, int T, int H, int dk, float*
 /* The same with the mask chosen by the caller: causal = 1 as above, causal = 0
  * attends over all T keys -- BigGPT.forward passes no mask when the sequence
  * is shorter than its position table (train_shakespeare_large.py:86). */
+/* LayerNorm (as kh_layernorm) with its output quantized per row -- per token
+ * -- in one pass: scales[r] = max_j |y[r,j]| / 127 in binary64 (1.0 for an
+ * all-zero row) and q[r,j] = clamp(round_half_even(y[r,j] / scales[r]),
+ * -127, 127), quantize_symmetric (quantize.py:50-70) applied to each row of
+ * nn.LayerNorm's output (nn.py:308-331).  The fp32 values are never stored.
+ * No reference counterpart as one call: the reference quantizes activations
+ * per tensor only; this is the per-token producer fusion for callers that
+ * choose per-row activation scales. */
+int kh_layernorm_quant_rows(const float* x, int64_t rows, int D, const float* weight, const float* bias, float eps,
+                            int8_t* q, double* scales);
 int kh_attention_ex(const float* qkv, int B, int T, int H, int dk, int causal, float* out, unsigned* absmax_parts,
                     int max_parts, int* nparts);
 

@@ -113,13 +113,19 @@ class CharLM:
     one (or a float32 checkpoint, quantized per output channel on the way)
     into it in place.  `w` stays the construction-time weights."""
 
-    def __init__(self, w: CharLMWeights, producer_quant: bool | str = "layer_norm"):
+    def __init__(self, w: CharLMWeights, producer_quant: bool | str = "layer_norm", act_granularity: str = "tensor"):
         """producer_quant (kir.quant_fusion's option): "layer_norm" (the
         default) -- each LayerNorm emits its int8 codes directly instead of
         fp32 (two passes over its input; the fastest on MI355X); True -- fc1
-        (-> GELU) as well (less memory, slower); False -- neither."""
+        (-> GELU) as well (less memory, slower); False -- neither.
+        act_granularity: "tensor" (the reference's quantize_symmetric over the
+        whole activation, the C4 configuration) or "row" (one scale per token;
+        a LayerNorm then emits codes and scales in one pass)."""
+        if act_granularity not in ("tensor", "row"):
+            raise ValueError(f"act_granularity must be 'tensor' or 'row', not {act_granularity!r}")
         self.w = w
         self.producer_quant = producer_quant
+        self.act_granularity = act_granularity
         up = DeviceTensor.from_host
         self.tok, self.pos = up(w.tok), up(w.pos)
         self.blocks = []
@@ -163,7 +169,7 @@ class CharLM:
 
     def _fn(self, batch, seq):
         def linear(x, qw, b=None):
-            y = x.quantize("tensor").int8_matmul(qw).dequantize()
+            y = x.quantize(self.act_granularity).int8_matmul(qw).dequantize()
             return y.add(b) if b is not None else y
 
         def fn(ids):

@@ -157,12 +157,13 @@ __device__ __forceinline__ unsigned store_block32_masked(const Epilogue& ep, int
 
 // store_block32 for a block inside the matrix in the common configuration --
 // fp32 output only (or one of the quantize passes), per-tensor activation
-// scale -- with the uniform choices (bias, activation, residual) taken once
+// scale, or per-row scales (ROWSA: sa[i] * sb[j] per row, as in
+// store_block32_impl) -- with the uniform choices (bias, activation, residual) taken once
 // per block instead of per element, and raw buffer accesses whose row offsets
 // are scalar (8*(r/4) + r%4 rows of N floats), so no element needs address
 // arithmetic.  Same arithmetic, in the same order, as store_block32_impl.
 // (rowblk, colblk): the block's first row and column; N <= 2^24.
-template <bool FUSED, int MODE>
+template <bool FUSED, int MODE, bool ROWSA = false>
 __device__ __forceinline__ unsigned store_block32_full(const Epilogue& ep, int64_t rowblk, int64_t colblk, int N,
                                                        int lane, double sa, const i32x16& v,
                                                        const kh::quant::Scale& sc) {
@@ -170,6 +171,13 @@ __device__ __forceinline__ unsigned store_block32_full(const Epilogue& ep, int64
     const int64_t j = colblk + fr;
     const double sbj = ep.sb ? ep.sb[ep.sb_per_col ? j : 0] : 0.0;
     const double s = sa * sbj;
+    double srow[ROWSA ? 16 : 1];
+    if constexpr (ROWSA) {
+        // value r of this lane is row rowblk + 4*fh + 8*(r/4) + r%4
+        const double* sar = ep.sa + rowblk + 4 * fh;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) srow[r] = sar[8 * (r >> 2) + (r & 3)] * sbj;
+    }
     const int64_t base = rowblk * N + colblk;
     const uint32_t span = (uint32_t)N * 32u * 4u;  // the block's 32 rows, in bytes
     const int voff = (4 * fh * N + fr) * 4;
@@ -182,7 +190,7 @@ __device__ __forceinline__ unsigned store_block32_full(const Epilogue& ep, int64
     }
     float y[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) y[r] = (float)((double)v[r] * s);
+    for (int r = 0; r < 16; ++r) y[r] = (float)((double)v[r] * (ROWSA ? srow[ROWSA ? r : 0] : s));
     if (ep.bias) {
         const float bj = ep.bias[j];
 #pragma unroll
@@ -532,6 +540,16 @@ __global__ __launch_bounds__(512, BN == 256 ? 2 : 4) void gemm_i8_pingpong_kerne
                 mx = max(mx, store_block32_full<FUSED, MODE>(ep, (int64_t)tm * BM + wm * kWaveM + a * 32,
                                                              (int64_t)tn * BN + wn * kWaveN + b * 32, N, lane, sa,
                                                              acc[a][b], sc));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+    } else if (full && !ep.acc && ep.sa_per_row && MODE == kh::quant::kOutStore && ep.out && N <= (1 << 24)) {
+#pragma unroll
+        for (int a = 0; a < kTM; ++a)
+#pragma unroll
+            for (int b = 0; b < kTN; ++b) {
+                mx = max(mx, store_block32_full<FUSED, MODE, true>(ep, (int64_t)tm * BM + wm * kWaveM + a * 32,
+                                                                   (int64_t)tn * BN + wn * kWaveN + b * 32, N, lane,
+                                                                   0.0, acc[a][b], sc));
                 __builtin_amdgcn_sched_barrier(0);
             }
     } else if (full) {

@@ -148,13 +148,18 @@ __device__ __forceinline__ unsigned layernorm_row(const float* __restrict__ x, i
 // made the kernel compute-bound).  Rows >= `rows` are computed on zeros and
 // not stored.
 constexpr int kLnRowsPerWave = 4;
+// LayerNorm output quantized per row (per token): each row's own absmax,
+// binary64 scale (quantize.py:67-69 applied to the row) and codes, in one
+// pass -- a wave owns whole rows, so no other workgroup is involved.
+constexpr int kLnRowQuant = 3;
 
 template <int KV, int MODE>
 __device__ __forceinline__ unsigned layernorm_rows_vec(const float* __restrict__ x, int64_t row0, int64_t rows,
                                                        int D, const float* __restrict__ w,
                                                        const float* __restrict__ b, float eps,
                                                        float* __restrict__ out, int8_t* __restrict__ q,
-                                                       const kh::quant::Scale& sc, int lane) {
+                                                       const kh::quant::Scale& sc, double* __restrict__ rscales,
+                                                       unsigned* __restrict__ fault, int lane) {
     using namespace kh::quant;
     typedef float f4 __attribute__((ext_vector_type(4)));
     constexpr int R = kLnRowsPerWave;
@@ -201,6 +206,34 @@ __device__ __forceinline__ unsigned layernorm_rows_vec(const float* __restrict__
 #pragma unroll
     for (int r = 0; r < R; ++r) inv[r] = 1.0f / sqrtf(wave_sum(sumsq[r]) / (float)D + eps);
     unsigned mx = 0;
+    if constexpr (MODE == kLnRowQuant) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            unsigned rm = 0;
+#pragma unroll
+            for (int i = 0; i < KV; ++i) {
+                if (lane + i * 64 < D4) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        v[r][i][e] = v[r][i][e] * inv[r] * wv[i][e] + bv[i][e];
+                        rm = max(rm, kh::abs_bits32(v[r][i][e]));
+                    }
+                }
+            }
+            const Scale rs = make_scale(wave_max(rm));
+            if (row0 + r >= rows) continue;
+            if (lane == 0) {
+                rscales[row0 + r] = rs.s;
+                if (rs.bad) flag_nonfinite(fault);
+            }
+#pragma unroll
+            for (int i = 0; i < KV; ++i) {
+                const int c4 = lane + i * 64;
+                if (c4 < D4) reinterpret_cast<unsigned*>(q + (row0 + r) * D)[c4] = pack4(v[r][i], rs);
+            }
+        }
+        return 0;
+    }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         if (row0 + r >= rows) continue;
@@ -252,8 +285,9 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict_
     if constexpr (KV > 0) {
         static_assert(kLnRowsPerBlock == 4 * kLnRowsPerWave, "four waves");
         const int64_t row0 = (int64_t)blockIdx.x * kLnRowsPerBlock + (threadIdx.x >> 6) * kLnRowsPerWave;
-        mx = layernorm_rows_vec<KV, MODE>(x, row0, rows, D, w, b, eps, out, q, sc, lane);
+        mx = layernorm_rows_vec<KV, MODE>(x, row0, rows, D, w, b, eps, out, q, sc, qscale, fault, lane);
     } else {
+        static_assert(MODE != kLnRowQuant, "per-row codes: vectorized path only");
 #pragma unroll 1
         for (int k = threadIdx.x >> 6; k < kLnRowsPerBlock; k += 4) {
             const int64_t row = (int64_t)blockIdx.x * kLnRowsPerBlock + k;
@@ -576,6 +610,37 @@ int kh_layernorm_quant(const float* x, int64_t rows, int D, const float* weight,
     else if (vec) passes(std::integral_constant<int, 4>{});
     else passes(std::integral_constant<int, 0>{});
     return kh::launch_status("layernorm_quant");
+}
+
+int kh_layernorm_quant_rows(const float* x, int64_t rows, int D, const float* weight, const float* bias, float eps,
+                            int8_t* q, double* scales) {
+    KH_REQUIRE(rows >= 0 && D > 0, "kh_layernorm_quant_rows: bad shape");
+    KH_REQUIRE(D <= 64 * kLnMaxPerLane, "kh_layernorm_quant_rows: rows longer than 1024 are not supported");
+    if (rows == 0) return KH_OK;
+    KH_REQUIRE(x && weight && bias && q && scales, "kh_layernorm_quant_rows: null pointer");
+    KH_DEVICE_OR_RETURN(d);
+    const int64_t blocks = (rows + kLnRowsPerBlock - 1) / kLnRowsPerBlock;
+    KH_REQUIRE(blocks <= 0x7FFFFFFFLL, "kh_layernorm_quant_rows: too many rows");
+    const bool vec = D % 4 == 0 && kh::aligned(x, 16) && kh::aligned(q, 4) && kh::aligned(weight, 16) &&
+                     kh::aligned(bias, 16);
+    if (!vec) {
+        // Other shapes: the fp32 LayerNorm into a pool buffer, then the
+        // per-row quantize of it (the same values, so the same codes).
+        void* tmp = nullptr;
+        int rc = kh_alloc((size_t)rows * D * sizeof(float), &tmp);
+        if (rc) return rc;
+        rc = kh_layernorm(x, rows, D, weight, bias, eps, static_cast<float*>(tmp));
+        if (!rc) rc = kh_quantize_rows(static_cast<float*>(tmp), rows, D, q, scales);
+        const int frc = kh_free(tmp);
+        return rc ? rc : frc;
+    }
+    if (D <= 512)
+        layernorm_kernel<2, kLnRowQuant><<<(unsigned)blocks, 256, 0, d->stream>>>(
+            x, rows, D, weight, bias, eps, nullptr, nullptr, q, nullptr, 0, scales, d->fault);
+    else
+        layernorm_kernel<4, kLnRowQuant><<<(unsigned)blocks, 256, 0, d->stream>>>(
+            x, rows, D, weight, bias, eps, nullptr, nullptr, q, nullptr, 0, scales, d->fault);
+    return kh::launch_status("layernorm_quant_rows");
 }
 
 int kh_gelu(const float* x, float* out, int64_t n) {

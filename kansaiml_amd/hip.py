@@ -321,6 +321,18 @@ def layer_norm_quant(x: DeviceTensor, w: DeviceTensor, b: DeviceTensor, eps: flo
     return q, s
 
 
+def layer_norm_quant_rows(x: DeviceTensor, w: DeviceTensor, b: DeviceTensor, eps: float = 1e-5):
+    """LayerNorm with its output quantized per row in one pass (the fp32
+    values are never stored).  Returns (codes int8 [rows, D], scales float64
+    [rows])."""
+    _need(x, "float32", 2, "layer_norm_quant_rows(x)")
+    rows, D = x.shape
+    q = DeviceTensor([rows, D], "int8")
+    s = DeviceTensor([rows], "float64")
+    N.call("kh_layernorm_quant_rows", x.ptr, rows, D, w.ptr, b.ptr, eps, q.ptr, s.ptr)
+    return q, s
+
+
 def layer_norm(x: DeviceTensor, w: DeviceTensor, b: DeviceTensor, eps: float = 1e-5, *, absmax: bool = False):
     """LayerNorm over the last axis (nn.py:308-331).  Returns (out, AbsmaxParts | None)."""
     _need(x, "float32", 2, "layer_norm(x)")

@@ -240,6 +240,7 @@ def quant_fusion(graph, producer_quant: bool | str = False) -> Graph:
     and, with producer_quant=True (both) or "layer_norm" (the second only),
       ... the int8_linear chain -> quantize (per tensor) => int8_linear_quant
       layer_norm -> quantize (per tensor)        =>  layer_norm_quant
+      layer_norm -> quantize (per row)           =>  layer_norm_quant_rows
     int8_linear's attrs record what it absorbed: bias (bool), act ("gelu" or
     None) and residual (bool; the residual operand comes last).  The *_quant
     nodes produce the quantized tensor directly: their kernels run the
@@ -248,6 +249,8 @@ def quant_fusion(graph, producer_quant: bool | str = False) -> Graph:
     LayerNorm (two passes over its input cost less than writing the fp32
     values and reading them back) but not for the GEMM, whose VALU-bound
     epilogue (binary64 dequantize, exact-erf GELU) the second pass repeats.
+    layer_norm_quant_rows needs no second pass: each row's scale depends on
+    that row only, so one pass stores codes and scales.
     Then every int8_linear, layer_norm or attention whose
     output feeds a per-tensor quantize is marked absmax=True: its kernel
     writes the absmax partials that quantize needs, so the quantize reads
@@ -321,6 +324,12 @@ def quant_fusion(graph, producer_quant: bool | str = False) -> Graph:
                 absorbed.add(n.id)
                 fused[q] = ("layer_norm_quant", list(n.inputs), dict(n.attrs))
                 continue
+            q = only_user(n.id)
+            if (producer_quant in (True, "layer_norm") and q is not None and by_id[q].op == "quantize"
+                    and by_id[q].attrs.get("granularity") == "row"):
+                absorbed.add(n.id)
+                fused[q] = ("layer_norm_quant_rows", list(n.inputs), dict(n.attrs))
+                continue
         if n.op == "matmul":
             ad = only_user(n.id)
             if ad is not None and by_id[ad].op == "add":
@@ -342,7 +351,7 @@ def quant_fusion(graph, producer_quant: bool | str = False) -> Graph:
             continue
         if n.id in fused:
             op, ins, attrs = fused[n.id]
-            dtype = n.dtype if op.endswith("_quant") else "float32"
+            dtype = n.dtype if op.endswith(("_quant", "_quant_rows")) else "float32"
             nid = out.add(op, [remap[i] for i in ins], n.shape, dtype, **attrs)
         else:
             nid = out.add(n.op, [remap[i] for i in n.inputs], n.shape, n.dtype, **n.attrs)
@@ -532,6 +541,11 @@ def _exec(node, vals):
         x, w, b = ins
         q, s = H.layer_norm_quant(x, w, b, node.attrs.get("eps", 1e-5))
         return QTensor(q, s, list(node.shape), "tensor", packed=False)
+    if op == "layer_norm_quant_rows":
+        from .quantize import QTensor
+        x, w, b = ins
+        q, s = H.layer_norm_quant_rows(x, w, b, node.attrs.get("eps", 1e-5))
+        return QTensor(q, s, list(node.shape), "row", packed=False)
     if op == "embedding":
         ids, tok, pos = ins
         rows, D = node.shape

@@ -65,30 +65,34 @@ def causal_attention(qkv, batch, seq, heads):
     return attention(qkv, batch, seq, heads, causal=True)
 
 
-def linear(x, w, b=None, quantized=True):
+def linear(x, w, b=None, quantized=True, act_granularity="tensor"):
     if not quantized:
         y = (x @ w).astype(f32)
         return y + b if b is not None else y
-    qx, sx = O.ko_quantize_tensor(x)
+    if act_granularity == "row":
+        qx, sx = O.ko_quantize_rows(x)
+    else:
+        qx, sx = O.ko_quantize_tensor(x)
+        sx = [sx]
     qw, sw = O.ko_quantize_cols_packed(w)
     acc = O.ko_gemm_i8(qx, qw)
-    return O.ko_epilogue(acc, [sx], sw, b)
+    return O.ko_epilogue(acc, sx, sw, b)
 
 
-def forward(w, ids, quantized=True):
+def forward(w, ids, quantized=True, act_granularity="tensor"):
     """w: kansaiml_amd.charlm.CharLMWeights (plain numpy arrays); ids [B, T]."""
     ids = np.asarray(ids)
     batch, seq = ids.shape
     x = (w.tok[ids.reshape(-1)] + np.tile(w.pos[:seq], (batch, 1))).astype(f32)
     for p in w.blocks:
         h = layer_norm(x, p["ln1_w"], p["ln1_b"])
-        qkv = linear(h, np.concatenate([p["w_q"], p["w_k"], p["w_v"]], axis=1), None, quantized)
+        qkv = linear(h, np.concatenate([p["w_q"], p["w_k"], p["w_v"]], axis=1), None, quantized, act_granularity)
         # BigGPT adds its causal mask only at seq == BLOCK_SIZE
         # (train_shakespeare_large.py:86)
         a = attention(qkv, batch, seq, w.heads, causal=seq == w.seq)
-        x = (x + linear(a, p["w_o"], None, quantized)).astype(f32)
+        x = (x + linear(a, p["w_o"], None, quantized, act_granularity)).astype(f32)
         h = layer_norm(x, p["ln2_w"], p["ln2_b"])
-        f = gelu(linear(h, p["fc1_w"], p["fc1_b"], quantized))
-        x = (x + linear(f, p["fc2_w"], p["fc2_b"], quantized)).astype(f32)
+        f = gelu(linear(h, p["fc1_w"], p["fc1_b"], quantized, act_granularity))
+        x = (x + linear(f, p["fc2_w"], p["fc2_b"], quantized, act_granularity)).astype(f32)
     x = layer_norm(x, w.lnf_w, w.lnf_b)
-    return linear(x, w.head_w, w.head_b, quantized)
+    return linear(x, w.head_w, w.head_b, quantized, act_granularity)

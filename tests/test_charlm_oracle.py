@@ -388,12 +388,27 @@ def test_fused_qkv_linear_equals_three_linears():
     np.testing.assert_array_equal(fused.view(np.uint32), split.view(np.uint32))
 
 
-def test_quantized_forward_tracks_fp32():
+@pytest.mark.parametrize("act_granularity", ["tensor", "row"])
+def test_quantized_forward_tracks_fp32(act_granularity):
     """The int8 forward differs from the fp32 one only by quantization error:
     close, but not identical (so the quantized Linears are really used)."""
     w = _tiny_weights(5)
     ids = _gen(6).integers(0, 11, (2, 6))
-    q = R.forward(w, ids, quantized=True).astype(f64)
+    q = R.forward(w, ids, quantized=True, act_granularity=act_granularity).astype(f64)
     f = R.forward(w, ids, quantized=False).astype(f64)
     err = np.max(np.abs(q - f)) / np.max(np.abs(f))
     assert 0 < err < 0.1
+
+
+def test_per_token_linear_is_row_by_row():
+    """A per-row activation scale makes each output row depend on its own
+    input row only: the Linear of a stack equals the stack of each row's
+    Linear, bit for bit, and differs from the per-tensor Linear."""
+    g = _gen(13)
+    x = (g.standard_normal((6, 32)) * g.uniform(0.1, 10, (6, 1))).astype(f32)
+    wt = (g.standard_normal((32, 24)) * 0.1).astype(f32)
+    b = g.standard_normal(24).astype(f32)
+    whole = R.linear(x, wt, b, True, "row")
+    rows = np.concatenate([R.linear(x[i:i + 1], wt, b, True, "tensor") for i in range(6)])
+    np.testing.assert_array_equal(whole.view(np.uint32), rows.view(np.uint32))
+    assert not np.array_equal(whole, R.linear(x, wt, b, True, "tensor"))

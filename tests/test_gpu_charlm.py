@@ -109,6 +109,10 @@ def _check_node(node, got, ins):
     elif op == "add":
         a, b = ins
         np.testing.assert_array_equal(got.view(np.uint32), (a + b).astype(np.float32).view(np.uint32))
+    elif op == "quantize" and node.attrs.get("granularity") == "row":
+        q, s = O.ko_quantize_rows(ins[0])
+        np.testing.assert_array_equal(got[0], q)
+        np.testing.assert_array_equal(got[1], s)
     elif op == "quantize":
         q, s = O.ko_quantize_tensor(ins[0])
         np.testing.assert_array_equal(got[0], q.reshape(got[0].shape))
@@ -143,6 +147,15 @@ def _check_node(node, got, ins):
         q, s = O.ko_quantize_tensor(yh)
         np.testing.assert_array_equal(got[0], q.reshape(got[0].shape))
         assert got[1][0] == s
+    elif op == "layer_norm_quant_rows":
+        # kh_layernorm on the same input, then the oracle's per-row quantize
+        from kansaiml_amd import hip as H
+        from kansaiml_amd.device import DeviceTensor as D
+        x, w, b = ins
+        y, _ = H.layer_norm(D.from_host(x), D.from_host(w), D.from_host(b), node.attrs.get("eps", 1e-5))
+        q, s = O.ko_quantize_rows(y.numpy())
+        np.testing.assert_array_equal(got[0], q)
+        np.testing.assert_array_equal(got[1], s)
     elif op == "int8_linear_quant":
         # the unfused int8_linear on the same inputs (checked against the
         # oracle as the int8_linear node is), then the oracle's quantize
@@ -236,6 +249,59 @@ def test_small_model_matches_restatement(G, seq, producer_quant):
     fp = R.forward(w, ids, quantized=False)
     assert np.abs(y - fp).max() < 0.1 * np.abs(fp).max()
     # repeated forwards through the memory plan are identical
+    np.testing.assert_array_equal(model(ids).view(np.uint32), y.view(np.uint32))
+
+
+@pytest.mark.parametrize("rows,D", [(1, 384), (17, 384), (1000, 384), (64, 1024), (33, 48), (40, 50), (5, 700)])
+def test_layernorm_quant_rows(G, rows, D):
+    """One-pass LayerNorm + per-row quantize against kh_layernorm's fp32
+    output quantized per row by the oracle: codes and binary64 scales bit for
+    bit.  Row 0 is constant (its output is the bias; with a zero bias an
+    all-zero row, scale 1.0); D = 50 takes the unvectorized fallback."""
+    from oracle import oracle as O
+    from kansaiml_amd import hip as H
+    N, D_ = G
+    gen = np.random.Generator(np.random.PCG64(rows * 7 + D))
+    x = (gen.standard_normal((rows, D)) * gen.uniform(0.1, 30, (rows, 1))).astype(np.float32)
+    x[0] = 2.5
+    w = gen.standard_normal(D).astype(np.float32)
+    b = np.zeros(D, np.float32) if D == 48 else (gen.standard_normal(D) * 0.1).astype(np.float32)
+    xd, wd, bd = D_.from_host(x), D_.from_host(w), D_.from_host(b)
+    q, s = H.layer_norm_quant_rows(xd, wd, bd)
+    y, _ = H.layer_norm(xd, wd, bd)
+    rq, rs = O.ko_quantize_rows(y.numpy())
+    np.testing.assert_array_equal(q.numpy(), rq)
+    np.testing.assert_array_equal(s.numpy(), rs)
+    if D == 48:
+        assert s.numpy()[0] == 1.0 and not q.numpy()[0].any()
+
+
+@pytest.mark.parametrize("producer_quant", [False, "layer_norm"])
+def test_small_model_per_token(G, producer_quant):
+    """The C4 architecture with per-token activation scales (every Linear's
+    input quantized per row), node by node against the restatement on the
+    GPU's own inputs; with producer fusion each LayerNorm emits its codes and
+    scales in one pass."""
+    from kansaiml_amd.charlm import CharLM, CharLMWeights
+    w = CharLMWeights(layers=2, seq=128, seed=3, bias_std=0.02)
+    ids = np.random.Generator(np.random.PCG64(4)).integers(0, 65, (2, 128)).astype(np.int32)
+    model = CharLM(w, producer_quant=producer_quant, act_granularity="row")
+    seen = {}
+    y = model(ids, observe=lambda node, v: seen.__setitem__(node.id, (node, _host(v))))
+    g, _ = model.graph(2, 128)
+    by_id = {n.id: n for n in g.nodes}
+    checked = set()
+    for nid, (node, got) in seen.items():
+        if node.op == "constant":
+            continue
+        ins = [ids if by_id[i].op == "placeholder" else seen[i][1] for i in node.inputs]
+        _check_node(node, got, ins)
+        checked.add(node.op)
+    ln = "layer_norm_quant_rows" if producer_quant else "layer_norm"
+    assert checked == {"embedding", ln, "quantize", "int8_linear", "attention"}
+    assert all(n.attrs.get("granularity") == "row" for n in g.nodes if n.op == "quantize")
+    fp = R.forward(w, ids, quantized=False)
+    assert np.abs(y - fp).max() < 0.1 * np.abs(fp).max()
     np.testing.assert_array_equal(model(ids).view(np.uint32), y.view(np.uint32))
 
 

@@ -245,16 +245,20 @@ def test_matmul_f32_c3b_full_size(hip):
                                    (300, 1152, 384),     # ping-pong, partial tiles
                                    (130, 70, 80),        # general kernel (K % 64 != 0)
                                    (8, 512, 512)])       # skinny kernel
-def test_gemm_i8_fused_epilogues(hip, M, N, K):
+@pytest.mark.parametrize("row_scales", [False, True])
+def test_gemm_i8_fused_epilogues(hip, M, N, K, row_scales):
     """GELU and residual epilogues give the same bits as the unfused graph
     (gemm -> gelu kernel, gemm -> fp32 add), and the absmax partials a fused
-    GEMM writes quantize its output exactly like kh_quantize_tensor."""
+    GEMM writes quantize its output exactly like kh_quantize_tensor; with a
+    per-tensor or a per-row (per-token) activation scale."""
     from kansaiml_amd import _native as Nn
     H, D = hip
     gen = np.random.Generator(np.random.PCG64(M + 3 * N + 7 * K))
     a = gen.integers(-127, 128, (M, K), dtype=np.int8)
     bt = gen.integers(-127, 128, (N, K), dtype=np.int8)
     sa, sb = np.array([3e-4]), gen.uniform(1e-4, 1e-3, N)
+    if row_scales:
+        sa = gen.uniform(1e-4, 1e-3, M)
     bias = gen.standard_normal(N).astype(np.float32)
     res = gen.standard_normal((M, N)).astype(np.float32)
     ad, bd, sad, sbd, biasd = D.from_host(a), D.from_host(bt), D.from_host(sa), D.from_host(sb), D.from_host(bias)

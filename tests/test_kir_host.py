@@ -150,9 +150,16 @@ def test_quantize_producers_fuse_into_quant_nodes():
     def per_row(x):
         return x.layer_norm(g1, b1).quantize("row").int8_matmul(x._coerce(w1).quantize()).dequantize()
 
-    ops3 = [n.op for n in kir.quant_fusion(kir.trace(per_row, np.zeros((4, 16), np.float32)),
-                                           producer_quant=True).nodes]
-    assert "layer_norm" in ops3 and "layer_norm_quant" not in ops3
+    # a per-row quantize of a LayerNorm fuses into one pass (codes and
+    # per-row scales), under either producer option, and not when it is off
+    gr = kir.trace(per_row, np.zeros((4, 16), np.float32))
+    for opt in (True, "layer_norm"):
+        fr = kir.quant_fusion(gr, producer_quant=opt)
+        ops3 = [n.op for n in fr.nodes]
+        assert "layer_norm_quant_rows" in ops3 and "layer_norm" not in ops3 and "layer_norm_quant" not in ops3
+        assert [n for n in fr.nodes if n.op == "layer_norm_quant_rows"][0].dtype == "int8"
+    ops4 = [n.op for n in kir.quant_fusion(gr).nodes]
+    assert "layer_norm" in ops4 and "layer_norm_quant_rows" not in ops4
 
 
 @pytest.mark.parametrize("values,shape", [([1.0, 2.0, 3.0], [2, 2]), ([], [1]), ([1.0], [-1]), ([1.0, 2.0], [1])])
