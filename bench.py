@@ -379,10 +379,15 @@ def bench_c4(steps, warmup):
     ms = time_kernel(lambda: g(ids, to_host=False), steps, warmup)
     g.close()
     breakdown = c4_gemm_breakdown(model, ids, ms, steps)
+    # the same forward with per-token activation scales (an option beside
+    # the reference's per-tensor configuration), replayed as a HIP graph
+    gr = CharLM(w, act_granularity="row").capture(64, 256)
+    ms_row = time_kernel(lambda: gr(ids, to_host=False), steps, warmup)
+    gr.close()
     ops = int8_linear_ops(w, 64, 256)
     return {"workload": "C4 int8 char-LM forward, batch 64 x seq 256 (16384 tokens), 6 layers, d 384",
             "ms_per_forward": round(ms, 4), "tokens_per_s": round(64 * 256 / (ms * 1e-3), 1),
-            "ms_per_forward_eager": round(eager, 4),
+            "ms_per_forward_eager": round(eager, 4), "ms_per_forward_per_token_scales": round(ms_row, 4),
             "int8_linear_ops": ops, "int8_linear_TOPS_over_forward": round(ops / (ms * 1e-3) / 1e12, 2),
             "attention_fp32_flops_full_square": attention_flops(w, 64, 256), **breakdown}
 
