@@ -46,12 +46,11 @@ class DeviceTensor:
             raise ValueError(f"negative dimension in {self.shape}")
         self.dtype = dtype
         self.nbytes = math.prod(self.shape) * np.dtype(DTYPES[dtype]).itemsize
+        self.ptr, self._owned, self.absmax_parts, self._base = None, False, None, None  # until kh_alloc succeeds
         p = ctypes.c_void_p()
         N.call("kh_alloc", max(self.nbytes, 1), ctypes.byref(p))
         self.ptr = p
         self._owned = True
-        self.absmax_parts = None
-        self._base = None
 
     # -- construction -----------------------------------------------------
     @classmethod

@@ -31,6 +31,18 @@ def _opt(t):
     return t.ptr if t is not None else None
 
 
+def _need_ln_params(x: DeviceTensor, w: DeviceTensor, b: DeviceTensor, what: str):
+    """LayerNorm operands: x [rows, D] fp32 and weight, bias fp32 [D].  The C
+    ABI cannot see buffer sizes, so a short weight or bias would be read out
+    of bounds on the device: refuse it here."""
+    _need(x, "float32", 2, f"{what}(x)")
+    _need(w, "float32", 1, f"{what}(weight)")
+    _need(b, "float32", 1, f"{what}(bias)")
+    D = x.shape[1]
+    if w.shape[0] != D or b.shape[0] != D:
+        raise RuntimeError(f"{what}: weight and bias must have {D} entries, got {w.shape} and {b.shape}")
+
+
 # ---------------------------------------------------------------------------
 # quantize / dequantize (python/kansai/quantize.py:50-77)
 # ---------------------------------------------------------------------------
@@ -314,7 +326,7 @@ def gemm_i8_quant(a: DeviceTensor, b_packed: DeviceTensor, sa: DeviceTensor, sb:
 def layer_norm_quant(x: DeviceTensor, w: DeviceTensor, b: DeviceTensor, eps: float = 1e-5):
     """quantize_tensor(layer_norm(x)) without writing the fp32 output:
     returns (codes int8 like x, scale float64 [1])."""
-    _need(x, "float32", 2, "layer_norm(x)")
+    _need_ln_params(x, w, b, "layer_norm_quant")
     q = DeviceTensor(x.shape, "int8")
     s = DeviceTensor([1], "float64")
     N.call("kh_layernorm_quant", x.ptr, x.shape[0], x.shape[1], w.ptr, b.ptr, eps, q.ptr, s.ptr)
@@ -325,7 +337,7 @@ def layer_norm_quant_rows(x: DeviceTensor, w: DeviceTensor, b: DeviceTensor, eps
     """LayerNorm with its output quantized per row in one pass (the fp32
     values are never stored).  Returns (codes int8 [rows, D], scales float64
     [rows])."""
-    _need(x, "float32", 2, "layer_norm_quant_rows(x)")
+    _need_ln_params(x, w, b, "layer_norm_quant_rows")
     rows, D = x.shape
     q = DeviceTensor([rows, D], "int8")
     s = DeviceTensor([rows], "float64")
@@ -335,7 +347,7 @@ def layer_norm_quant_rows(x: DeviceTensor, w: DeviceTensor, b: DeviceTensor, eps
 
 def layer_norm(x: DeviceTensor, w: DeviceTensor, b: DeviceTensor, eps: float = 1e-5, *, absmax: bool = False):
     """LayerNorm over the last axis (nn.py:308-331).  Returns (out, AbsmaxParts | None)."""
-    _need(x, "float32", 2, "layer_norm(x)")
+    _need_ln_params(x, w, b, "layer_norm")
     out = DeviceTensor(x.shape, "float32")
     parts = AbsmaxParts() if absmax else None
     N.call("kh_layernorm_ex", x.ptr, x.shape[0], x.shape[1], w.ptr, b.ptr, eps, out.ptr,
@@ -348,6 +360,12 @@ def attention(qkv: DeviceTensor, batch: int, seq: int, heads: int, d_model: int,
     """Multi-head attention core (nn.py:381-427), with the causal mask or none.
     Returns (out, AbsmaxParts | None)."""
     _need(qkv, "float32", 2, "attention(qkv)")
+    if heads <= 0 or d_model != heads * 64:
+        raise RuntimeError(f"attention: d_model must be heads * 64 (the kernel's head size), got {d_model} "
+                           f"for {heads} heads")
+    if batch < 0 or seq < 0 or list(qkv.shape) != [batch * seq, 3 * d_model]:
+        raise RuntimeError(f"attention: qkv must be [batch * seq, 3 * d_model] = [{batch * seq}, {3 * d_model}], "
+                           f"got {qkv.shape}")
     out = DeviceTensor([batch * seq, d_model], "float32")
     parts = AbsmaxParts() if absmax else None
     N.call("kh_attention_ex", qkv.ptr, batch, seq, heads, d_model // heads, int(bool(causal)), out.ptr,

@@ -17,7 +17,8 @@ QTensor here lives on the device (int8 codes + binary64 scales) and may be
 per-tensor, per-row (per token) or per-column (per output channel, stored
 packed [out, in] for the GEMM); QLinear(linear, mode="int8") quantizes its
 input dynamically and runs the int8 GEMM with a fused dequantize + bias
-epilogue.  Traced through kansaiml_amd.kir, QLinear emits quantize /
+epilogue.  Traced through kansaiml_amd.kir (or any tracer on the reference's
+schema that has the three emitters), QLinear emits quantize /
 int8_matmul / dequantize nodes.
 """
 
@@ -158,6 +159,8 @@ class QLinear:
                  weight_granularity: str = "tensor"):
         if mode not in ("weight_only", "int8"):
             raise ValueError(f"QLinear: mode must be 'weight_only' or 'int8', got {mode!r}")
+        if act_granularity not in ("tensor", "row"):
+            raise ValueError(f"QLinear: act_granularity must be 'tensor' or 'row', got {act_granularity!r}")
         self.mode = mode
         self.act_granularity = act_granularity
         self.qweight = QTensor.from_weight(linear.weight, weight_granularity)
@@ -181,13 +184,8 @@ class QLinear:
         assign_in_place(name, target, value)
 
     def __call__(self, x):
-        from .kir import TraceValue
-        if isinstance(x, TraceValue):
-            if self.mode == "weight_only":
-                y = x.matmul(x._coerce(self.qweight).dequantize())
-            else:
-                y = x.quantize(self.act_granularity).int8_matmul(self.qweight).dequantize()
-            return y.add(self.bias) if self.bias is not None else y
+        if _is_traced(x):
+            return self._trace(x)
         if self.mode == "weight_only":
             return qlinear(x, self.qweight, self.bias)
         xd = to_device(x, "float32")
@@ -196,3 +194,32 @@ class QLinear:
         q, s = H.quantize_tensor(xd)
         out, _ = H.gemm_i8(q.reshape(xd.shape), self.qweight.codes, s, self.qweight.scales, self.bias)
         return out
+
+    def _trace(self, x):
+        """Records this layer into x's graph.  x is a value of this package's
+        tracer or of any tracer on the reference's schema (the reference's
+        kansai.kir.TraceValue, kir.py:115-147).  int8 mode needs the tracer's
+        quantize / int8_matmul / dequantize emitters (the reference's tracer
+        has none until they are added to it).  weight_only mode under a
+        tracer without them records what the reference's own QLinear records
+        there: a matmul with the dequantized weight captured as a constant
+        (kir.py:129-136)."""
+        from .kir import TraceValue
+        has_int8 = all(callable(getattr(x, m, None)) for m in ("quantize", "int8_matmul", "dequantize"))
+        if self.mode == "weight_only":
+            if isinstance(x, TraceValue):
+                y = x.matmul(x._coerce(self.qweight).dequantize())
+            else:
+                y = x.matmul(self.qweight.dequantize())
+        elif has_int8:
+            y = x.quantize(self.act_granularity).int8_matmul(self.qweight).dequantize()
+        else:
+            raise TypeError(f"QLinear(mode='int8'): the tracer's {type(x).__name__} has no quantize / int8_matmul / "
+                            "dequantize emitters; add them to it (kansaiml_amd.kir.TraceValue defines the three)")
+        return y.add(self.bias) if self.bias is not None else y
+
+
+def _is_traced(x) -> bool:
+    """True for a tracer's value: it names a graph and a node instead of
+    holding storage (the reference's TraceValue, kir.py:115-127)."""
+    return hasattr(x, "graph") and hasattr(x, "node_id")

@@ -62,6 +62,19 @@ def test_per_col_packed_matches_golden(name):
     np.testing.assert_array_equal(q, g["q_packed"])
 
 
+@pytest.mark.parametrize("name", ["ref_test_quantize_1000"] + golden_names("per_col_"))
+def test_per_tensor_packed_is_transposed_per_tensor(name):
+    """ko_quantize_tensor_packed is its own loop: pin it to the per-tensor
+    quantize (itself pinned by the fixtures above) of the same [k, n] weight,
+    transposed into the packed [n, k] layout -- codes and scale."""
+    g = load_golden(name)
+    w = g["w"] if "w" in g else g["x"].reshape(40, 25)
+    q, s = O.ko_quantize_tensor_packed(w)
+    qt, st_ = O.ko_quantize_tensor(w)
+    assert s == st_
+    np.testing.assert_array_equal(q, qt.T)
+
+
 def test_ties_go_to_even():
     g = load_golden("ties_scale_one")
     q, s = O.ko_quantize_tensor(g["x"])
