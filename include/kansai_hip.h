@@ -226,6 +226,22 @@ int kh_linear_i8(const float* x, int64_t M, int64_t K, const int8_t* b_packed, i
                  const double* sb, int sb_per_col, const float* bias,
                  int8_t* q_scratch, double* sx_scratch, float* out);
 
+/* kh_linear_i8 for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight decode loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference.  The per-row codes and scales go to a
+ * fixed array compiled into the library (2 MiB of codes + 2048 binary64
+ * scales, one copy per device for the life of the process) instead of
+ * q_scratch / sx_scratch: calls with M > 2048 or M * K > 2 MiB are
+ * rejected (KH_ERR_INVALID_ARG).  Allocates nothing and never initialises
+ * a device: call kh_init (or any other entry point) on the device first,
+ * else KH_ERR_NO_DEVICE.  Output is identical to kh_linear_i8's.  Every
+ * call on a device shares its one array, which keeps the last call's
+ * codes; calls are ordered on the library stream, so calls that overlap
+ * on one GPU (a graph holding this call replayed outside the library
+ * stream, say) race on it. */
+int kh_linear_i8_noalloc(const float* x, int64_t M, int64_t K, const int8_t* b_packed, int64_t N,
+                         const double* sb, int sb_per_col, const float* bias, float* out);
+
 /* The epilogue alone, for an int8_matmul whose dequantize was not fused:
  * out[i, j] = (float)((double)acc[i, j] * (sa_i * sb_j)) [+ bias[j]].
  * quantize.py:76 applied to an accumulator. */
@@ -281,6 +297,16 @@ int kh_layernorm_ex(const float* x, int64_t rows, int D, const float* weight, co
  * kh_quantize_tensor of kh_layernorm's output bit for bit. */
 int kh_layernorm_quant(const float* x, int64_t rows, int D, const float* weight, const float* bias, float eps,
                        int8_t* q, double* scale);
+/* LayerNorm (as kh_layernorm) with its output quantized per row -- per token
+ * -- in one pass: scales[r] = max_j |y[r,j]| / 127 in binary64 (1.0 for an
+ * all-zero row) and q[r,j] = clamp(round_half_even(y[r,j] / scales[r]),
+ * -127, 127), quantize_symmetric (quantize.py:50-70) applied to each row of
+ * nn.LayerNorm's output (nn.py:308-331).  The fp32 values are never stored.
+ * No reference counterpart as one call: the reference quantizes activations
+ * per tensor only; this is the per-token producer fusion for callers that
+ * choose per-row activation scales. */
+int kh_layernorm_quant_rows(const float* x, int64_t rows, int D, const float* weight, const float* bias, float eps,
+                            int8_t* q, double* scales);
 
 /* Exact-erf GELU (backend/cpu/src/Ops.cpp:250-256). */
 int kh_gelu(const float* x, float* out, int64_t n);
@@ -297,16 +323,6 @@ int kh_causal_attention_ex(const float* qkv, int B, int T, int H, int dk, float*
 /* The same with the mask chosen by the caller: causal = 1 as above, causal = 0
  * attends over all T keys -- BigGPT.forward passes no mask when the sequence
  * is shorter than its position table (train_shakespeare_large.py:86). */
-/* LayerNorm (as kh_layernorm) with its output quantized per row -- per token
- * -- in one pass: scales[r] = max_j |y[r,j]| / 127 in binary64 (1.0 for an
- * all-zero row) and q[r,j] = clamp(round_half_even(y[r,j] / scales[r]),
- * -127, 127), quantize_symmetric (quantize.py:50-70) applied to each row of
- * nn.LayerNorm's output (nn.py:308-331).  The fp32 values are never stored.
- * No reference counterpart as one call: the reference quantizes activations
- * per tensor only; this is the per-token producer fusion for callers that
- * choose per-row activation scales. */
-int kh_layernorm_quant_rows(const float* x, int64_t rows, int D, const float* weight, const float* bias, float eps,
-                            int8_t* q, double* scales);
 int kh_attention_ex(const float* qkv, int B, int T, int H, int dk, int causal, float* out, unsigned* absmax_parts,
                     int max_parts, int* nparts);
 

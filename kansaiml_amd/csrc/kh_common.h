@@ -28,11 +28,22 @@ int launch_status(const char* kernel);
 constexpr unsigned kFaultNonFinite = 1u;
 constexpr unsigned kFaultBadIndex = 2u;
 
+// The fixed device array behind the entry points that allocate nothing
+// (kh_linear_i8_noalloc): kNoAllocCodeBytes of int8 codes followed by
+// kNoAllocRows binary64 scales.  Defined in kh_runtime.hip; every device
+// holds its own copy from module load until the process ends.
+constexpr size_t kNoAllocCodeBytes = size_t(2) << 20;
+constexpr int64_t kNoAllocRows = 2048;
+constexpr size_t kNoAllocBytes = kNoAllocCodeBytes + size_t(kNoAllocRows) * sizeof(double);
+
 struct Device {
     int id = -1;
     hipStream_t stream = nullptr;
     unsigned* fault = nullptr;   // device word, see kFaultNonFinite
     int cus = 0;
+    // This device's address of the fixed no-alloc array, looked up once by
+    // hipGetSymbolAddress when the device is initialised.
+    unsigned char* noalloc = nullptr;
 };
 
 // The calling thread's current device, initialised on first use (device 0
@@ -40,11 +51,17 @@ struct Device {
 // when no usable gfx950 device exists.
 Device* current();
 
-// A device scratch area of at least `bytes`, owned by the library, valid
-// until the next scratch() call on the same device.  All library work is
-// ordered on the device's single library stream, so consecutive calls
-// reuse it safely.  Returns nullptr (and sets the last error) on OOM.
-void* scratch(Device* d, size_t bytes);
+// The calling thread's current device only if it is already initialised
+// (by kh_init or any earlier call); otherwise nullptr and the last error.
+// Initialising creates a stream and allocates, so entry points that must
+// not allocate use this instead of current().
+Device* current_initialized();
+
+// A growable device scratch area of at least `bytes`, owned by the library,
+// valid until the next scratch_area() call on the same device.  All library
+// work is ordered on the device's single library stream, so consecutive
+// calls reuse it safely.  Returns nullptr (and sets the last error) on OOM.
+void* scratch_area(Device* d, size_t bytes);
 
 // True while a graph capture (kh_graph_capture_begin .. _end) is open on the
 // device's library stream: host-synchronous work must refuse to run.

@@ -1097,7 +1097,7 @@ int kh_gemm_i8_quant(const int8_t* a, const int8_t* b_packed, int64_t M, int64_t
         // (so the same values), quantized with the scale of those partials;
         // the fp32 result never reaches memory.
         const int64_t worst = ((M + 127) / 128) * ((N + 127) / 128);
-        auto* parts = static_cast<unsigned*>(kh::scratch(d, (size_t)worst * sizeof(unsigned)));
+        auto* parts = static_cast<unsigned*>(kh::scratch_area(d, (size_t)worst * sizeof(unsigned)));
         if (!parts) return KH_ERR_OOM;
         Epilogue ep{sa, sb, bias, nullptr, nullptr, sa_per_row, sb_per_col, act, residual,
                     q, parts, 0, scale, d->fault};
@@ -1120,9 +1120,11 @@ int kh_gemm_i8_quant(const int8_t* a, const int8_t* b_packed, int64_t M, int64_t
     return rc;
 }
 
-int kh_linear_i8(const float* x, int64_t M, int64_t K, const int8_t* b_packed, int64_t N, const double* sb,
-                 int sb_per_col, const float* bias, int8_t* q_scratch, double* sx_scratch, float* out) {
-    KH_REQUIRE(out, "kh_linear_i8: null out");
+// kh_linear_i8's work with the codes and scales in q_scratch / sx_scratch.
+// Allocates nothing: the decode kernel, kh_quantize_rows and kh_gemm_i8
+// without absmax partials use no library scratch.
+static int linear_i8_impl(const float* x, int64_t M, int64_t K, const int8_t* b_packed, int64_t N, const double* sb,
+                          int sb_per_col, const float* bias, int8_t* q_scratch, double* sx_scratch, float* out) {
     if (M >= 1 && N >= 1 && x && b_packed && sb && q_scratch && sx_scratch &&
         decode_fits(x, M, K, b_packed, N, q_scratch)) {
         KH_DEVICE_OR_RETURN(d);
@@ -1135,6 +1137,30 @@ int kh_linear_i8(const float* x, int64_t M, int64_t K, const int8_t* b_packed, i
     int rc = kh_quantize_rows(x, M, K, q_scratch, sx_scratch);
     if (rc) return rc;
     return kh_gemm_i8(q_scratch, b_packed, M, N, K, sx_scratch, 1, sb, sb_per_col, bias, out, nullptr);
+}
+
+int kh_linear_i8(const float* x, int64_t M, int64_t K, const int8_t* b_packed, int64_t N, const double* sb,
+                 int sb_per_col, const float* bias, int8_t* q_scratch, double* sx_scratch, float* out) {
+    KH_REQUIRE(out, "kh_linear_i8: null out");
+    return linear_i8_impl(x, M, K, b_packed, N, sb, sb_per_col, bias, q_scratch, sx_scratch, out);
+}
+
+int kh_linear_i8_noalloc(const float* x, int64_t M, int64_t K, const int8_t* b_packed, int64_t N, const double* sb,
+                         int sb_per_col, const float* bias, float* out) {
+    KH_REQUIRE(out, "kh_linear_i8_noalloc: null out");
+    KH_REQUIRE(M >= 0 && K >= 0, "kh_linear_i8_noalloc: negative shape");
+    KH_REQUIRE(M <= kh::kNoAllocRows,
+               "kh_linear_i8_noalloc: M = " + std::to_string(M) + " exceeds the fixed scratch's " +
+                   std::to_string(kh::kNoAllocRows) + " rows");
+    KH_REQUIRE(K <= (int64_t)kh::kNoAllocCodeBytes && M * K <= (int64_t)kh::kNoAllocCodeBytes,
+               "kh_linear_i8_noalloc: M * K = " + std::to_string(M * K) + " codes exceed the fixed scratch's " +
+                   std::to_string(kh::kNoAllocCodeBytes) + " bytes");
+    // Never initialises the device (that allocates): kh_init first.
+    kh::Device* d = kh::current_initialized();
+    if (!d) return KH_ERR_NO_DEVICE;
+    int8_t* q = reinterpret_cast<int8_t*>(d->noalloc);
+    double* sx = reinterpret_cast<double*>(d->noalloc + kh::kNoAllocCodeBytes);
+    return linear_i8_impl(x, M, K, b_packed, N, sb, sb_per_col, bias, q, sx, out);
 }
 
 }  // extern "C"

@@ -80,7 +80,7 @@ int kh_probe_stream_read(const void* p, int64_t bytes) {
     KH_REQUIRE(p && bytes > 0 && bytes % 16 == 0 && bytes < (1LL << 31) && kh::aligned(p, 16),
                "kh_probe_stream_read: 16-byte aligned buffer of 16 B .. 2 GiB (a multiple of 16) required");
     KH_DEVICE_OR_RETURN(d);
-    int* sink = static_cast<int*>(kh::scratch(d, 256));
+    int* sink = static_cast<int*>(kh::scratch_area(d, 256));
     if (!sink) return KH_ERR_OOM;
     const int64_t per_block = 8LL * kProbeThreads * 16;
     const unsigned blocks = (unsigned)((bytes + per_block - 1) / per_block);
@@ -95,7 +95,7 @@ int kh_probe_mfma_i8(const int8_t* operands, int64_t bytes, int64_t iters, doubl
     const int64_t need = (int64_t)d->cus * kProbeThreads * 8 * 16;
     KH_REQUIRE(operands && bytes >= need && kh::aligned(operands, 16),
                "kh_probe_mfma_i8: operands must be 16-byte aligned and hold cus * 64 KiB");
-    unsigned long long* clocks = static_cast<unsigned long long*>(kh::scratch(d, 512));
+    unsigned long long* clocks = static_cast<unsigned long long*>(kh::scratch_area(d, 512));
     if (!clocks) return KH_ERR_OOM;
     int rc = kh::hip_status(hipMemsetAsync(clocks, 0, 512, d->stream), "hipMemsetAsync(probe)");
     if (rc) return rc;

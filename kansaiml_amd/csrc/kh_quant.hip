@@ -440,7 +440,7 @@ int fill_scales_one(kh::Device* d, double* scales, int64_t count) {
 // Pass 1 of a per-tensor quantize: per-block absmax bits into library scratch.
 int tensor_absmax(kh::Device* d, const float* x, int64_t n, bool vec, unsigned** partials, int* nparts) {
     const int g = grid_for(vec ? (n >> 2) : n, 8, kMaxPartials);
-    unsigned* p = static_cast<unsigned*>(kh::scratch(d, kMaxPartials * sizeof(unsigned)));
+    unsigned* p = static_cast<unsigned*>(kh::scratch_area(d, kMaxPartials * sizeof(unsigned)));
     if (!p) return KH_ERR_OOM;
     if (vec)
         absmax_partials_kernel<true><<<g, 256, 0, d->stream>>>(x, n, p);
@@ -543,7 +543,7 @@ static int quantize_packed(const float* w, int64_t k, int64_t n, int8_t* qp, dou
     const unsigned gx = (unsigned)((n + kTile - 1) / kTile);
     const unsigned gy = (unsigned)((k + kTile - 1) / kTile);
     if (per_col) {
-        unsigned* colmax = static_cast<unsigned*>(kh::scratch(d, (size_t)n * sizeof(unsigned)));
+        unsigned* colmax = static_cast<unsigned*>(kh::scratch_area(d, (size_t)n * sizeof(unsigned)));
         if (!colmax) return KH_ERR_OOM;
         fill_u32_kernel<<<(unsigned)((n + 255) / 256), 256, 0, d->stream>>>(colmax, n, 0u);
         dim3 g1((unsigned)((n + 255) / 256), (unsigned)((k + kColRowsPerBlock - 1) / kColRowsPerBlock));

@@ -17,6 +17,12 @@
 
 #include "kh_common.h"
 
+// The fixed scratch array of the allocation-free entry points (see
+// kh::kNoAllocBytes).  In host code this name is a host-side stand-in, not a
+// device address: host code uses only the per-device address that
+// hipGetSymbolAddress returns in init_slot (Device::noalloc).
+static __device__ __align__(256) unsigned char scratch[kh::kNoAllocBytes];
+
 namespace kh {
 
 namespace {
@@ -101,6 +107,11 @@ int init_slot(int dev) {
     if (rc) return rc;
     rc = hip_status(hipMemset(s.dev.fault, 0, 256), "hipMemset(fault word)");
     if (rc) return rc;
+    // With `dev` current: this device's copy of the fixed no-alloc array.
+    void* na = nullptr;
+    rc = hip_status(hipGetSymbolAddress(&na, HIP_SYMBOL(::scratch)), "hipGetSymbolAddress(no-alloc scratch)");
+    if (rc) return rc;
+    s.dev.noalloc = static_cast<unsigned char*>(na);
     s.ready = true;
     return KH_OK;
 }
@@ -149,7 +160,26 @@ Device* current() {
     return &g_slots[dev].dev;
 }
 
-void* scratch(Device* d, size_t bytes) {
+Device* current_initialized() {
+    const int dev = t_device < 0 ? 0 : t_device;
+    {
+        std::lock_guard<std::mutex> lk(g_init_mu);
+        if (!g_slots[dev].ready) {
+            fail(KH_ERR_NO_DEVICE, "device not initialised: call kh_init (or any other entry point) first");
+            return nullptr;
+        }
+    }
+    if (t_device != dev) {
+        if (hipSetDevice(dev) != hipSuccess) {
+            fail(KH_ERR_HIP, "hipSetDevice failed");
+            return nullptr;
+        }
+        t_device = dev;
+    }
+    return &g_slots[dev].dev;
+}
+
+void* scratch_area(Device* d, size_t bytes) {
     DeviceSlot& s = g_slots[d->id];
     std::lock_guard<std::mutex> lk(s.scratch_mu);
     if (bytes <= s.scratch_bytes) return s.scratch;

@@ -590,7 +590,7 @@ int kh_layernorm_quant(const float* x, int64_t rows, int D, const float* weight,
     KH_REQUIRE(x && weight && bias && q, "kh_layernorm_quant: null pointer");
     const int64_t blocks = (rows + kLnRowsPerBlock - 1) / kLnRowsPerBlock;
     KH_REQUIRE(blocks <= 0x7FFFFFFFLL, "kh_layernorm_quant: too many rows");
-    auto* parts = static_cast<unsigned*>(kh::scratch(d, (size_t)blocks * sizeof(unsigned)));
+    auto* parts = static_cast<unsigned*>(kh::scratch_area(d, (size_t)blocks * sizeof(unsigned)));
     if (!parts) return KH_ERR_OOM;
     const bool vec = D % 4 == 0 && kh::aligned(x, 16) && kh::aligned(q, 4) && kh::aligned(weight, 16) &&
                      kh::aligned(bias, 16);
