@@ -68,11 +68,13 @@ WARM_MS = 50.0
 WARMUP_LOG = {}
 
 
-def warm_up(fn, calls, min_ms=WARM_MS, tag=None):
+def warm_up(fn, calls, min_ms=None, tag=None):
     """At least `calls` untimed calls of fn(), continued in batches (each
     followed by a device synchronization) until min_ms of wall time has
     passed.  Returns the milliseconds spent; recorded under `tag`."""
     from kansaiml_amd import _native as N
+    if min_ms is None:
+        min_ms = WARM_MS  # read at call time: --warm-ms sets it
     N.synchronize()
     t0 = time.perf_counter()
     n, batch = 0, max(1, calls)
@@ -90,7 +92,7 @@ def warm_up(fn, calls, min_ms=WARM_MS, tag=None):
     return el
 
 
-def time_kernel(fn, steps, warmup, tag=None, min_warm_ms=WARM_MS):
+def time_kernel(fn, steps, warmup, tag=None, min_warm_ms=None):
     """Average ms per call of fn() over `steps` back-to-back calls, HIP events
     on the library stream, synchronized before and after, after warm_up()."""
     from kansaiml_amd import _native as N
@@ -507,7 +509,7 @@ _GEMM_ARGS = "--only gemm --steps 3 --warmup 1 --no-cpu --warm-ms 0"
 _C4_ARGS = "--only c4 --steps 4 --warmup 2 --no-cpu --warm-ms 0"
 _TRAFFIC_ARGS = "--only gemm,quant,f32,copy --steps 3 --warmup 1 --no-cpu --warm-ms 0"
 PROFILE_RUNS = {
-    "trace": ("--kernel-trace --stats", "--no-cpu"),
+    "trace": ("--kernel-trace --stats", "--no-cpu --warm-ms 10"),
     "fetch": ("--pmc FETCH_SIZE", _TRAFFIC_ARGS),
     "write": ("--pmc WRITE_SIZE", _TRAFFIC_ARGS),
     "gemm_p1": ("--pmc SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_VALU_MFMA_BUSY_CYCLES SQ_WAIT_ANY SQ_WAIT_INST_ANY "
@@ -662,7 +664,8 @@ def _summarize_traffic(root, traffic):
     c5 = []
     for M, K, N in C5_ROWS:
         d5 = _per_dispatch(root, [f"c5_{M}_{K}_{N}_fetch", f"c5_{M}_{K}_{N}_write"])
-        per = _by_kernel({k: v for k, v in d5.items() if not v["kernel"].startswith(("__amd", "stream_read"))})
+        per = _by_kernel({k: v for k, v in d5.items()
+                          if not v["kernel"].startswith(_SETUP_KERNELS + ("stream_read",))})
         f = sum(v.get("FETCH_SIZE", 0.0) for v in per.values())
         w = sum(v.get("WRITE_SIZE", 0.0) for v in per.values())
         if not per or not f:
@@ -694,7 +697,7 @@ def _counter_table(per, cal):
     ff = cal["fetch_factor"] if cal else 2.0
     wf = cal["write_factor"] if cal else 1.0
     cols = [("kernel", None), ("WGs", None), ("dispatches", None), ("us (median)", "{:.1f}"), ("clock MHz", "{:.0f}"),
-            ("MFMA busy", "{:.2f}"), ("VALU issue", "{:.2f}"), ("fetched MB", "{:.1f}"), ("written MB", "{:.1f}"),
+            ("MFMA busy", "{:.2f}"), ("MFMA busy at that clock", "{:.2f}"), ("VALU issue", "{:.2f}"), ("fetched MB", "{:.1f}"), ("written MB", "{:.1f}"),
             ("L1->L2 reads", "{:.0f}"), ("L1->L2 latency (cycles)", "{:.0f}"), ("L2 hit", "{:.2f}"),
             ("L1 pending-stall share", "{:.2f}"), ("TD busy share", "{:.2f}"), ("LDS-DMA wave loads", "{:.3g}"),
             ("LDS bank-conflict cycles", "{:.3g}")]
@@ -710,6 +713,8 @@ def _counter_table(per, cal):
             r["clock MHz"] = v["GRBM_COUNT"] / 8 / (us * 1e-6) / 1e6
         if "SQ_VALU_MFMA_BUSY_CYCLES" in v:
             r["MFMA busy"] = v["SQ_VALU_MFMA_BUSY_CYCLES"] / 1024 / cyc
+            if "clock MHz" in r:
+                r["MFMA busy at that clock"] = v["SQ_VALU_MFMA_BUSY_CYCLES"] / 1024 / (us * r["clock MHz"])
         if "SQ_INSTS_VALU" in v:
             r["VALU issue"] = (v["SQ_INSTS_VALU"] - v.get("SQ_INSTS_MFMA", 0.0)) * 4 / 1024 / cyc
         if "FETCH_SIZE" in v:
@@ -738,9 +743,10 @@ def _counter_table(per, cal):
 
 _COUNTER_NOTE = ("Per dispatch, averaged over the runs.  us: median duration under the counter runs.  clock (launches "
                  "of 100 us or more): SQ_CYCLES / 32 shader engines, or GRBM_COUNT / 8 XCDs, over the duration.  MFMA "
-                 "busy: SQ_VALU_MFMA_BUSY_CYCLES / 1024 SIMDs / (duration x 2.4 GHz); VALU issue: (SQ_INSTS_VALU - "
-                 "SQ_INSTS_MFMA) x 4 cycles / 1024 / (duration x 2.4 GHz); the L1 pending-stall and TD busy shares "
-                 "are per CU over the same cycles -- all against the peak clock, so lower bounds.  Bytes: FETCH_SIZE "
+                 "busy: SQ_VALU_MFMA_BUSY_CYCLES / 1024 SIMDs / (duration x 2.4 GHz), and the same over the "
+                 "measured clock's cycles where there is one; VALU issue: (SQ_INSTS_VALU - SQ_INSTS_MFMA) x 4 cycles "
+                 "/ 1024 / (duration x 2.4 GHz); the L1 pending-stall and TD busy shares are per CU over the same "
+                 "cycles -- all but the second against the peak clock, so lower bounds.  Bytes: FETCH_SIZE "
                  "and WRITE_SIZE scaled by the 1 GiB copy calibration (`hbm_traffic_mi355x.md`).  L1->L2 reads: "
                  "TCP_TCC_READ_REQ_sum (requests of up to 128 B).\n\n")
 
