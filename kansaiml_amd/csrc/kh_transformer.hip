@@ -255,6 +255,119 @@ __device__ __forceinline__ unsigned layernorm_rows_vec(const float* __restrict__
     return mx;
 }
 
+// Reductions over each half-wave (lanes 0-31 and 32-63) that leave the result
+// in every lane of the half, without the LDS: within each 16-lane row, DPP
+// rotations by 8, 4, 2 and 1 (after them every lane holds its row's total,
+// bit for bit the same in every lane, as each step adds two copies of the
+// same partial tree); then the two rows of a half exchanged by
+// v_permlane16_swap (rows 0, 1, 2, 3 -> 0, 0, 2, 2 and 1, 1, 3, 3).
+template <int CTRL>
+__device__ __forceinline__ unsigned dpp_u32(unsigned v) {
+    return (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float half_sum(float v) {
+    v += __uint_as_float(dpp_u32<0x128>(__float_as_uint(v)));  // row_ror:8
+    v += __uint_as_float(dpp_u32<0x124>(__float_as_uint(v)));  // row_ror:4
+    v += __uint_as_float(dpp_u32<0x122>(__float_as_uint(v)));  // row_ror:2
+    v += __uint_as_float(dpp_u32<0x121>(__float_as_uint(v)));  // row_ror:1
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ unsigned half_max(unsigned v) {
+    v = max(v, dpp_u32<0x128>(v));
+    v = max(v, dpp_u32<0x124>(v));
+    v = max(v, dpp_u32<0x122>(v));
+    v = max(v, dpp_u32<0x121>(v));
+    const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return max((unsigned)p[0], (unsigned)p[1]);
+}
+
+// The LayerNorm of kLnRowsPerWave consecutive rows by one wave, two rows at a
+// time (D == 128 * KH, 16-byte aligned rows): lanes 0-31 hold row 2p and
+// lanes 32-63 row 2p + 1 of pair p, KH float4 each, so every lane carries
+// data in every instruction and a row's mean, variance and 1 / sqrt(var +
+// eps) are computed once per pair; the reductions stay in the VALU
+// (half_sum).  Otherwise as layernorm_rows_vec: all loads before any
+// arithmetic, the centred values multiplied by the correctly rounded
+// 1 / sqrt(var + eps), rows >= `rows` computed on zeros and not stored.
+template <int KH, int MODE>
+__device__ __forceinline__ unsigned layernorm_rows_half(const float* __restrict__ x, int64_t row0, int64_t rows,
+                                                        int D, const float* __restrict__ w,
+                                                        const float* __restrict__ b, float eps,
+                                                        float* __restrict__ out, int8_t* __restrict__ q,
+                                                        const kh::quant::Scale& sc, double* __restrict__ rscales,
+                                                        unsigned* __restrict__ fault, int lane) {
+    using namespace kh::quant;
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    constexpr int P = kLnRowsPerWave / 2;
+    const int half = lane >> 5, hl = lane & 31;
+    f4 v[P][KH];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const int64_t row = row0 + 2 * p + half;
+#pragma unroll
+        for (int i = 0; i < KH; ++i)
+            v[p][i] = row < rows ? reinterpret_cast<const f4*>(x + row * D)[hl + 32 * i] : f4{0.f, 0.f, 0.f, 0.f};
+    }
+    f4 wv[KH], bv[KH];
+#pragma unroll
+    for (int i = 0; i < KH; ++i) {
+        wv[i] = reinterpret_cast<const f4*>(w)[hl + 32 * i];
+        bv[i] = reinterpret_cast<const f4*>(b)[hl + 32 * i];
+    }
+    float mean[P], inv[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < KH; ++i) s += (v[p][i].x + v[p][i].y) + (v[p][i].z + v[p][i].w);
+        mean[p] = half_sum(s) / (float)D;
+    }
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < KH; ++i) {
+            v[p][i] -= mean[p];
+            ss += (v[p][i].x * v[p][i].x + v[p][i].y * v[p][i].y) + (v[p][i].z * v[p][i].z + v[p][i].w * v[p][i].w);
+        }
+        inv[p] = 1.0f / sqrtf(half_sum(ss) / (float)D + eps);
+    }
+    unsigned mx = 0;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const int64_t row = row0 + 2 * p + half;
+        unsigned rm = 0;
+#pragma unroll
+        for (int i = 0; i < KH; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[p][i][e] = v[p][i][e] * inv[p] * wv[i][e] + bv[i][e];
+                rm = max(rm, kh::abs_bits32(v[p][i][e]));
+            }
+        if constexpr (MODE == kLnRowQuant) {
+            // The row's own scale (quantize.py:67-69 applied to the row).
+            const Scale rs = make_scale(half_max(rm));
+            if (row >= rows) continue;
+            if (hl == 0) {
+                rscales[row] = rs.s;
+                if (rs.bad) flag_nonfinite(fault);
+            }
+#pragma unroll
+            for (int i = 0; i < KH; ++i) reinterpret_cast<unsigned*>(q + row * D)[hl + 32 * i] = pack4(v[p][i], rs);
+        } else {
+            if (row >= rows) continue;
+            mx = max(mx, rm);
+#pragma unroll
+            for (int i = 0; i < KH; ++i) {
+                if (MODE == kOutStore) reinterpret_cast<f4*>(out + row * D)[hl + 32 * i] = v[p][i];
+                if (MODE == kOutQuant) reinterpret_cast<unsigned*>(q + row * D)[hl + 32 * i] = pack4(v[p][i], sc);
+            }
+        }
+    }
+    return mx;
+}
+
 // A 256-thread workgroup normalizes kLnRowsPerBlock rows, each wave one row
 // at a time, and (when parts is given) writes the max |out| of its rows.
 // MODE kOutQuant first reduces the pass-1 partials qparts[0..nqparts) to the
@@ -262,8 +375,9 @@ __device__ __forceinline__ unsigned layernorm_rows_vec(const float* __restrict__
 constexpr int kLnRowsPerBlock = 16;
 
 // KV: 0 for the scalar path, else float4 columns per lane of the vectorized
-// path (2 for D <= 512, 4 for D <= 1024).
-template <int KV, int MODE>
+// path (2 for D <= 512, 4 for D <= 1024); HALF: the two-rows-per-wave path
+// with KV float4 per lane (D == 128 * KV).
+template <int KV, int MODE, bool HALF = false>
 __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict__ x, int64_t rows, int D,
                                                         const float* __restrict__ w, const float* __restrict__ b,
                                                         float eps, float* __restrict__ out,
@@ -285,7 +399,10 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict_
     if constexpr (KV > 0) {
         static_assert(kLnRowsPerBlock == 4 * kLnRowsPerWave, "four waves");
         const int64_t row0 = (int64_t)blockIdx.x * kLnRowsPerBlock + (threadIdx.x >> 6) * kLnRowsPerWave;
-        mx = layernorm_rows_vec<KV, MODE>(x, row0, rows, D, w, b, eps, out, q, sc, qscale, fault, lane);
+        if constexpr (HALF)
+            mx = layernorm_rows_half<KV, MODE>(x, row0, rows, D, w, b, eps, out, q, sc, qscale, fault, lane);
+        else
+            mx = layernorm_rows_vec<KV, MODE>(x, row0, rows, D, w, b, eps, out, q, sc, qscale, fault, lane);
     } else {
         static_assert(MODE != kLnRowQuant, "per-row codes: vectorized path only");
 #pragma unroll 1
@@ -375,8 +492,45 @@ __device__ __forceinline__ void attention_tile_dma(__amdgpu_buffer_rsrc_t r, flo
                             voff + 16 * i * row_bytes, 0);
 }
 
+// S^T = K Q^T for key subtiles t < NT of the tile in `ks` (st[t][r] = score of
+// key 16t + 4g + r); subtiles t >= NT are left as they are.
+template <int NT>
+__device__ __forceinline__ void attention_scores(const float* ks, const float (&qf)[16], int li, int g,
+                                                 f32x4v (&st)[4]) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        f32x4v kv[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+            kv[t] = *reinterpret_cast<const f32x4v*>(&ks[(16 * t + li) * kDk + 4 * ((4 * g + c) ^ li)]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+                st[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[t][e], qf[4 * c + e], st[t], 0, 0, 0);
+    }
+}
+
+// O^T += V^T P^T over key subtiles t < NT of the tile in `vs`: product j,
+// A = V^T (d 4 li + j, key 16t + 4g + r), B = P^T (in registers).
+template <int NT>
+__device__ __forceinline__ void attention_pv(const float* vs, const f32x4v (&st)[4], int li, int g, f32x4v (&o)[4]) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        f32x4v va[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            va[r] = *reinterpret_cast<const f32x4v*>(&vs[(16 * t + 4 * g + r) * kDk + 4 * (li ^ (4 * g + r))]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(va[r][j], st[t][r], o[j], 0, 0, 0);
+    }
+}
+
 template <bool CAUSAL>
-__global__ __launch_bounds__(256) void attention_mfma_kernel(const float* __restrict__ qkv, int B, int T, int H,
+__global__ __launch_bounds__(256, 3) void attention_mfma_kernel(const float* __restrict__ qkv, int B, int T, int H,
                                                              float* __restrict__ out, unsigned* __restrict__ parts) {
     __shared__ __attribute__((aligned(1024))) float ks[kAttK * kDk];
     __shared__ __attribute__((aligned(1024))) float vs[kAttK * kDk];
@@ -421,8 +575,16 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(const float* __rest
 
     // Causal: key tiles through the workgroup's last query; otherwise all of them.
     const int tiles = ((CAUSAL ? min(T, (qb + 1) * kAttQ) : T) - 1) / kAttK + 1;
+    // The last key any of this wave's queries attends to.  Key subtiles
+    // beyond it (the diagonal tile's upper subtiles, keys past T) hold only
+    // masked scores, whose probabilities are exactly 0: their products are
+    // skipped (the same results: the mask below still covers their scores).
+    const int last_key = __builtin_amdgcn_readfirstlane(CAUSAL ? min(q0 + 15, T - 1) : T - 1);
     for (int it = 0; it < tiles; ++it) {
         const int k0 = it * kAttK;
+        // Key subtiles with a key <= last_key: 1..4 (k0 <= last_key for
+        // every tile the loop visits).
+        const int nt = min(4, (last_key - k0) / 16 + 1);
         // K(it) has landed for every wave, and every wave is done with V(it-1).
         __builtin_amdgcn_s_waitcnt(wait_imm(0, 15));
         __syncthreads();
@@ -432,18 +594,10 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(const float* __rest
         f32x4v st[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) st[t] = f32x4v{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            f32x4v kv[4];
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-                kv[t] = *reinterpret_cast<const f32x4v*>(&ks[(16 * t + li) * kDk + 4 * ((4 * g + c) ^ li)]);
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-#pragma unroll
-                for (int t = 0; t < 4; ++t)
-                    st[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[t][e], qf[4 * c + e], st[t], 0, 0, 0);
-        }
+        if (nt == 4) attention_scores<4>(ks, qf, li, g, st);
+        else if (nt == 3) attention_scores<3>(ks, qf, li, g, st);
+        else if (nt == 2) attention_scores<2>(ks, qf, li, g, st);
+        else attention_scores<1>(ks, qf, li, g, st);
         // Causal mask (key > query) and keys past T -- only where the tile
         // reaches this wave's diagonal or the sequence end.
         if (!((!CAUSAL || k0 + kAttK - 1 <= q0) && k0 + kAttK <= T)) {
@@ -483,19 +637,11 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(const float* __rest
         __syncthreads();
         if (it + 1 < tiles) attention_tile_dma(rsrc, ks, k0 + kAttK, row_bytes, kcol, wave, lane);
 
-        // O^T += V^T P^T: product j, A = V^T (d 4 li + j, key 16t + 4g + r), B = P^T (in registers).
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            f32x4v va[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                va[r] = *reinterpret_cast<const f32x4v*>(&vs[(16 * t + 4 * g + r) * kDk + 4 * (li ^ (4 * g + r))]);
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(va[r][j], st[t][r], o[j], 0, 0, 0);
-        }
+        // O^T += V^T P^T.
+        if (nt == 4) attention_pv<4>(vs, st, li, g, o);
+        else if (nt == 3) attention_pv<3>(vs, st, li, g, o);
+        else if (nt == 2) attention_pv<2>(vs, st, li, g, o);
+        else attention_pv<1>(vs, st, li, g, o);
     }
     unsigned mxo = 0;
     if (q < T) {
@@ -514,6 +660,35 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(const float* __rest
         __shared__ unsigned wmax[4];
         mxo = block4_max(mxo, wmax);
         if (tid == 0) parts[blockIdx.x] = mxo;
+    }
+}
+
+// Launches the LayerNorm kernel in the layout the row length takes: two rows
+// per wave for D = 128, 256, 384 or 512 (16-byte aligned), one row per wave
+// otherwise (float4 columns where aligned, scalar for the rest).  Every mode
+// of one D takes the same layout, so a fused pass computes exactly the values
+// the plain LayerNorm stores.
+template <int MODE>
+void launch_layernorm(kh::Device* d, bool vec, int64_t blocks, const float* x, int64_t rows, int D, const float* w,
+                      const float* b, float eps, float* out, unsigned* parts, int8_t* q, const unsigned* qparts,
+                      int nqparts, double* qscale) {
+    auto go = [&](auto kv, auto half) {
+        layernorm_kernel<decltype(kv)::value, MODE, decltype(half)::value><<<(unsigned)blocks, 256, 0, d->stream>>>(
+            x, rows, D, w, b, eps, out, parts, q, qparts, nqparts, qscale, d->fault);
+    };
+    using yes = std::true_type;
+    using no = std::false_type;
+    if (vec && D % 128 == 0 && D <= 512) {
+        if (D == 128) go(std::integral_constant<int, 1>{}, yes{});
+        else if (D == 256) go(std::integral_constant<int, 2>{}, yes{});
+        else if (D == 384) go(std::integral_constant<int, 3>{}, yes{});
+        else go(std::integral_constant<int, 4>{}, yes{});
+    } else if (vec && D <= 512) {
+        go(std::integral_constant<int, 2>{}, no{});
+    } else if (vec) {
+        go(std::integral_constant<int, 4>{}, no{});
+    } else if constexpr (MODE != kLnRowQuant) {
+        go(std::integral_constant<int, 0>{}, no{});
     }
 }
 
@@ -554,15 +729,8 @@ int kh_layernorm_ex(const float* x, int64_t rows, int D, const float* weight, co
                      kh::aligned(bias, 16);
     using kh::quant::kOutStore;
     unsigned* parts = fused ? absmax_parts : nullptr;
-    if (vec && D <= 512)
-        layernorm_kernel<2, kOutStore><<<(unsigned)blocks, 256, 0, d->stream>>>(
-            x, rows, D, weight, bias, eps, out, parts, nullptr, nullptr, 0, nullptr, d->fault);
-    else if (vec)
-        layernorm_kernel<4, kOutStore><<<(unsigned)blocks, 256, 0, d->stream>>>(
-            x, rows, D, weight, bias, eps, out, parts, nullptr, nullptr, 0, nullptr, d->fault);
-    else
-        layernorm_kernel<0, kOutStore><<<(unsigned)blocks, 256, 0, d->stream>>>(
-            x, rows, D, weight, bias, eps, out, parts, nullptr, nullptr, 0, nullptr, d->fault);
+    launch_layernorm<kOutStore>(d, vec, blocks, x, rows, D, weight, bias, eps, out, parts, nullptr, nullptr, 0,
+                                nullptr);
     int rc = kh::launch_status("layernorm");
     if (rc || !absmax_parts) return rc;
     if (fused) {
@@ -599,16 +767,10 @@ int kh_layernorm_quant(const float* x, int64_t rows, int D, const float* weight,
     // Pass 1 reduces the normalized values' absmax into one partial per
     // workgroup without storing them; pass 2 recomputes them (the same
     // arithmetic, so the same values) and stores their codes.
-    auto passes = [&](auto kv) {
-        constexpr int KV = decltype(kv)::value;
-        layernorm_kernel<KV, kOutMaxOnly><<<(unsigned)blocks, 256, 0, d->stream>>>(
-            x, rows, D, weight, bias, eps, nullptr, parts, nullptr, nullptr, 0, nullptr, d->fault);
-        layernorm_kernel<KV, kOutQuant><<<(unsigned)blocks, 256, 0, d->stream>>>(
-            x, rows, D, weight, bias, eps, nullptr, nullptr, q, parts, (int)blocks, scale, d->fault);
-    };
-    if (vec && D <= 512) passes(std::integral_constant<int, 2>{});
-    else if (vec) passes(std::integral_constant<int, 4>{});
-    else passes(std::integral_constant<int, 0>{});
+    launch_layernorm<kOutMaxOnly>(d, vec, blocks, x, rows, D, weight, bias, eps, nullptr, parts, nullptr, nullptr, 0,
+                                  nullptr);
+    launch_layernorm<kOutQuant>(d, vec, blocks, x, rows, D, weight, bias, eps, nullptr, nullptr, q, parts,
+                                (int)blocks, scale);
     return kh::launch_status("layernorm_quant");
 }
 
@@ -634,12 +796,8 @@ int kh_layernorm_quant_rows(const float* x, int64_t rows, int D, const float* we
         const int frc = kh_free(tmp);
         return rc ? rc : frc;
     }
-    if (D <= 512)
-        layernorm_kernel<2, kLnRowQuant><<<(unsigned)blocks, 256, 0, d->stream>>>(
-            x, rows, D, weight, bias, eps, nullptr, nullptr, q, nullptr, 0, scales, d->fault);
-    else
-        layernorm_kernel<4, kLnRowQuant><<<(unsigned)blocks, 256, 0, d->stream>>>(
-            x, rows, D, weight, bias, eps, nullptr, nullptr, q, nullptr, 0, scales, d->fault);
+    launch_layernorm<kLnRowQuant>(d, vec, blocks, x, rows, D, weight, bias, eps, nullptr, nullptr, q, nullptr, 0,
+                                  scales);
     return kh::launch_status("layernorm_quant_rows");
 }
 
