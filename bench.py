@@ -106,6 +106,43 @@ def time_kernel(fn, steps, warmup, tag=None, min_warm_ms=None):
     return e0.elapsed_ms(e1) / steps
 
 
+def time_graph(call, steps, reps=15):
+    """Microseconds per call of `steps` dependent calls of call() recorded
+    once as a HIP graph on the library stream (kh_graph_*), the median over
+    `reps` replays, each between its own HIP events.  Unlike a Python loop
+    issuing the calls, the replay never waits for the host: for kernels of a
+    few microseconds the per-call cost of issuing them from Python (a ctypes
+    call and a launch) is as large as the kernel, and a host-side pause
+    inside a short timed loop shows up in the average.  call() must have run
+    before (scratch sized, pool warm) and must not synchronize."""
+    import ctypes
+    from kansaiml_amd import _native as N
+    N.synchronize()
+    N.call("kh_graph_capture_begin")
+    try:
+        for _ in range(steps):
+            call()
+    except BaseException:
+        N.lib().kh_graph_capture_end(None)
+        raise
+    g = ctypes.c_void_p()
+    N.call("kh_graph_capture_end", ctypes.byref(g))
+    try:
+        e0, e1 = N.Event(), N.Event()
+        N.call("kh_graph_launch", g)  # first replay: uploads the graph
+        N.synchronize()
+        times = []
+        for _ in range(reps):
+            e0.record()
+            N.call("kh_graph_launch", g)
+            e1.record()
+            N.synchronize()
+            times.append(e0.elapsed_ms(e1))
+    finally:
+        N.call("kh_graph_destroy", g)
+    return float(np.median(times)) / steps * 1e3
+
+
 def measured_traffic(kernel_key):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary
     (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration), or None."""
@@ -199,9 +236,11 @@ def bench_skinny(steps, warmup, rows=None):
     {1, 8, 32}, (K, N) in {(4096, 4096), (4096, 11008)}.  Copies of the
     quantized weight are rotated so more than 512 MB of distinct weights pass
     through HBM (beyond the 256 MB Infinity Cache).  `us` is the average over
-    `steps` calls issued back to back between one pair of HIP events (a
-    decode loop's dependent layer calls); `us_single` brackets each call with
-    its own events (launch latency included, host gaps excluded)."""
+    `steps` dependent calls back to back (a decode loop's layer calls),
+    recorded as a HIP graph and replayed (time_graph); `us_stream` is the
+    same calls issued one by one from Python between one pair of HIP events;
+    `us_single` brackets each call with its own events (launch latency
+    included, host gaps excluded)."""
     from kansaiml_amd import _native as Nn
     from kansaiml_amd.device import DeviceTensor as D
     gen = np.random.Generator(np.random.PCG64(6))
@@ -241,7 +280,8 @@ def bench_skinny(steps, warmup, rows=None):
                 call()
             e1.record()
             Nn.synchronize()
-            us = e0.elapsed_ms(e1) / steps * 1e3
+            us_stream = e0.elapsed_ms(e1) / steps * 1e3
+            us = time_graph(call, steps)
             evs = [(Nn.Event(), Nn.Event()) for _ in range(steps)]
             for a, b in evs:
                 a.record()
@@ -252,13 +292,15 @@ def bench_skinny(steps, warmup, rows=None):
             nbytes = N * K + 8 * N + 4 * M * K + 2 * M * K + 4 * M * N
             gbs = nbytes / (us * 1e-6) / 1e9
             key = f"c5_M{M}_K{K}_N{N}"
-            out_rows.append({"M": M, "K": K, "N": N, "us": round(us, 2), "us_single": round(us_single, 2),
+            out_rows.append({"M": M, "K": K, "N": N, "us": round(us, 2), "us_stream": round(us_stream, 2),
+                             "us_single": round(us_single, 2),
                              "GB/s": round(gbs, 1), "TOPS": round(2.0 * M * N * K / (us * 1e-6) / 1e12, 2),
                              "path": "fused decode kernel" if M <= 2 else "quantize_rows + skinny GEMM",
                              "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                                           "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
                                           "traffic": measured_traffic(key), "traffic_key": key}})
-            log(f"skinny M={M} K={K} N={N}: {us:.2f} us back-to-back ({gbs:.0f} GB/s), {us_single:.2f} us single")
+            log(f"skinny M={M} K={K} N={N}: {us:.2f} us back-to-back ({gbs:.0f} GB/s; {us_stream:.2f} us issued "
+                f"from Python), {us_single:.2f} us single")
         # The practical ceiling for these rows: a plain streaming read of the
         # same weight bytes (kh_probe_stream_read), rotated and issued back
         # to back the same way.
@@ -272,13 +314,7 @@ def bench_skinny(steps, warmup, rows=None):
             i_read[0] += 1
 
         warm_up(read, max(3, warmup), tag=f"c5_read_N{N}")
-        e0, e1 = Nn.Event(), Nn.Event()
-        e0.record()
-        for _ in range(steps):
-            read()
-        e1.record()
-        Nn.synchronize()
-        read_us = e0.elapsed_ms(e1) / steps * 1e3
+        read_us = time_graph(read, steps)
         read_gbs = N * K / (read_us * 1e-6) / 1e9
         for r in out_rows:
             if r["K"] == K and r["N"] == N:
@@ -311,10 +347,11 @@ def bench_c1(steps, warmup):
     """Config C1, the reference's CPU-runnable case: an int8 quantized Linear,
     x fp32 [64, 512] ~N(0,1), W fp32 [512, 512] ~N(0, 0.02), bias zeros,
     per-tensor scales for x and W (seed 0; W quantized once at construction).
-    Latency-bound, so reported as microseconds per call two ways: the two
-    kernels back to back (one-launch per-tensor quantize of x; the skinny
-    int8 GEMM with the dequantize and bias fused) and the eager QLinear call
-    (Python dispatch and output allocation included)."""
+    Latency-bound, so reported as microseconds per call: the two kernels
+    back to back (one-launch per-tensor quantize of x; the skinny int8 GEMM
+    with the dequantize and bias fused), replayed as a HIP graph
+    (time_graph) and issued from Python (`us_kernels_stream`), and the eager
+    QLinear call (Python dispatch and output allocation included)."""
     from kansaiml_amd import _native as Nn
     from kansaiml_amd.device import DeviceTensor as D
     from kansaiml_amd.quantize import QLinear
@@ -335,11 +372,13 @@ def bench_c1(steps, warmup):
     Nn.call("kh_quantize_tensor", *qargs)  # checked once; the timed calls skip the status check
     Nn.call("kh_gemm_i8", *gargs)
 
-    us_kernels = time_kernel(kernels, steps, warmup, tag="c1_kernels") * 1e3
+    us_stream = time_kernel(kernels, steps, warmup, tag="c1_kernels") * 1e3
+    us_kernels = time_graph(kernels, steps)
     us_eager = time_kernel(lambda: layer(xd), steps, warmup, tag="c1_eager") * 1e3
     ops = 2 * 64 * 512 * 512
     return {"workload": "C1 int8 quantized Linear x[64,512] @ W[512,512] + b, per-tensor scales (seed 0)",
-            "us_kernels_back_to_back": round(us_kernels, 2), "us_eager_call": round(us_eager, 2), "ops": ops,
+            "us_kernels_back_to_back": round(us_kernels, 2), "us_kernels_stream": round(us_stream, 2),
+            "us_eager_call": round(us_eager, 2), "ops": ops,
             "TOPS_kernels": round(ops / (us_kernels * 1e-6) / 1e12, 3), "bound": "latency"}
 
 
@@ -1078,8 +1117,8 @@ def main():
     if "c1" in only:
         log("C1 int8 quantized Linear ...")
         c1 = bench_c1(max(50, args.steps), args.warmup)
-        log(f"C1: {c1['us_kernels_back_to_back']:.2f} us per call (kernels back to back), "
-            f"{c1['us_eager_call']:.2f} us eager")
+        log(f"C1: {c1['us_kernels_back_to_back']:.2f} us per call (kernels back to back as a graph; "
+            f"{c1['us_kernels_stream']:.2f} us issued from Python), {c1['us_eager_call']:.2f} us eager")
     skinny = None
     if "skinny" in only:
         log("skinny decode GEMMs C5 ...")

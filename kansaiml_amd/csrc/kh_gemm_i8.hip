@@ -969,15 +969,12 @@ __global__ __launch_bounds__(512) void linear_i8_decode_kernel(const float* __re
 #pragma unroll
             for (int e = 0; e < 4; ++e) p[m][i] = __builtin_amdgcn_sdot4(a[m][e], b[i][e], p[m][i], false);
         }
-    // Wave sums of all S * MAXM partials in lockstep: each shuffle round is
-    // S * MAXM independent exchanges and one wait, not S * MAXM dependent
-    // chains one after another.
+    // Wave sums of all S * MAXM partials, in the VALU (independent chains
+    // the compiler interleaves; int32 sums are exact in any order).
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1)
+    for (int m = 0; m < MAXM; ++m)
 #pragma unroll
-        for (int m = 0; m < MAXM; ++m)
-#pragma unroll
-            for (int i = 0; i < S; ++i) p[m][i] += __shfl_xor(p[m][i], off, 64);
+        for (int i = 0; i < S; ++i) p[m][i] = kh::lanes::wave_sum(p[m][i]);
     if (lane == 0) {
 #pragma unroll
         for (int m = 0; m < MAXM; ++m)

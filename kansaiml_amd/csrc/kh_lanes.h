@@ -1,0 +1,83 @@
+// kh_lanes.h -- reductions across the lanes of a wave that stay in the VALU.
+// Internal header.
+//
+// __shfl_xor compiles to ds_bpermute_b32 on gfx950: every step of a reduction
+// is then an LDS round trip that the next step waits for.  These reductions
+// use DPP row rotations within each 16-lane row, then the gfx950 lane swaps
+// between rows: v_permlane16_swap (rows 0,1,2,3 of two copies -> 0,0,2,2 and
+// 1,1,3,3) and v_permlane32_swap (halves lo,hi -> lo,lo and hi,hi).  After a
+// rotation by 8, 4, 2 and 1 every lane of a row holds the row's total, bit
+// for bit the same in every lane (each step adds two copies of the same
+// partial tree), so float sums are the same in every lane too.
+//
+// Every lane of the wave must be active (the callers reduce in uniform
+// control flow, before any per-lane branch or early return).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <type_traits>
+
+namespace kh {
+namespace lanes {
+
+// Lane i of each 16-lane row reads lane (i - n) mod 16 of its row (DPP
+// row_ror:n, n = 1..15).
+template <int N>
+__device__ __forceinline__ unsigned row_ror(unsigned v) {
+    static_assert(N >= 1 && N <= 15, "row_ror");
+    return (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x120 + N, 0xF, 0xF, false);
+}
+
+// Op over the 16 lanes of each row, in every lane of the row.
+template <typename T, typename Op>
+__device__ __forceinline__ T row16_reduce(T v, Op op) {
+    auto rot = [](T x, auto n) {
+        return __builtin_bit_cast(T, row_ror<decltype(n)::value>(__builtin_bit_cast(unsigned, x)));
+    };
+    v = op(v, rot(v, std::integral_constant<int, 8>{}));
+    v = op(v, rot(v, std::integral_constant<int, 4>{}));
+    v = op(v, rot(v, std::integral_constant<int, 2>{}));
+    v = op(v, rot(v, std::integral_constant<int, 1>{}));
+    return v;
+}
+
+// Combines rows 0 with 1 and 2 with 3.
+template <typename T, typename Op>
+__device__ __forceinline__ T swap16(T v, Op op) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
+                                                    false, false);
+    return op(__builtin_bit_cast(T, (unsigned)p[0]), __builtin_bit_cast(T, (unsigned)p[1]));
+}
+
+// Combines lanes 0-31 with 32-63.
+template <typename T, typename Op>
+__device__ __forceinline__ T swap32(T v, Op op) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v), __builtin_bit_cast(unsigned, v),
+                                                    false, false);
+    return op(__builtin_bit_cast(T, (unsigned)p[0]), __builtin_bit_cast(T, (unsigned)p[1]));
+}
+
+struct MaxU {
+    __device__ unsigned operator()(unsigned a, unsigned b) const { return a > b ? a : b; }
+};
+struct AddI {
+    __device__ int operator()(int a, int b) const { return a + b; }
+};
+struct AddF {
+    __device__ float operator()(float a, float b) const { return a + b; }
+};
+
+// Over each half-wave (lanes 0-31 and 32-63), in every lane of the half.
+__device__ __forceinline__ float half_sum(float v) { return swap16(row16_reduce(v, AddF{}), AddF{}); }
+__device__ __forceinline__ unsigned half_max(unsigned v) { return swap16(row16_reduce(v, MaxU{}), MaxU{}); }
+
+// Over the whole wave, in every lane.
+__device__ __forceinline__ float wave_sum(float v) { return swap32(half_sum(v), AddF{}); }
+__device__ __forceinline__ unsigned wave_max(unsigned v) { return swap32(half_max(v), MaxU{}); }
+__device__ __forceinline__ int wave_sum(int v) {
+    return swap32(swap16(row16_reduce(v, AddI{}), AddI{}), AddI{});
+}
+
+}  // namespace lanes
+}  // namespace kh

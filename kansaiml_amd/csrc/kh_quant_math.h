@@ -11,6 +11,7 @@
 #include <hip/hip_runtime.h>
 
 #include "kh_common.h"
+#include "kh_lanes.h"
 
 #pragma clang fp contract(off)
 
@@ -54,11 +55,8 @@ struct AbsMax {
     __device__ __forceinline__ unsigned bits() const { return max(umax & 0x7FFFFFFFu, (unsigned)max(smax, 0)); }
 };
 
-__device__ __forceinline__ unsigned wave_max(unsigned v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = max(v, (unsigned)__shfl_xor((int)v, off, 64));
-    return v;
-}
+// Max over the wave, in every lane (whole wave active).
+__device__ __forceinline__ unsigned wave_max(unsigned v) { return kh::lanes::wave_max(v); }
 
 struct Scale {
     double s;    // the reference's binary64 scale

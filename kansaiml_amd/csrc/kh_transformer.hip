@@ -75,18 +75,13 @@ __global__ __launch_bounds__(256) void embedding4_kernel(const int32_t* __restri
 // ---------------------------------------------------------------------------
 // LayerNorm: one wave per row; the row lives in registers (D <= 64 * 16).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
+__device__ __forceinline__ float wave_sum(float v) { return kh::lanes::wave_sum(v); }
 
 constexpr int kLnMaxPerLane = 16;
 
 // Max over a 256-thread workgroup (4 waves); every thread gets the result.
 __device__ __forceinline__ unsigned block4_max(unsigned v, unsigned* wmax) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = max(v, (unsigned)__shfl_xor((int)v, off, 64));
+    v = kh::lanes::wave_max(v);
     if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = v;
     __syncthreads();
     return max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
@@ -255,39 +250,12 @@ __device__ __forceinline__ unsigned layernorm_rows_vec(const float* __restrict__
     return mx;
 }
 
-// Reductions over each half-wave (lanes 0-31 and 32-63) that leave the result
-// in every lane of the half, without the LDS: within each 16-lane row, DPP
-// rotations by 8, 4, 2 and 1 (after them every lane holds its row's total,
-// bit for bit the same in every lane, as each step adds two copies of the
-// same partial tree); then the two rows of a half exchanged by
-// v_permlane16_swap (rows 0, 1, 2, 3 -> 0, 0, 2, 2 and 1, 1, 3, 3).
-template <int CTRL>
-__device__ __forceinline__ unsigned dpp_u32(unsigned v) {
-    return (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
-}
-__device__ __forceinline__ float half_sum(float v) {
-    v += __uint_as_float(dpp_u32<0x128>(__float_as_uint(v)));  // row_ror:8
-    v += __uint_as_float(dpp_u32<0x124>(__float_as_uint(v)));  // row_ror:4
-    v += __uint_as_float(dpp_u32<0x122>(__float_as_uint(v)));  // row_ror:2
-    v += __uint_as_float(dpp_u32<0x121>(__float_as_uint(v)));  // row_ror:1
-    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
-}
-__device__ __forceinline__ unsigned half_max(unsigned v) {
-    v = max(v, dpp_u32<0x128>(v));
-    v = max(v, dpp_u32<0x124>(v));
-    v = max(v, dpp_u32<0x122>(v));
-    v = max(v, dpp_u32<0x121>(v));
-    const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-    return max((unsigned)p[0], (unsigned)p[1]);
-}
-
 // The LayerNorm of kLnRowsPerWave consecutive rows by one wave, two rows at a
 // time (D == 128 * KH, 16-byte aligned rows): lanes 0-31 hold row 2p and
 // lanes 32-63 row 2p + 1 of pair p, KH float4 each, so every lane carries
 // data in every instruction and a row's mean, variance and 1 / sqrt(var +
 // eps) are computed once per pair; the reductions stay in the VALU
-// (half_sum).  Otherwise as layernorm_rows_vec: all loads before any
+// (kh::lanes::half_sum).  Otherwise as layernorm_rows_vec: all loads before any
 // arithmetic, the centred values multiplied by the correctly rounded
 // 1 / sqrt(var + eps), rows >= `rows` computed on zeros and not stored.
 template <int KH, int MODE>
@@ -321,7 +289,7 @@ __device__ __forceinline__ unsigned layernorm_rows_half(const float* __restrict_
         float s = 0.0f;
 #pragma unroll
         for (int i = 0; i < KH; ++i) s += (v[p][i].x + v[p][i].y) + (v[p][i].z + v[p][i].w);
-        mean[p] = half_sum(s) / (float)D;
+        mean[p] = kh::lanes::half_sum(s) / (float)D;
     }
 #pragma unroll
     for (int p = 0; p < P; ++p) {
@@ -331,7 +299,7 @@ __device__ __forceinline__ unsigned layernorm_rows_half(const float* __restrict_
             v[p][i] -= mean[p];
             ss += (v[p][i].x * v[p][i].x + v[p][i].y * v[p][i].y) + (v[p][i].z * v[p][i].z + v[p][i].w * v[p][i].w);
         }
-        inv[p] = 1.0f / sqrtf(half_sum(ss) / (float)D + eps);
+        inv[p] = 1.0f / sqrtf(kh::lanes::half_sum(ss) / (float)D + eps);
     }
     unsigned mx = 0;
 #pragma unroll
@@ -347,7 +315,7 @@ __device__ __forceinline__ unsigned layernorm_rows_half(const float* __restrict_
             }
         if constexpr (MODE == kLnRowQuant) {
             // The row's own scale (quantize.py:67-69 applied to the row).
-            const Scale rs = make_scale(half_max(rm));
+            const Scale rs = make_scale(kh::lanes::half_max(rm));
             if (row >= rows) continue;
             if (hl == 0) {
                 rscales[row] = rs.s;
