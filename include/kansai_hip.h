@@ -192,8 +192,8 @@ int kh_gemm_i8(const int8_t* a, const int8_t* b_packed, int64_t M, int64_t N, in
 /* kh_gemm_i8's output with the graph's next elementwise steps fused into
  * the epilogue, in the order the reference applies them:
  *   y = (float)((double)acc * (sa_i * sb_j)) + bias[j];
- *   y = act(y)            act: KH_ACT_NONE or KH_ACT_GELU (exact erf,
- *                         backend/cpu/src/Ops.cpp:250-256);
+ *   y = act(y)            act: KH_ACT_NONE or KH_ACT_GELU (the erf form of
+ *                         backend/cpu/src/Ops.cpp:250-256, to ~1e-7 * max(1, |x|));
  *   out = residual + y    when residual (fp32 [M, N]) is not NULL -- the
  *                         pre-LN block's x.add(linear(..)), nn.py:466-478.
  * absmax_parts (may be NULL): up to max_parts partial maxima of |out| for

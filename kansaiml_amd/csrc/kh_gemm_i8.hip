@@ -68,7 +68,7 @@ __device__ __forceinline__ float epilogue_finish(const Epilogue& ep, int32_t acc
     float y = (float)((double)acc * s);
     if (ep.bias) y = y + bj;
     if (FUSED) {
-        if (ep.act == kActGelu) y = kh::gelu_exact(y);
+        if (ep.act == kActGelu) y = kh::gelu(y);
         if (ep.residual) y = resid + y;
     }
     return y;
@@ -198,7 +198,7 @@ __device__ __forceinline__ unsigned store_block32_full(const Epilogue& ep, int64
     }
     if (FUSED && ep.act == kActGelu) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) y[r] = kh::gelu_exact(y[r]);
+        for (int r = 0; r < 16; ++r) y[r] = kh::gelu(y[r]);
     }
     if (FUSED && ep.residual) {
 #pragma unroll

@@ -1,6 +1,6 @@
 // kh_transformer.hip -- the fp32 pieces of a decoder block around the int8
-// Linear layers (config C4): token + position embedding, LayerNorm, exact-erf
-// GELU, and multi-head attention (causal or unmasked).
+// Linear layers (config C4): token + position embedding, LayerNorm, GELU, and
+// multi-head attention (causal or unmasked).
 //
 // Semantics follow the reference's modules (python/kansai/nn.py):
 //   Embedding      out[r] = tok[id[r]] + pos[r % T]        (nn.py:624-646, the
@@ -387,11 +387,11 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict_
 }
 
 // ---------------------------------------------------------------------------
-// GELU (exact erf).
+// GELU (kh::gelu: the erf form of the reference, evaluated through erfc).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void gelu_kernel(const float* __restrict__ x, float* __restrict__ out, int64_t n) {
     const int64_t stride = (int64_t)gridDim.x * 256;
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) out[i] = kh::gelu_exact(x[i]);
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) out[i] = kh::gelu(x[i]);
 }
 
 // ---------------------------------------------------------------------------

@@ -248,7 +248,7 @@ def quant_fusion(graph, producer_quant: bool | str = False) -> Graph:
     That saves the fp32 intermediate's memory; on MI355X it saves time for
     LayerNorm (two passes over its input cost less than writing the fp32
     values and reading them back) but not for the GEMM, whose VALU-bound
-    epilogue (binary64 dequantize, exact-erf GELU) the second pass repeats.
+    epilogue (binary64 dequantize, GELU) the second pass repeats.
     layer_norm_quant_rows needs no second pass: each row's scale depends on
     that row only, so one pass stores codes and scales.
     Then every int8_linear, layer_norm or attention whose

@@ -36,14 +36,29 @@ def test_layernorm(G, rows, d):
 
 
 def test_gelu(G):
+    """kh_gelu (the GELU the fused GEMM epilogues share) against binary64
+    x * 0.5 * (1 + erf(x / sqrt(2))): within 2e-7 * max(1, |x|) everywhere
+    (the binary32 formula's bound, tests/test_gelu_formula.py, plus the
+    hardware reciprocal's and exp2's ulp), the special values as the
+    reference's binary32 formula gives them."""
     N, D = G
-    x = np.linspace(-8, 8, 100_001, dtype=np.float32)
+    x = np.concatenate([np.linspace(-12, 12, 400_001, dtype=np.float32),
+                        (10.0 ** np.linspace(-30, 30, 2001)).astype(np.float32),
+                        -(10.0 ** np.linspace(-30, 30, 2001)).astype(np.float32),
+                        np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 3e38, -3e38], np.float32)])
     out = D([x.size])
     xd = D.from_host(x)
     N.call("kh_gelu", xd.ptr, out.ptr, x.size)
-    x64 = x.astype(np.float64)
+    got = out.numpy()
+    fin = np.isfinite(x)
+    x64 = x[fin].astype(np.float64)
     ref = x64 * 0.5 * (1 + erf(x64 / np.sqrt(2)))
-    assert np.abs(out.numpy() - ref).max() < 4e-6 * max(1.0, np.abs(ref).max())
+    err = np.abs(got[fin].astype(np.float64) - ref) / np.maximum(1.0, np.abs(x64))
+    assert err.max() < 2e-7, (err.max(), x[fin][np.argmax(err)])
+    sp = got[-7:]
+    assert sp[0] == 0 and not np.signbit(sp[0]) and sp[1] == 0 and np.signbit(sp[1])
+    assert sp[2] == np.inf and np.isnan(sp[3]) and np.isnan(sp[4])  # -inf * 0, as the reference formula
+    assert sp[5] == np.float32(3e38) and sp[6] == 0
 
 
 @pytest.mark.parametrize("d", [48, 50])  # float4 path, scalar path
