@@ -67,6 +67,9 @@ struct AddI {
 struct AddF {
     __device__ float operator()(float a, float b) const { return a + b; }
 };
+struct MaxF {
+    __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
 
 // Over each half-wave (lanes 0-31 and 32-63), in every lane of the half.
 __device__ __forceinline__ float half_sum(float v) { return swap16(row16_reduce(v, AddF{}), AddF{}); }

@@ -424,7 +424,9 @@ __global__ __launch_bounds__(256) void gelu_kernel(const float* __restrict__ x, 
 //   operands for the four products are one 16-byte read of V's row, and lane
 //   l ends up holding d = 16g .. 16g+15 of its query's output.
 // The softmax of a query reduces over its lane's 16 scores and the 4 lanes
-// l % 16 + 16g.  The 1/sqrt(dk) = 1/8 scale is applied to Q (exact).
+// l % 16 + 16g (lane swaps, kh_lanes.h).  Scores are kept in base-2 units:
+// Q is scaled by log2(e) / sqrt(dk) = log2(e) / 8 (one rounding), so the
+// softmax's exponentials are bare v_exp_f32 (2^x).
 //
 // Workgroups are ordered so that the query blocks of one (batch, head) run on
 // one XCD (its L2 holds their shared K and V; workgroup i runs on XCD i % 8)
@@ -433,17 +435,18 @@ __global__ __launch_bounds__(256) void gelu_kernel(const float* __restrict__ x, 
 constexpr int kDk = 64;
 constexpr int kAttQ = 64;  // queries per workgroup (16 per wave)
 constexpr int kAttK = 64;  // keys per LDS tile
+constexpr float kLog2eOver8 = 0.18033688011112042f;  // log2(e) / sqrt(64)
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
-// max / sum over the 4 lanes l % 16 + 16g holding one query's scores.
+// max / sum over the 4 lanes l % 16 + 16g holding one query's scores (the
+// same lane of each 16-lane row: one row swap, one half swap; every one of
+// the 4 lanes gets the same bits).
 __device__ __forceinline__ float query4_max(float v) {
-    v = fmaxf(v, __shfl_xor(v, 16, 64));
-    return fmaxf(v, __shfl_xor(v, 32, 64));
+    return kh::lanes::swap32(kh::lanes::swap16(v, kh::lanes::MaxF{}), kh::lanes::MaxF{});
 }
 __device__ __forceinline__ float query4_sum(float v) {
-    v += __shfl_xor(v, 16, 64);
-    return v + __shfl_xor(v, 32, 64);
+    return kh::lanes::swap32(kh::lanes::swap16(v, kh::lanes::AddF{}), kh::lanes::AddF{});
 }
 
 // One 64-key tile of K or V (rows of the batch's qkv at byte offset `col`)
@@ -524,7 +527,7 @@ __global__ __launch_bounds__(256, 3) void attention_mfma_kernel(const float* __r
     const __amdgpu_buffer_rsrc_t rsrc = kh::pipe::make_rsrc(bq, (uint32_t)(T * row_bytes));
     const int kcol = (D + h * kDk) * 4, vcol = kcol + D * 4;
 
-    // Q operand: query q, d = 16g .. 16g+15, scaled by 1/8.
+    // Q operand: query q, d = 16g .. 16g+15, scaled by log2(e) / 8.
     float qf[16];
     {
         const f32x4v* qr = reinterpret_cast<const f32x4v*>(bq + (int64_t)min(q, T - 1) * 3 * D + h * kDk + 16 * g);
@@ -532,7 +535,7 @@ __global__ __launch_bounds__(256, 3) void attention_mfma_kernel(const float* __r
         for (int c = 0; c < 4; ++c) {
             const f32x4v v = qr[c];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) qf[4 * c + e] = q < T ? v[e] * 0.125f : 0.0f;
+            for (int e = 0; e < 4; ++e) qf[4 * c + e] = q < T ? v[e] * kLog2eOver8 : 0.0f;
         }
     }
     attention_tile_dma(rsrc, ks, 0, row_bytes, kcol, wave, lane);
@@ -584,14 +587,16 @@ __global__ __launch_bounds__(256, 3) void attention_mfma_kernel(const float* __r
             for (int r = 0; r < 4; ++r) mx = fmaxf(mx, st[t][r]);
         mx = query4_max(mx);
         const float m_new = fmaxf(m, mx);
-        const float corr = __expf(m - m_new);
+        const float corr = __builtin_amdgcn_exp2f(m - m_new);
         float sum = 0.0f;
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                // A masked score (-3e38) gives exactly 0: m_new is a real score.
-                const float p = st[t][r] == -3.0e38f ? 0.0f : __expf(st[t][r] - m_new);
+                // A masked score (-3e38) gives exactly 0: m_new is a real
+                // score (the first tile holds key 0, which every query sees),
+                // so the exponent is about -3e38 and 2^x underflows to 0.
+                const float p = __builtin_amdgcn_exp2f(st[t][r] - m_new);
                 st[t][r] = p;
                 sum += p;
             }
@@ -800,7 +805,7 @@ int kh_attention_ex(const float* qkv, int B, int T, int H, int dk, int causal, f
     const bool fused = absmax_parts && blocks <= max_parts;
     // 1/sqrt(d_k) = 1/8 for dk = 64 (the reference's binary64 Python float,
     // nn.py:413, is exactly representable in binary32); the kernel applies it
-    // to Q.
+    // to Q together with log2(e), keeping the scores in base-2 units.
     if (causal)
         attention_mfma_kernel<true><<<(unsigned)blocks, 256, 0, d->stream>>>(qkv, B, T, H, out,
                                                                           fused ? absmax_parts : nullptr);
