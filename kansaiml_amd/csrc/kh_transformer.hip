@@ -72,6 +72,52 @@ __global__ __launch_bounds__(256) void embedding4_kernel(const int32_t* __restri
     *o = reinterpret_cast<const f4*>(tok)[(int64_t)id * D4 + c] + reinterpret_cast<const f4*>(pos)[(int64_t)(r % T) * D4 + c];
 }
 
+// Rows of D = 128 * KH floats (D = 128 .. 512, 16-byte aligned tables and
+// output): half a wave per row, KH float4 per lane, each wave four rows (two
+// pairs) with every id and table load issued before the first store, so a
+// launch of rows / 16 workgroups is resident at once and each wave waits
+// for two round trips (ids, then tables) instead of the one-float4-per-
+// thread kernel's many short-lived waves each waiting for both.
+template <int KH>
+__global__ __launch_bounds__(256) void embedding_rows_kernel(const int32_t* __restrict__ ids,
+                                                             const float* __restrict__ tok,
+                                                             const float* __restrict__ pos, int rows, int T, int V,
+                                                             float* __restrict__ out, unsigned* __restrict__ fault) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    constexpr int P = 2, D4 = 32 * KH;
+    const int lane = threadIdx.x & 63, half = lane >> 5, hl = lane & 31;
+    const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * (2 * P);
+    int id[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const int r = row0 + 2 * p + half;
+        id[p] = r < rows ? ids[r] : 0;
+    }
+    f4 tv[P][KH], pv[P][KH];
+    bool bad[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const int r = row0 + 2 * p + half;
+        bad[p] = id[p] < 0 || id[p] >= V;
+        const int idc = bad[p] ? 0 : id[p];
+#pragma unroll
+        for (int i = 0; i < KH; ++i) {
+            tv[p][i] = reinterpret_cast<const f4*>(tok)[(int64_t)idc * D4 + hl + 32 * i];
+            pv[p][i] = reinterpret_cast<const f4*>(pos)[(int64_t)((r < rows ? r : 0) % T) * D4 + hl + 32 * i];
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const int r = row0 + 2 * p + half;
+        if (r >= rows) continue;
+        if (bad[p] && hl == 0) atomicOr(fault, kh::kFaultBadIndex);
+#pragma unroll
+        for (int i = 0; i < KH; ++i)
+            reinterpret_cast<f4*>(out)[(int64_t)r * D4 + hl + 32 * i] =
+                bad[p] ? f4{0.f, 0.f, 0.f, 0.f} : tv[p][i] + pv[p][i];
+    }
+}
+
 // ---------------------------------------------------------------------------
 // LayerNorm: one wave per row; the row lives in registers (D <= 64 * 16).
 // ---------------------------------------------------------------------------
@@ -676,8 +722,21 @@ int kh_embedding(const int32_t* ids, int64_t rows, int T, const float* tok, int 
     KH_REQUIRE(ids && tok && pos && out, "kh_embedding: null pointer");
     KH_DEVICE_OR_RETURN(d);
     const int64_t n = rows * D;
-    if (D % 4 == 0 && rows <= 0x7FFFFFFF && n / 4 <= 0xFFFFFFFFLL * 256 && kh::aligned(tok, 16) &&
-        kh::aligned(pos, 16) && kh::aligned(out, 16)) {
+    const bool vec = D % 4 == 0 && rows <= 0x7FFFFFFF && kh::aligned(tok, 16) && kh::aligned(pos, 16) &&
+                     kh::aligned(out, 16);
+    if (vec && D % 128 == 0 && D <= 512 && rows <= 0x7FFFFFFF - 16) {
+        const unsigned blocks = (unsigned)((rows + 15) / 16);
+        auto go = [&](auto kh_) {
+            embedding_rows_kernel<decltype(kh_)::value><<<blocks, 256, 0, d->stream>>>(ids, tok, pos, (int)rows, T, V,
+                                                                                     out, d->fault);
+        };
+        if (D == 128) go(std::integral_constant<int, 1>{});
+        else if (D == 256) go(std::integral_constant<int, 2>{});
+        else if (D == 384) go(std::integral_constant<int, 3>{});
+        else go(std::integral_constant<int, 4>{});
+        return kh::launch_status("embedding");
+    }
+    if (vec && n / 4 <= 0xFFFFFFFFLL * 256) {
         embedding4_kernel<<<(unsigned)((n / 4 + 255) / 256), 256, 0, d->stream>>>(ids, tok, pos, (int)rows, T, D / 4,
                                                                                   V, out, d->fault);
         return kh::launch_status("embedding");

@@ -61,7 +61,7 @@ def test_gelu(G):
     assert sp[5] == np.float32(3e38) and sp[6] == 0
 
 
-@pytest.mark.parametrize("d", [48, 50])  # float4 path, scalar path
+@pytest.mark.parametrize("d", [48, 50, 384, 256])  # float4 path, scalar path, half-wave rows (C4's 384)
 def test_embedding_exact_and_bad_id(G, d):
     N, D = G
     gen = np.random.Generator(np.random.PCG64(3))
@@ -79,6 +79,10 @@ def test_embedding_exact_and_bad_id(G, d):
     with pytest.raises(RuntimeError):
         N.synchronize()
     N.synchronize()
+    got = out.numpy()
+    np.testing.assert_array_equal(got[24], np.zeros(d, np.float32))  # the bad id's row is zeros
+    ok = np.arange(60) != 24
+    np.testing.assert_array_equal(got[ok].view(np.uint32), ref[ok].astype(np.float32).view(np.uint32))
 
 
 @pytest.mark.parametrize("batch,seq,heads", [(2, 1, 2), (2, 5, 3), (1, 64, 2), (2, 100, 2), (2, 256, 6), (4, 200, 2),
