@@ -396,7 +396,7 @@ using namespace kh::pipe;
 // SIMD: 2 for 256-wide N tiles (128 accumulators per wave), 4 otherwise (two
 // resident workgroups per CU within the 128-register budget).
 template <int BM, int BN, int NS, bool FUSED, int MODE = kh::quant::kOutStore>
-__global__ __launch_bounds__(512, BN == 256 ? 2 : 4) void gemm_i8_pingpong_kernel(
+__global__ __launch_bounds__(512, BN == 256 ? 2 : (FUSED ? 4 : 6)) void gemm_i8_pingpong_kernel(
     const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, int N, int K, int group_m, Epilogue ep,
     unsigned* parts) {
     constexpr int BK = 64, WM = 2, WN = 4, kWaves = WM * WN;
