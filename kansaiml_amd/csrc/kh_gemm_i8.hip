@@ -155,6 +155,28 @@ __device__ __forceinline__ unsigned store_block32_masked(const Epilogue& ep, int
     return store_block32_impl<FUSED, RG, true, MODE>(ep, i0, j, M, N, v, sc);
 }
 
+// max |GELU(y)| over 16 values as bits, with GELU evaluated once instead of
+// 16 times: kh::gelu, as the hardware computes it, is non-decreasing on
+// [0, +inf), and |GELU(x)| for every negative x is below GELU(0.3) (both
+// checked over every binary32 value by tests/test_gpu_charlm.py), so when the
+// largest value is >= 0.3 its GELU is the largest in magnitude.  Otherwise
+// every value's GELU is evaluated.  A NaN or +-inf among the values gives a
+// non-finite result, as GELU would (GELU of NaN, +inf, -inf: NaN, +inf, NaN).
+constexpr int kGeluMonoBits = 0x3E99999A;  // 0.3f
+
+__device__ __forceinline__ unsigned gelu_absmax_bits(const float (&y)[16]) {
+    kh::quant::AbsMax am;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) am.add1(y[r]);
+    const unsigned m = am.bits();
+    if (m >= KH_NONFINITE_BITS) return m;
+    if (am.smax >= kGeluMonoBits) return kh::abs_bits32(kh::gelu(__int_as_float(am.smax)));
+    unsigned g = 0;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) g = max(g, kh::abs_bits32(kh::gelu(y[r])));
+    return g;
+}
+
 // store_block32 for a block inside the matrix in the common configuration --
 // fp32 output only (or one of the quantize passes), per-tensor activation
 // scale, or per-row scales (ROWSA: sa[i] * sb[j] per row, as in
@@ -196,6 +218,9 @@ __device__ __forceinline__ unsigned store_block32_full(const Epilogue& ep, int64
 #pragma unroll
         for (int r = 0; r < 16; ++r) y[r] = y[r] + bj;
     }
+    if constexpr (FUSED && MODE == kh::quant::kOutMaxOnly) {
+        if (ep.act == kActGelu && !ep.residual) return gelu_absmax_bits(y);
+    }
     if (FUSED && ep.act == kActGelu) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) y[r] = kh::gelu(y[r]);
@@ -212,11 +237,33 @@ __device__ __forceinline__ unsigned store_block32_full(const Epilogue& ep, int64
 #pragma unroll
         for (int r = 0; r < 16; ++r) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y[r]), ro, voff, row_off(r), 0);
     } else if (MODE == kh::quant::kOutQuant) {
-        const __amdgpu_buffer_rsrc_t rq = kh::pipe::make_rsrc(ep.q + base, span / 4u);
+        // The codes of quant_one: the fast path for all 16 values, and the
+        // exact path for all 16 in a lane holding an undecided value (or
+        // everywhere when the scale rules the fast path out).
+        unsigned c[16];
+        bool ok = sc.fast;
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-            __builtin_amdgcn_raw_buffer_store_b8((unsigned char)kh::quant::quant_one(y[r], sc), rq, voff / 4,
-                                                 row_off(r) / 4, 0);
+        for (int r = 0; r < 16; ++r) c[r] = kh::quant::quant_fast(y[r], sc.rf, ok);  // low byte: the code
+        if (!ok) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) c[r] = sc.bad ? 0u : (unsigned)kh::quant::quant_exact(y[r], sc.s);
+        }
+        // Codes of rows 8g + t (t = 0..3) of this lane's column, packed (byte
+        // t = row t), then transposed across each quad of lanes so that lane
+        // 4p + t holds row 8g + t of columns 4p .. 4p + 3: one dword store per
+        // group instead of four byte stores.
+        const unsigned sel_a = (fr & 1) ? 0x03070105u : 0x06020400u;  // with lane ^ 1: bytes (0,2) or (1,3)
+        const unsigned sel_b = (fr & 2) ? 0x03020706u : 0x05040100u;  // with lane ^ 2: halves 0 or 1
+        const __amdgpu_buffer_rsrc_t rq = kh::pipe::make_rsrc(ep.q + base, span / 4u);
+        const int qoff = (4 * fh + (fr & 3)) * N + (fr & ~3);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const unsigned p = __builtin_amdgcn_perm(c[4 * g + 1], c[4 * g], 0x0c0c0400u) |
+                               __builtin_amdgcn_perm(c[4 * g + 3], c[4 * g + 2], 0x04000c0cu);
+            const unsigned a = __builtin_amdgcn_perm(kh::lanes::quad_perm<0xB1>(p), p, sel_a);
+            const unsigned t = __builtin_amdgcn_perm(kh::lanes::quad_perm<0x4E>(a), a, sel_b);
+            __builtin_amdgcn_raw_buffer_store_b32(t, rq, qoff, 8 * g * N, 0);
+        }
     }
     return mx;
 }
@@ -392,11 +439,17 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_i8_kernel(const int8_t* __r
 // ---------------------------------------------------------------------------
 using namespace kh::pipe;
 
-// FUSED: the epilogue may apply an activation and a residual add.  Waves per
-// SIMD: 2 for 256-wide N tiles (128 accumulators per wave), 4 otherwise (two
-// resident workgroups per CU within the 128-register budget).
-template <int BM, int BN, int NS, bool FUSED, int MODE = kh::quant::kOutStore>
-__global__ __launch_bounds__(512, BN == 256 ? 2 : (FUSED ? 4 : 6)) void gemm_i8_pingpong_kernel(
+// FUSED: the epilogue may apply an activation and a residual add.  FAST: the
+// launch guarantees full tiles, no int32 output, a per-tensor activation
+// scale and N <= 2^24, so only store_block32_full is compiled in.  Waves per
+// SIMD: 2 for 256-wide N tiles (128 accumulators per wave); 4 for the
+// 256x128 tile; 6 (three resident workgroups per CU, 80 registers) for the
+// 128x128 tile unless the general fused epilogue is compiled in, which needs 4
+// (128 registers: its per-element residual and masking paths spill heavily
+// at 80).  At K = 384 the third workgroup's main loop covers the other two's
+// epilogues.
+template <int BM, int BN, int NS, bool FUSED, int MODE = kh::quant::kOutStore, bool FAST = false>
+__global__ __launch_bounds__(512, BN == 256 ? 2 : ((BM == 256 || (FUSED && !FAST)) ? 4 : 6)) void gemm_i8_pingpong_kernel(
     const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, int N, int K, int group_m, Epilogue ep,
     unsigned* parts) {
     constexpr int BK = 64, WM = 2, WN = 4, kWaves = WM * WN;
@@ -531,7 +584,17 @@ __global__ __launch_bounds__(512, BN == 256 ? 2 : (FUSED ? 4 : 6)) void gemm_i8_
     const int64_t col_base = (int64_t)tn * BN + wn * kWaveN + fr;
     unsigned mx = 0;
     const bool full = rows_a == BM && rows_b == BN;
-    if (full && !ep.acc && !ep.sa_per_row && (MODE != kh::quant::kOutStore || ep.out) && N <= (1 << 24)) {
+    if constexpr (FAST) {
+#pragma unroll
+        for (int a = 0; a < kTM; ++a)
+#pragma unroll
+            for (int b = 0; b < kTN; ++b) {
+                mx = max(mx, store_block32_full<FUSED, MODE>(ep, (int64_t)tm * BM + wm * kWaveM + a * 32,
+                                                             (int64_t)tn * BN + wn * kWaveN + b * 32, N, lane,
+                                                             ep.sa[0], acc[a][b], sc));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+    } else if (full && !ep.acc && !ep.sa_per_row && (MODE != kh::quant::kOutStore || ep.out) && N <= (1 << 24)) {
         const double sa = ep.sa[0];
 #pragma unroll
         for (int a = 0; a < kTM; ++a)
@@ -770,6 +833,29 @@ int launch_pingpong_cfg(kh::Device* d, const int8_t* A, const int8_t* B, int64_t
     // (8192^3: 2320 TOPS against 2230-2260 with 4-8 rows and 2030 with 1 or
     // 32), 8 elsewhere (no measurable difference at C4's shapes).
     constexpr int group_m = (BM == 256 && BN == 256) ? 2 : 8;
+    // Every tile full and the common epilogue: the FAST kernels.
+    const bool fast = M % BM == 0 && N % BN == 0 && N <= (1 << 24) && !ep.acc && !ep.sa_per_row &&
+                      (mode != kOutStore || ep.out) && (mode != kOutQuant || kh::aligned(ep.q, 4));
+    if (fast) {
+        if constexpr (BM == 128 && BN == 128) {
+            if (mode == kOutMaxOnly)
+                gemm_i8_pingpong_kernel<BM, BN, NS, true, kOutMaxOnly, true>
+                    <<<tiles, 512, 0, d->stream>>>(A, B, (int)M, (int)N, (int)K, group_m, ep, parts);
+            else if (mode == kOutQuant)
+                gemm_i8_pingpong_kernel<BM, BN, NS, true, kOutQuant, true>
+                    <<<tiles, 512, 0, d->stream>>>(A, B, (int)M, (int)N, (int)K, group_m, ep, nullptr);
+        }
+        if (mode != kOutStore) {
+            // launched above (launch_pingpong routes the quantize passes to the 128x128 tile)
+        } else if (ep.act != kActNone || ep.residual)
+            gemm_i8_pingpong_kernel<BM, BN, NS, true, kOutStore, true>
+                <<<tiles, 512, 0, d->stream>>>(A, B, (int)M, (int)N, (int)K, group_m, ep, parts);
+        else
+            gemm_i8_pingpong_kernel<BM, BN, NS, false, kOutStore, true>
+                <<<tiles, 512, 0, d->stream>>>(A, B, (int)M, (int)N, (int)K, group_m, ep, parts);
+        if (nparts) *nparts = (int)tiles;
+        return kh::launch_status("gemm_i8_pingpong");
+    }
     if constexpr (BM == 128 && BN == 128) {
         if (mode == kOutMaxOnly)
             gemm_i8_pingpong_kernel<BM, BN, NS, true, kOutMaxOnly>
@@ -802,13 +888,19 @@ int launch_pingpong(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, 
                     int mode = kh::quant::kOutStore) {
     auto tiles = [&](int64_t bm, int64_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
     const int64_t want = (int64_t)d->cus * 3 / 2;
-    if (K <= 512 || mode != kh::quant::kOutStore)
+    // At most two 128x128 tiles per CU: LDS holds two workgroups of a
+    // 4-stage ring, one stage more in flight per K-step.
+    const bool deep = tiles(128, 128) <= 2 * (int64_t)d->cus && K >= 192;
+    if (K <= 512 || mode != kh::quant::kOutStore) {
+        if (deep) return launch_pingpong_cfg<128, 128, 4>(d, A, B, M, N, K, ep, parts, nparts, mode);
         return launch_pingpong_cfg<128, 128, 3>(d, A, B, M, N, K, ep, parts, nparts, mode);
+    }
     if (tiles(256, 256) >= want) {
         if (K >= 1024) return launch_pingpong_cfg<256, 256, 4>(d, A, B, M, N, K, ep, parts, nparts, mode);
         return launch_pingpong_cfg<256, 256, 3>(d, A, B, M, N, K, ep, parts, nparts, mode);
     }
     if (tiles(256, 128) >= want) return launch_pingpong_cfg<256, 128, 3>(d, A, B, M, N, K, ep, parts, nparts, mode);
+    if (deep) return launch_pingpong_cfg<128, 128, 4>(d, A, B, M, N, K, ep, parts, nparts, mode);
     return launch_pingpong_cfg<128, 128, 3>(d, A, B, M, N, K, ep, parts, nparts, mode);
 }
 

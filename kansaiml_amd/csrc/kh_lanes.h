@@ -29,6 +29,13 @@ __device__ __forceinline__ unsigned row_ror(unsigned v) {
     return (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x120 + N, 0xF, 0xF, false);
 }
 
+// Lane 4q + i reads lane 4q + ((CTRL >> 2i) & 3) (DPP quad_perm).
+template <int CTRL>
+__device__ __forceinline__ unsigned quad_perm(unsigned v) {
+    static_assert(CTRL >= 0 && CTRL <= 0xFF, "quad_perm");
+    return (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+
 // Op over the 16 lanes of each row, in every lane of the row.
 template <typename T, typename Op>
 __device__ __forceinline__ T row16_reduce(T v, Op op) {

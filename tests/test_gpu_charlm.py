@@ -61,6 +61,45 @@ def test_gelu(G):
     assert sp[5] == np.float32(3e38) and sp[6] == 0
 
 
+def test_gelu_order_over_every_binary32_value(G):
+    """The absmax pass of a GELU epilogue (gelu_absmax_bits in
+    kansaiml_amd/csrc/kh_gemm_i8.hip) takes max |GELU| over values whose
+    largest is >= 0.3 as the GELU of that largest value.  Exact when the
+    GPU's kh::gelu is non-decreasing over every non-negative binary32 value
+    (+0 to +inf) and |GELU(x)| < GELU(0.3) for every negative finite x:
+    both checked here value by value, all 2^32 - 2^24 + 1 of them, against
+    the kernel's own threshold constant."""
+    import os
+    import re
+    N, D = G
+    src = open(os.path.join(os.path.dirname(__file__), "..", "kansaiml_amd", "csrc", "kh_gemm_i8.hip")).read()
+    thr = int(re.search(r"constexpr int kGeluMonoBits = (0x[0-9A-Fa-f]+);", src).group(1), 16)
+    assert thr == int(np.array([0.3], np.float32).view(np.uint32)[0])
+    chunk = 1 << 27
+    xd, od = D([chunk]), D([chunk])
+
+    def gelu_bits(lo, hi):  # GELU of the binary32 values with bit patterns lo .. hi - 1
+        n = hi - lo
+        xd.view(0, [n]).copy_from(np.arange(lo, hi, dtype=np.uint32).view(np.float32))
+        N.call("kh_gelu", xd.ptr, od.ptr, n)
+        return od.view(0, [n]).numpy()
+
+    prev = np.float32(-1.0)
+    for lo in range(0, 0x7F800001, chunk):  # +0 .. +inf
+        y = gelu_bits(lo, min(lo + chunk, 0x7F800001))
+        assert not np.isnan(y).any(), lo
+        assert y[0] >= prev and not (y[1:] < y[:-1]).any(), hex(lo)
+        prev = y[-1]
+    assert prev == np.inf
+    g_thr = gelu_bits(thr, thr + 1)[0]
+    neg_max = np.float32(0.0)
+    for lo in range(0x80000000, 0xFF800000, chunk):  # -0 .. the most negative finite value
+        y = gelu_bits(lo, min(lo + chunk, 0xFF800000))
+        assert not np.isnan(y).any(), hex(lo)
+        neg_max = max(neg_max, np.abs(y).max())
+    assert 0.169 < neg_max < g_thr, (neg_max, g_thr)
+
+
 @pytest.mark.parametrize("d", [48, 50, 384, 256])  # float4 path, scalar path, half-wave rows (C4's 384)
 def test_embedding_exact_and_bad_id(G, d):
     N, D = G

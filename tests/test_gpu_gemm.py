@@ -335,6 +335,54 @@ def test_gemm_i8_quant_edge_cases(hip):
     Nn.synchronize()
 
 
+@pytest.mark.parametrize("case", ["negative", "threshold", "nan_bias", "inf_bias", "neg_inf_bias"])
+def test_gemm_i8_quant_gelu_absmax_paths(hip, case):
+    """The absmax pass of a GELU epilogue takes each lane's largest value's
+    GELU when that value is >= 0.3 and every value's GELU otherwise; both
+    give the unfused scale and codes.  Pre-activations near -0.75 (the
+    largest |GELU| of a negative argument; the second path everywhere),
+    straddling 0.3 by a few ulps (both paths, lane by lane), and a NaN or
+    infinite bias (a non-finite result: reported as ValueError, as the
+    unfused quantize reports it, with the same codes)."""
+    from kansaiml_amd import _native as Nn
+    H, D = hip
+    M, N, K = 512, 384, 128  # full 128x128 tiles
+    gen = np.random.Generator(np.random.PCG64(77))
+    a = gen.integers(-127, 128, (M, K), dtype=np.int8)
+    bt = gen.integers(-127, 128, (N, K), dtype=np.int8)
+    sa, sb = np.array([3e-4]), np.full(N, 1e-4)  # GEMM terms of about 2e-3
+    if case == "negative":
+        bias = np.float32(-0.75) + gen.uniform(-0.01, 0.01, N).astype(np.float32)
+    elif case == "threshold":
+        sb = np.full(N, 1e-9)  # terms of about 2e-8: a few ulps of 0.3
+        bias = np.full(N, 0.3, np.float32)
+    else:
+        bias = gen.standard_normal(N).astype(np.float32)
+        bias[N // 3] = {"nan_bias": np.nan, "inf_bias": np.inf, "neg_inf_bias": -np.inf}[case]
+    ad, bd, sad, sbd, biasd = D.from_host(a), D.from_host(bt), D.from_host(sa), D.from_host(sb), D.from_host(bias)
+    bad = case.endswith("_bias")
+    q, s = H.gemm_i8_quant(ad, bd, sad, sbd, biasd, act="gelu")
+    if bad:
+        with pytest.raises(ValueError):
+            Nn.synchronize()
+    y, _ = H.gemm_i8_fused(ad, bd, sad, sbd, biasd, act="gelu")
+    q2, s2 = H.quantize_tensor(y)
+    if bad:
+        with pytest.raises(ValueError):
+            Nn.synchronize()
+        assert np.isnan(s.numpy()[0]) and np.isnan(s2.numpy()[0])
+    else:
+        yh = y.numpy()
+        if case == "threshold":  # pre-activations on both sides of 0.3
+            pre = H.gemm_i8_fused(ad, bd, sad, sbd, biasd)[0].numpy()
+            assert (pre >= np.float32(0.3)).any() and (pre < np.float32(0.3)).any()
+        oq, os_ = O.ko_quantize_tensor(yh)
+        np.testing.assert_array_equal(q.numpy().reshape(-1), oq.reshape(-1))
+        assert s.numpy()[0] == os_
+        assert s.numpy()[0] == s2.numpy()[0]
+    np.testing.assert_array_equal(q.numpy(), q2.numpy())
+
+
 @pytest.mark.parametrize("rows,d", [(1000, 384), (16384, 384), (37, 100), (1, 1024), (5, 3)])
 def test_layernorm_quant_matches_unfused(hip, rows, d):
     """kh_layernorm_quant's codes and scale equal the per-tensor quantize of
