@@ -303,31 +303,30 @@ __device__ __forceinline__ unsigned layernorm_rows_vec(const float* __restrict__
 // eps) are computed once per pair; the reductions stay in the VALU
 // (kh::lanes::half_sum).  Otherwise as layernorm_rows_vec: all loads before any
 // arithmetic, the centred values multiplied by the correctly rounded
-// 1 / sqrt(var + eps), rows >= `rows` computed on zeros and not stored.
-template <int KH, int MODE>
-__device__ __forceinline__ unsigned layernorm_rows_half(const float* __restrict__ x, int64_t row0, int64_t rows,
-                                                        int D, const float* __restrict__ w,
-                                                        const float* __restrict__ b, float eps,
-                                                        float* __restrict__ out, int8_t* __restrict__ q,
-                                                        const kh::quant::Scale& sc, double* __restrict__ rscales,
-                                                        unsigned* __restrict__ fault, int lane) {
-    using namespace kh::quant;
-    typedef float f4 __attribute__((ext_vector_type(4)));
-    constexpr int P = kLnRowsPerWave / 2;
+// 1 / sqrt(var + eps), rows >= `rows` computed on zeros.  Leaves the
+// normalized values in v and each pair's largest |value| bits in rm.
+constexpr int kLnPairs = kLnRowsPerWave / 2;
+
+template <int KH>
+__device__ __forceinline__ void layernorm_half_values(const float* __restrict__ x, int64_t row0, int64_t rows, int D,
+                                                      const float* __restrict__ w, const float* __restrict__ b,
+                                                      float eps, kh::quant::f32x4 (&v)[kLnPairs][KH],
+                                                      unsigned (&rm)[kLnPairs], int lane) {
+    using kh::quant::f32x4;
+    constexpr int P = kLnPairs;
     const int half = lane >> 5, hl = lane & 31;
-    f4 v[P][KH];
 #pragma unroll
     for (int p = 0; p < P; ++p) {
         const int64_t row = row0 + 2 * p + half;
 #pragma unroll
         for (int i = 0; i < KH; ++i)
-            v[p][i] = row < rows ? reinterpret_cast<const f4*>(x + row * D)[hl + 32 * i] : f4{0.f, 0.f, 0.f, 0.f};
+            v[p][i] = row < rows ? reinterpret_cast<const f32x4*>(x + row * D)[hl + 32 * i] : f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    f4 wv[KH], bv[KH];
+    f32x4 wv[KH], bv[KH];
 #pragma unroll
     for (int i = 0; i < KH; ++i) {
-        wv[i] = reinterpret_cast<const f4*>(w)[hl + 32 * i];
-        bv[i] = reinterpret_cast<const f4*>(b)[hl + 32 * i];
+        wv[i] = reinterpret_cast<const f32x4*>(w)[hl + 32 * i];
+        bv[i] = reinterpret_cast<const f32x4*>(b)[hl + 32 * i];
     }
     float mean[P], inv[P];
 #pragma unroll
@@ -347,21 +346,41 @@ __device__ __forceinline__ unsigned layernorm_rows_half(const float* __restrict_
         }
         inv[p] = 1.0f / sqrtf(kh::lanes::half_sum(ss) / (float)D + eps);
     }
-    unsigned mx = 0;
 #pragma unroll
     for (int p = 0; p < P; ++p) {
-        const int64_t row = row0 + 2 * p + half;
-        unsigned rm = 0;
+        rm[p] = 0;
 #pragma unroll
         for (int i = 0; i < KH; ++i)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 v[p][i][e] = v[p][i][e] * inv[p] * wv[i][e] + bv[i][e];
-                rm = max(rm, kh::abs_bits32(v[p][i][e]));
+                rm[p] = max(rm[p], kh::abs_bits32(v[p][i][e]));
             }
+    }
+}
+
+// layernorm_half_values, then MODE's output; returns this lane's largest
+// |out| bits over its rows < `rows`.
+template <int KH, int MODE>
+__device__ __forceinline__ unsigned layernorm_rows_half(const float* __restrict__ x, int64_t row0, int64_t rows,
+                                                        int D, const float* __restrict__ w,
+                                                        const float* __restrict__ b, float eps,
+                                                        float* __restrict__ out, int8_t* __restrict__ q,
+                                                        const kh::quant::Scale& sc, double* __restrict__ rscales,
+                                                        unsigned* __restrict__ fault, int lane) {
+    using namespace kh::quant;
+    constexpr int P = kLnPairs;
+    const int half = lane >> 5, hl = lane & 31;
+    f32x4 v[P][KH];
+    unsigned rm[P];
+    layernorm_half_values<KH>(x, row0, rows, D, w, b, eps, v, rm, lane);
+    unsigned mx = 0;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const int64_t row = row0 + 2 * p + half;
         if constexpr (MODE == kLnRowQuant) {
             // The row's own scale (quantize.py:67-69 applied to the row).
-            const Scale rs = make_scale(kh::lanes::half_max(rm));
+            const Scale rs = make_scale(kh::lanes::half_max(rm[p]));
             if (row >= rows) continue;
             if (hl == 0) {
                 rscales[row] = rs.s;
@@ -371,10 +390,10 @@ __device__ __forceinline__ unsigned layernorm_rows_half(const float* __restrict_
             for (int i = 0; i < KH; ++i) reinterpret_cast<unsigned*>(q + row * D)[hl + 32 * i] = pack4(v[p][i], rs);
         } else {
             if (row >= rows) continue;
-            mx = max(mx, rm);
+            mx = max(mx, rm[p]);
 #pragma unroll
             for (int i = 0; i < KH; ++i) {
-                if (MODE == kOutStore) reinterpret_cast<f4*>(out + row * D)[hl + 32 * i] = v[p][i];
+                if (MODE == kOutStore) reinterpret_cast<f32x4*>(out + row * D)[hl + 32 * i] = v[p][i];
                 if (MODE == kOutQuant) reinterpret_cast<unsigned*>(q + row * D)[hl + 32 * i] = pack4(v[p][i], sc);
             }
         }

@@ -383,10 +383,13 @@ def test_gemm_i8_quant_gelu_absmax_paths(hip, case):
     np.testing.assert_array_equal(q.numpy(), q2.numpy())
 
 
-@pytest.mark.parametrize("rows,d", [(1000, 384), (16384, 384), (37, 100), (1, 1024), (5, 3)])
+@pytest.mark.parametrize("rows,d", [(1000, 384), (16384, 384), (37, 100), (1, 1024), (5, 3), (3001, 128),
+                                    (777, 256), (4097, 512), (16, 384),
+                                    (40000, 384)])
 def test_layernorm_quant_matches_unfused(hip, rows, d):
     """kh_layernorm_quant's codes and scale equal the per-tensor quantize of
-    kh_layernorm's output (vector and scalar row paths)."""
+    kh_layernorm's output (two rows per wave for D = 128..512, vector and
+    scalar row paths, one workgroup to 2500)."""
     H, D = hip
     gen = np.random.Generator(np.random.PCG64(rows * 7 + d))
     x = (gen.standard_normal((rows, d)) * 3 + 0.5).astype(np.float32)
@@ -397,6 +400,24 @@ def test_layernorm_quant_matches_unfused(hip, rows, d):
     q, s = H.layer_norm_quant(xd, wd, bd)
     np.testing.assert_array_equal(q.numpy().reshape(-1), oq.reshape(-1))
     assert s.numpy()[0] == os_
+
+
+def test_layernorm_quant_back_to_back(hip):
+    """Consecutive LayerNorm quantizes with no synchronization between them
+    (the partials scratch reused), of different sizes and data, each equal
+    to the two-step result."""
+    H, D = hip
+    gen = np.random.Generator(np.random.PCG64(12))
+    w, b = gen.standard_normal(384).astype(np.float32), gen.standard_normal(384).astype(np.float32)
+    wd, bd = D.from_host(w), D.from_host(b)
+    xs = [D.from_host((gen.standard_normal((r, 384)) * (i + 1)).astype(np.float32))
+          for i, r in enumerate((16384, 16, 5000, 16384, 1, 9000))]
+    got = [H.layer_norm_quant(xd, wd, bd) for xd in xs]
+    for xd, (q, s) in zip(xs, got):
+        y, _ = H.layer_norm(xd, wd, bd)
+        oq, os_ = O.ko_quantize_tensor(y.numpy())
+        np.testing.assert_array_equal(q.numpy().reshape(-1), oq.reshape(-1))
+        assert s.numpy()[0] == os_
 
 
 def test_layernorm_quant_edge_cases(hip):
