@@ -163,6 +163,8 @@ __global__ __launch_bounds__(256) void absmax_partials_kernel(const float* __res
     if (threadIdx.x == 0) partials[blockIdx.x] = max(max(red[0], red[1]), max(red[2], red[3]));
 }
 
+constexpr int kTensorUnroll = 4;
+
 template <bool VEC>
 __global__ __launch_bounds__(256) void quant_tensor_kernel(const float* __restrict__ x, int64_t n,
                                                            int8_t* __restrict__ q, double* __restrict__ scale,
@@ -180,7 +182,22 @@ __global__ __launch_bounds__(256) void quant_tensor_kernel(const float* __restri
         const int64_t n4 = n >> 2;
         const f32x4* x4 = reinterpret_cast<const f32x4*>(x);
         unsigned* q4 = reinterpret_cast<unsigned*>(q);
-        for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride) q4[i] = pack4(x4[i], sc);
+        // kTensorUnroll float4 per thread in flight before the first code is
+        // stored (one load at a time per wave left HBM idle between them).
+        constexpr int U = kTensorUnroll;
+        for (int64_t i0 = (int64_t)blockIdx.x * 256 * U + threadIdx.x; i0 < n4; i0 += stride * U) {
+            f32x4 v[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int64_t i = i0 + (int64_t)u * 256;
+                v[u] = i < n4 ? x4[i] : f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int64_t i = i0 + (int64_t)u * 256;
+                if (i < n4) q4[i] = pack4(v[u], sc);
+            }
+        }
         if (blockIdx.x == 0)
             for (int64_t i = n4 * 4 + threadIdx.x; i < n; i += 256) q[i] = (int8_t)quant_one(x[i], sc);
     } else {
