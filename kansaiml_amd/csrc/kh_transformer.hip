@@ -469,10 +469,17 @@ __global__ __launch_bounds__(256) void gelu_kernel(const float* __restrict__ x, 
 //
 // A workgroup owns 64 queries of one (batch, head); wave w owns queries
 // 16w .. 16w+15 of them, lane l query 16w + l % 16.  Keys go through LDS 64
-// at a time, K and V each as [key][d] (256-byte rows whose 16-byte chunk c sits
-// at position c ^ (key % 16), so the column reads below touch 16 distinct
-// chunks), brought in by LDS-DMA from a buffer resource spanning the batch's
-// rows (keys past T read as 0).  Each has one buffer and its own point in the
+// at a time, K and V each as [key][d]: 256-byte rows whose 16-byte chunk c
+// sits at position c ^ att_swz(key % 16), brought in by LDS-DMA from a buffer
+// resource spanning the batch's rows (keys past T read as 0).  LDS bank
+// conflicts of ds_read_b128 on gfx950, measured with a probe kernel: none when
+// each 16-lane group reads one 256-byte row at 16 distinct positions and the
+// two groups of a half-wave read rows of different parity, two-way when a
+// half-wave's lanes read 16 different rows as the K reads below must (one key
+// per lane).  The key order att_key gives the V reads the first form; the K
+// reads keep the two-way conflict (about 0.8 M conflict cycles per launch at
+// C4's shape, hidden behind the MFMAs: the launch time did not change when
+// the V reads' conflicts were removed).  Each has one buffer and its own point in the
 // iteration: V of tile i is loaded while S of tile i is computed and
 // softmaxed, K of tile i+1 while P V of tile i is computed, so no wave waits
 // on HBM once the pipeline runs.  Both products run on
@@ -481,10 +488,11 @@ __global__ __launch_bounds__(256) void gelu_kernel(const float* __restrict__ x, 
 // l is D[4 * (l / 16) + r][l % 16]).  The reduction index of each product is
 // order-free, so it is mapped to keep operands in registers:
 //   S^T = K Q^T (k = head dim; step s of lane group g = l / 16 takes
-//   d = 16g + s): lane l ends up holding, for its own query, the scores of
-//   keys 16t + 4g + r (t, r = 0..3) of the tile;
+//   d = 16g + s; A's row i is key att_key(i) of the subtile): lane l ends up
+//   holding, for its own query, the scores of keys 16t + att_key(4g + r)
+//   (t, r = 0..3) of the tile;
 //   O^T = V^T P^T (k = key; step (t, r) of lane group g takes key
-//   16t + 4g + r; product j's row i is d = 4i + j): P^T's operand is exactly
+//   16t + att_key(4g + r); product j's row i is d = 4i + j): P^T's operand is exactly
 //   the probabilities lane l holds, so P never leaves registers, V^T's
 //   operands for the four products are one 16-byte read of V's row, and lane
 //   l ends up holding d = 16g .. 16g+15 of its query's output.
@@ -504,6 +512,14 @@ constexpr float kLog2eOver8 = 0.18033688011112042f;  // log2(e) / sqrt(64)
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
+// LDS position of a row's 16-byte chunks: chunk c of key k (k % 16) at
+// c ^ att_swz(k), a different permutation of the 16 positions per key.
+__device__ __forceinline__ int att_swz(int k) { return (k & 10) | ((k >> 2) & 1); }
+// Key of row i of a 16-key subtile in the products: rows 4g + r take key
+// 4g + (r ^ (g & 1)), so the two lane groups of a half-wave read V rows of
+// different parity (different 256-byte halves of the bank window).
+__device__ __forceinline__ int att_key(int i) { return i ^ ((i >> 2) & 1); }
+
 // max / sum over the 4 lanes l % 16 + 16g holding one query's scores (the
 // same lane of each 16-lane row: one row swap, one half swap; every one of
 // the 4 lanes gets the same bits).
@@ -521,7 +537,7 @@ __device__ __forceinline__ float query4_sum(float v) {
 __device__ __forceinline__ void attention_tile_dma(__amdgpu_buffer_rsrc_t r, float* tile, int k0, int row_bytes,
                                                    int col, int wave, int lane) {
     const int row = 4 * wave + (lane >> 4);  // 16i + row, i = 0..3
-    const int voff = (k0 + row) * row_bytes + col + 16 * ((lane & 15) ^ row);
+    const int voff = (k0 + row) * row_bytes + col + 16 * ((lane & 15) ^ att_swz(row));
 #pragma unroll
     for (int i = 0; i < 4; ++i)
         kh::pipe::lds_dma16(r, reinterpret_cast<char*>(tile) + (16 * i + 4 * wave) * kDk * 4,
@@ -529,16 +545,17 @@ __device__ __forceinline__ void attention_tile_dma(__amdgpu_buffer_rsrc_t r, flo
 }
 
 // S^T = K Q^T for key subtiles t < NT of the tile in `ks` (st[t][r] = score of
-// key 16t + 4g + r); subtiles t >= NT are left as they are.
+// key 16t + att_key(4g + r)); subtiles t >= NT are left as they are.
 template <int NT>
 __device__ __forceinline__ void attention_scores(const float* ks, const float (&qf)[16], int li, int g,
                                                  f32x4v (&st)[4]) {
+    const int kr = att_key(li), ksw = att_swz(kr);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         f32x4v kv[NT];
 #pragma unroll
         for (int t = 0; t < NT; ++t)
-            kv[t] = *reinterpret_cast<const f32x4v*>(&ks[(16 * t + li) * kDk + 4 * ((4 * g + c) ^ li)]);
+            kv[t] = *reinterpret_cast<const f32x4v*>(&ks[(16 * t + kr) * kDk + 4 * ((4 * g + c) ^ ksw)]);
 #pragma unroll
         for (int e = 0; e < 4; ++e)
 #pragma unroll
@@ -548,7 +565,7 @@ __device__ __forceinline__ void attention_scores(const float* ks, const float (&
 }
 
 // O^T += V^T P^T over key subtiles t < NT of the tile in `vs`: product j,
-// A = V^T (d 4 li + j, key 16t + 4g + r), B = P^T (in registers).
+// A = V^T (d 4 li + j, key 16t + att_key(4g + r)), B = P^T (in registers).
 template <int NT>
 __device__ __forceinline__ void attention_pv(const float* vs, const f32x4v (&st)[4], int li, int g, f32x4v (&o)[4]) {
 #pragma unroll
@@ -556,7 +573,8 @@ __device__ __forceinline__ void attention_pv(const float* vs, const f32x4v (&st)
         f32x4v va[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-            va[r] = *reinterpret_cast<const f32x4v*>(&vs[(16 * t + 4 * g + r) * kDk + 4 * (li ^ (4 * g + r))]);
+            va[r] = *reinterpret_cast<const f32x4v*>(
+                &vs[(16 * t + att_key(4 * g + r)) * kDk + 4 * (li ^ att_swz(att_key(4 * g + r)))]);
 #pragma unroll
         for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -626,7 +644,7 @@ __global__ __launch_bounds__(256, 3) void attention_mfma_kernel(const float* __r
         __syncthreads();
         attention_tile_dma(rsrc, vs, k0, row_bytes, vcol, wave, lane);
 
-        // S^T = K Q^T, 4 subtiles of 16 keys: st[t][r] = score of key 16t + 4g + r.
+        // S^T = K Q^T, 4 subtiles of 16 keys: st[t][r] = score of key 16t + att_key(4g + r).
         f32x4v st[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) st[t] = f32x4v{0.f, 0.f, 0.f, 0.f};
@@ -641,7 +659,7 @@ __global__ __launch_bounds__(256, 3) void attention_mfma_kernel(const float* __r
             for (int t = 0; t < 4; ++t)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int key = k0 + 16 * t + 4 * g + r;
+                    const int key = k0 + 16 * t + att_key(4 * g + r);
                     st[t][r] = ((CAUSAL && key > q) || key >= T) ? -3.0e38f : st[t][r];
                 }
         }
