@@ -106,6 +106,9 @@ def time_kernel(fn, steps, warmup, tag=None, min_warm_ms=None):
     return e0.elapsed_ms(e1) / steps
 
 
+GRAPH_TIMING = True  # False (--no-graph-timing): time_graph times a stream of calls instead
+
+
 def time_graph(call, steps, reps=15):
     """Microseconds per call of `steps` dependent calls of call() recorded
     once as a HIP graph on the library stream (kh_graph_*), the median over
@@ -114,9 +117,23 @@ def time_graph(call, steps, reps=15):
     few microseconds the per-call cost of issuing them from Python (a ctypes
     call and a launch) is as large as the kernel, and a host-side pause
     inside a short timed loop shows up in the average.  call() must have run
-    before (scratch sized, pool warm) and must not synchronize."""
+    before (scratch sized, pool warm) and must not synchronize.
+
+    With GRAPH_TIMING off (the profiler runs: rocprofv3's kernel trace
+    crashed inside hipGraphLaunch on these graphs of short kernels, and the
+    profiles read kernel durations, not this figure) it returns the mean
+    over `steps` calls issued from Python between HIP events."""
     import ctypes
     from kansaiml_amd import _native as N
+    if not GRAPH_TIMING:
+        N.synchronize()
+        e0, e1 = N.Event(), N.Event()
+        e0.record()
+        for _ in range(steps):
+            call()
+        e1.record()
+        N.synchronize()
+        return e0.elapsed_ms(e1) / steps * 1e3
     N.synchronize()
     N.call("kh_graph_capture_begin")
     try:
@@ -548,7 +565,7 @@ _GEMM_ARGS = "--only gemm --steps 3 --warmup 1 --no-cpu --warm-ms 0"
 _C4_ARGS = "--only c4 --steps 4 --warmup 2 --no-cpu --warm-ms 0"
 _TRAFFIC_ARGS = "--only gemm,quant,f32,copy --steps 3 --warmup 1 --no-cpu --warm-ms 0"
 PROFILE_RUNS = {
-    "trace": ("--kernel-trace --stats", "--no-cpu --warm-ms 10"),
+    "trace": ("--kernel-trace --stats", "--no-cpu --warm-ms 10 --no-graph-timing"),
     "fetch": ("--pmc FETCH_SIZE", _TRAFFIC_ARGS),
     "write": ("--pmc WRITE_SIZE", _TRAFFIC_ARGS),
     "gemm_p1": ("--pmc SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_VALU_MFMA_BUSY_CYCLES SQ_WAIT_ANY SQ_WAIT_INST_ANY "
@@ -565,7 +582,7 @@ PROFILE_RUNS = {
     "c4_p4": ("--pmc WRITE_SIZE", _C4_ARGS),
 }
 for _M, _K, _N in C5_ROWS:
-    _row = f"--only skinny --c5-rows {_M}:{_K}:{_N} --steps 20 --warmup 3 --no-cpu --warm-ms 0"
+    _row = f"--only skinny --c5-rows {_M}:{_K}:{_N} --steps 20 --warmup 3 --no-cpu --warm-ms 0 --no-graph-timing"
     PROFILE_RUNS[f"c5_{_M}_{_K}_{_N}_fetch"] = ("--pmc FETCH_SIZE", _row)
     PROFILE_RUNS[f"c5_{_M}_{_K}_{_N}_write"] = ("--pmc WRITE_SIZE", _row)
     PROFILE_RUNS[f"c5_{_M}_{_K}_{_N}_l2"] = ("--pmc TCP_TCC_READ_REQ_sum TCC_HIT_sum TCC_MISS_sum "
@@ -1071,7 +1088,7 @@ def cpu_c5(rows, budget_s=0.6):
 
 
 def main():
-    global WARM_MS
+    global WARM_MS, GRAPH_TIMING
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
@@ -1086,6 +1103,8 @@ def main():
                     help="minimum untimed warm-up per leg in ms (0 under counter runs, which serialise dispatches)")
     ap.add_argument("--profile-commands", metavar="DIR",
                     help="print the rocprofv3 commands whose output --summarize reads, and exit")
+    ap.add_argument("--no-graph-timing", action="store_true",
+                    help="time C1 and C5 from Python-issued calls only (for profiler runs)")
     ap.add_argument("--c5-rows", default=None,
                     help="C5 rows to run as M:K:N,... (default: all six); for per-row counter runs")
     args = ap.parse_args()
@@ -1097,6 +1116,7 @@ def main():
             print(profile_command(name, args.profile_commands))
         return
     WARM_MS = args.warm_ms
+    GRAPH_TIMING = not args.no_graph_timing
     only = set(args.only.split(","))
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only: the int8 path has no multi-GPU leg "
