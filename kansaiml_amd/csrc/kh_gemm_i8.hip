@@ -193,13 +193,6 @@ __device__ __forceinline__ unsigned store_block32_full(const Epilogue& ep, int64
     const int64_t j = colblk + fr;
     const double sbj = ep.sb ? ep.sb[ep.sb_per_col ? j : 0] : 0.0;
     const double s = sa * sbj;
-    double srow[ROWSA ? 16 : 1];
-    if constexpr (ROWSA) {
-        // value r of this lane is row rowblk + 4*fh + 8*(r/4) + r%4
-        const double* sar = ep.sa + rowblk + 4 * fh;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) srow[r] = sar[8 * (r >> 2) + (r & 3)] * sbj;
-    }
     const int64_t base = rowblk * N + colblk;
     const uint32_t span = (uint32_t)N * 32u * 4u;  // the block's 32 rows, in bytes
     const int voff = (4 * fh * N + fr) * 4;
@@ -211,8 +204,24 @@ __device__ __forceinline__ unsigned store_block32_full(const Epilogue& ep, int64
         for (int r = 0; r < 16; ++r) res[r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rr, voff, row_off(r), 0));
     }
     float y[16];
+    if constexpr (ROWSA) {
+        // Value r of this lane is row rowblk + 4*fh + 8*(r/4) + r%4: four
+        // row scales at a time (sa[i] * sb[j], then the product), so only
+        // four binary64 scales are live at once.
+        const double* sar = ep.sa + rowblk + 4 * fh;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) y[r] = (float)((double)v[r] * (ROWSA ? srow[ROWSA ? r : 0] : s));
+        for (int g = 0; g < 4; ++g) {
+            double s4[4];
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) s4[rr] = sar[8 * g + rr] * sbj;
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) y[4 * g + rr] = (float)((double)v[4 * g + rr] * s4[rr]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) y[r] = (float)((double)v[r] * s);
+    }
     if (ep.bias) {
         const float bj = ep.bias[j];
 #pragma unroll
@@ -439,17 +448,20 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_i8_kernel(const int8_t* __r
 // ---------------------------------------------------------------------------
 using namespace kh::pipe;
 
-// FUSED: the epilogue may apply an activation and a residual add.  FAST: the
-// launch guarantees full tiles, no int32 output, a per-tensor activation
-// scale and N <= 2^24, so only store_block32_full is compiled in.  Waves per
+// FUSED: the epilogue may apply an activation and a residual add.  EPI:
+// kEpiGeneral, every epilogue path; kEpiFull / kEpiFullRows, the launch
+// guarantees full tiles, no int32 output and N <= 2^24 with a per-tensor /
+// per-row activation scale, so only that store_block32_full is compiled in.  Waves per
 // SIMD: 2 for 256-wide N tiles (128 accumulators per wave); 4 for the
 // 256x128 tile; 6 (three resident workgroups per CU, 80 registers) for the
 // 128x128 tile unless the general fused epilogue is compiled in, which needs 4
 // (128 registers: its per-element residual and masking paths spill heavily
 // at 80).  At K = 384 the third workgroup's main loop covers the other two's
 // epilogues.
-template <int BM, int BN, int NS, bool FUSED, int MODE = kh::quant::kOutStore, bool FAST = false>
-__global__ __launch_bounds__(512, BN == 256 ? 2 : ((BM == 256 || (FUSED && !FAST)) ? 4 : 6)) void gemm_i8_pingpong_kernel(
+constexpr int kEpiGeneral = 0, kEpiFull = 1, kEpiFullRows = 2;
+
+template <int BM, int BN, int NS, bool FUSED, int MODE = kh::quant::kOutStore, int EPI = kEpiGeneral>
+__global__ __launch_bounds__(512, BN == 256 ? 2 : ((BM == 256 || NS >= 4 || (FUSED && EPI == kEpiGeneral)) ? 4 : 6)) void gemm_i8_pingpong_kernel(
     const int8_t* __restrict__ A, const int8_t* __restrict__ B, int M, int N, int K, int group_m, Epilogue ep,
     unsigned* parts) {
     constexpr int BK = 64, WM = 2, WN = 4, kWaves = WM * WN;
@@ -584,14 +596,16 @@ __global__ __launch_bounds__(512, BN == 256 ? 2 : ((BM == 256 || (FUSED && !FAST
     const int64_t col_base = (int64_t)tn * BN + wn * kWaveN + fr;
     unsigned mx = 0;
     const bool full = rows_a == BM && rows_b == BN;
-    if constexpr (FAST) {
+    if constexpr (EPI != kEpiGeneral) {
+        constexpr bool kRows = EPI == kEpiFullRows;
+        const double sa = kRows ? 0.0 : ep.sa[0];
 #pragma unroll
         for (int a = 0; a < kTM; ++a)
 #pragma unroll
             for (int b = 0; b < kTN; ++b) {
-                mx = max(mx, store_block32_full<FUSED, MODE>(ep, (int64_t)tm * BM + wm * kWaveM + a * 32,
-                                                             (int64_t)tn * BN + wn * kWaveN + b * 32, N, lane,
-                                                             ep.sa[0], acc[a][b], sc));
+                mx = max(mx, store_block32_full<FUSED, MODE, kRows>(ep, (int64_t)tm * BM + wm * kWaveM + a * 32,
+                                                                    (int64_t)tn * BN + wn * kWaveN + b * 32, N,
+                                                                    lane, sa, acc[a][b], sc));
                 __builtin_amdgcn_sched_barrier(0);
             }
     } else if (full && !ep.acc && !ep.sa_per_row && (MODE != kh::quant::kOutStore || ep.out) && N <= (1 << 24)) {
@@ -833,25 +847,37 @@ int launch_pingpong_cfg(kh::Device* d, const int8_t* A, const int8_t* B, int64_t
     // (8192^3: 2320 TOPS against 2230-2260 with 4-8 rows and 2030 with 1 or
     // 32), 8 elsewhere (no measurable difference at C4's shapes).
     constexpr int group_m = (BM == 256 && BN == 256) ? 2 : 8;
-    // Every tile full and the common epilogue: the FAST kernels.
-    const bool fast = M % BM == 0 && N % BN == 0 && N <= (1 << 24) && !ep.acc && !ep.sa_per_row &&
-                      (mode != kOutStore || ep.out) && (mode != kOutQuant || kh::aligned(ep.q, 4));
+    // Every tile full and the common epilogues: the full-tile kernels.
+    const bool full = M % BM == 0 && N % BN == 0 && N <= (1 << 24) && !ep.acc;
+    const bool fast = full && !ep.sa_per_row && (mode != kOutStore || ep.out) &&
+                      (mode != kOutQuant || kh::aligned(ep.q, 4));
+    const bool fast_rows = full && ep.sa_per_row && mode == kOutStore && ep.out;
     if (fast) {
         if constexpr (BM == 128 && BN == 128) {
             if (mode == kOutMaxOnly)
-                gemm_i8_pingpong_kernel<BM, BN, NS, true, kOutMaxOnly, true>
+                gemm_i8_pingpong_kernel<BM, BN, NS, true, kOutMaxOnly, kEpiFull>
                     <<<tiles, 512, 0, d->stream>>>(A, B, (int)M, (int)N, (int)K, group_m, ep, parts);
             else if (mode == kOutQuant)
-                gemm_i8_pingpong_kernel<BM, BN, NS, true, kOutQuant, true>
+                gemm_i8_pingpong_kernel<BM, BN, NS, true, kOutQuant, kEpiFull>
                     <<<tiles, 512, 0, d->stream>>>(A, B, (int)M, (int)N, (int)K, group_m, ep, nullptr);
         }
         if (mode != kOutStore) {
             // launched above (launch_pingpong routes the quantize passes to the 128x128 tile)
         } else if (ep.act != kActNone || ep.residual)
-            gemm_i8_pingpong_kernel<BM, BN, NS, true, kOutStore, true>
+            gemm_i8_pingpong_kernel<BM, BN, NS, true, kOutStore, kEpiFull>
                 <<<tiles, 512, 0, d->stream>>>(A, B, (int)M, (int)N, (int)K, group_m, ep, parts);
         else
-            gemm_i8_pingpong_kernel<BM, BN, NS, false, kOutStore, true>
+            gemm_i8_pingpong_kernel<BM, BN, NS, false, kOutStore, kEpiFull>
+                <<<tiles, 512, 0, d->stream>>>(A, B, (int)M, (int)N, (int)K, group_m, ep, parts);
+        if (nparts) *nparts = (int)tiles;
+        return kh::launch_status("gemm_i8_pingpong");
+    }
+    if (fast_rows) {
+        if (ep.act != kActNone || ep.residual)
+            gemm_i8_pingpong_kernel<BM, BN, NS, true, kOutStore, kEpiFullRows>
+                <<<tiles, 512, 0, d->stream>>>(A, B, (int)M, (int)N, (int)K, group_m, ep, parts);
+        else
+            gemm_i8_pingpong_kernel<BM, BN, NS, false, kOutStore, kEpiFullRows>
                 <<<tiles, 512, 0, d->stream>>>(A, B, (int)M, (int)N, (int)K, group_m, ep, parts);
         if (nparts) *nparts = (int)tiles;
         return kh::launch_status("gemm_i8_pingpong");
