@@ -218,6 +218,22 @@ int kh_gemm_i8_quant(const int8_t* a, const int8_t* b_packed, int64_t M, int64_t
                      const double* sa, int sa_per_row, const double* sb, int sb_per_col,
                      const float* bias, int act, const float* residual, int8_t* q, double* scale);
 
+/* The per-tensor quantize of an fp32 activation fused into the GEMM that
+ * consumes it: kh_quantize_tensor_parts(x, x_parts) (quantize.py:50-70 on
+ * the activation, with the absmax partials its producer wrote) followed by
+ * kh_gemm_i8_ex(codes, b_packed, sa = that scale, ...) (qlinear's int8
+ * matmul and dequantize, quantize.py:115-144, with the fused bias / GELU /
+ * residual), without the codes ever being written.  x fp32 [M, K] (16-byte
+ * aligned for the fused kernel); x_parts: the producer's partials (at least
+ * one); x_scale (may be NULL) receives the activation's binary64 scale;
+ * absmax_parts as kh_gemm_i8_ex.  The same outputs as the two calls (other
+ * shapes run them).  A NaN/inf in x reports KH_ERR_NONFINITE at the next
+ * synchronize, as kh_quantize_tensor_parts does. */
+int kh_gemm_i8_qload(const float* x, int64_t M, int64_t N, int64_t K, const unsigned* x_parts, int x_nparts,
+                     const int8_t* b_packed, const double* sb, int sb_per_col, const float* bias, int act,
+                     const float* residual, float* out, double* x_scale, unsigned* absmax_parts, int max_parts,
+                     int* nparts);
+
 /* Per-token activation quantize fused into the GEMM's producer: x fp32
  * [M, K] is quantized per row into q_scratch (int8 [M, K]) and
  * sx_scratch (binary64 [M]), then kh_gemm_i8 runs with sa = sx_scratch

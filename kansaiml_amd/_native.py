@@ -74,6 +74,8 @@ _SIGNATURES = {
     "kh_gemm_i8_ex": [_vp, _vp, _i64, _i64, _i64, _vp, _int, _vp, _int, _vp, _int, _vp, _vp, _vp, _int,
                       ctypes.POINTER(ctypes.c_int)],
     "kh_gemm_i8_quant": [_vp, _vp, _i64, _i64, _i64, _vp, _int, _vp, _int, _vp, _int, _vp, _vp, _vp],
+    "kh_gemm_i8_qload": [_vp, _i64, _i64, _i64, _vp, _int, _vp, _vp, _int, _vp, _int, _vp, _vp, _vp, _vp, _int,
+                         ctypes.POINTER(ctypes.c_int)],
     "kh_absmax_parts": [_vp, _i64, _vp, _int, ctypes.POINTER(ctypes.c_int)],
     "kh_quantize_tensor_parts": [_vp, _i64, _vp, _int, _vp, _vp],
     "kh_layernorm_ex": [_vp, _i64, _int, _vp, _vp, ctypes.c_float, _vp, _vp, _int, ctypes.POINTER(ctypes.c_int)],

@@ -113,11 +113,16 @@ class CharLM:
     one (or a float32 checkpoint, quantized per output channel on the way)
     into it in place.  `w` stays the construction-time weights."""
 
-    def __init__(self, w: CharLMWeights, producer_quant: bool | str = "layer_norm", act_granularity: str = "tensor"):
+    def __init__(self, w: CharLMWeights, producer_quant: bool | str = "layer_norm", act_granularity: str = "tensor",
+                 qload: bool = False):
         """producer_quant (kir.quant_fusion's option): "layer_norm" (the
         default) -- each LayerNorm emits its int8 codes directly instead of
         fp32 (two passes over its input; the fastest on MI355X); True -- fc1
         (-> GELU) as well (less memory, slower); False -- neither.
+        qload (kir.quant_fusion's option): the remaining per-tensor
+        quantizes (of the attention and fc1 outputs) run inside the GEMM
+        that consumes them (kh_gemm_i8_qload), so their codes are never
+        written.
         act_granularity: "tensor" (the reference's quantize_symmetric over the
         whole activation, the C4 configuration) or "row" (one scale per token;
         a LayerNorm then emits codes and scales in one pass)."""
@@ -126,6 +131,7 @@ class CharLM:
         self.w = w
         self.producer_quant = producer_quant
         self.act_granularity = act_granularity
+        self.qload = qload
         up = DeviceTensor.from_host
         self.tok, self.pos = up(w.tok), up(w.pos)
         self.blocks = []
@@ -189,7 +195,7 @@ class CharLM:
         key = (batch, seq)
         if key not in self._graphs:
             g = kir.quant_fusion(kir.trace(self._fn(batch, seq), np.zeros((batch, seq), np.int32)),
-                                 producer_quant=self.producer_quant)
+                                 producer_quant=self.producer_quant, qload=self.qload)
             self._graphs[key] = (g, kir.plan_memory(g))
         return self._graphs[key]
 

@@ -35,6 +35,7 @@ namespace {
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
 struct Epilogue {
     const double* sa;
@@ -664,6 +665,154 @@ __global__ __launch_bounds__(512, BN == 256 ? 2 : ((BM == 256 || NS >= 4 || (FUS
 }
 
 // ---------------------------------------------------------------------------
+// Quantize-on-load GEMM: out = epilogue(quantize_tensor(X) . B^T) for fp32 X
+// [M, K] whose per-tensor scale comes from the absmax partials its producer
+// wrote.  The codes of X are made in the main loop and never stored: where the
+// two-step path reads X (4 bytes per value), writes its codes (1) and reads
+// them back once per N-tile (1 each), this reads X once.
+//
+// * Workgroup tile kQlBM = 64 rows x BN = 128 NB columns (C4's N = 384 in one
+//   tile, so X is read once); 8 waves as 2 (M) x 4 (N), each 32 x 32 NB
+//   outputs (NB blocks of v_mfma_i32_32x32x32_i8).
+// * K in steps of 64 through a ring of NS LDS stages, each A codes 64 x 64
+//   and B codes BN x 64 in the ping-pong kernel's layout (64-byte rows, chunk
+//   c of row r at slot c ^ ((r >> 2) & 3)).  B arrives by LDS-DMA.  For A,
+//   thread t loads 8 floats of row t / 8 (two 16-byte loads, D = NS - 1 steps
+//   ahead, into a register ring), quantizes them with the shared element
+//   arithmetic (pack4: the fast path, the exact binary64 path where it is not
+//   decisive) and writes the 8 codes to the stage (ds_write_b64).
+// * Per step: wait for this wave's loads of the step, quantize and write A,
+//   barrier (publishes A and B of the step; every read of the stage that the
+//   next loads refill is done), issue the loads of step k + D, read the
+//   fragments and multiply.
+// * Epilogue: store_block32_full with the tensor's scale as the per-tensor
+//   activation scale -- the same values as kh_quantize_tensor_parts followed
+//   by kh_gemm_i8_ex.
+// ---------------------------------------------------------------------------
+constexpr int kQlBM = 64;
+
+template <int NB, int NS, bool FUSED>
+__global__ __launch_bounds__(512, 2) void gemm_i8_qload_kernel(const float* __restrict__ X, int M, int N, int K,
+                                                               const unsigned* __restrict__ xparts, int nxparts,
+                                                               const int8_t* __restrict__ B, Epilogue ep,
+                                                               unsigned* parts) {
+    using kh::quant::f32x4;
+    constexpr int BK = 64, BN = 128 * NB, WN = 4, kWaves = 8, D = NS - 1;
+    constexpr int kLdsA = kQlBM * BK;
+    constexpr int kStage = kLdsA + BN * BK;
+    constexpr int kBInst = BN / 16 / kWaves;  // 1 KB = 16 rows per LDS-DMA instruction
+    constexpr int kLoads = kBInst + 2;        // loads per wave per stage
+    static_assert(NS >= 2 && NS <= 5, "wait_loads_beyond covers up to 3 stages ahead");
+    __shared__ __attribute__((aligned(1024))) int8_t lds[NS * kStage];
+    __shared__ unsigned red[kWaves];
+
+    // The tensor's scale (quantize.py:67-68), the same in every workgroup.
+    const kh::quant::Scale sc = kh::quant::make_scale(kh::quant::block_reduce_partials(xparts, nxparts, red));
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        if (ep.qscale) *ep.qscale = sc.s;
+        if (sc.bad) kh::quant::flag_nonfinite(ep.fault);
+    }
+
+    const int tiles_n = N / BN;
+    const int tm = blockIdx.x / tiles_n, tn = blockIdx.x - tm * tiles_n;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WN, wn = wave % WN;
+    auto swz = [](int r) { return (r >> 2) & 3; };
+
+    // A: 8 floats of row t / 8 at k = 8 (t % 8) of each step; their codes go
+    // to bytes 8 (t % 2) of chunk (t % 8) / 2.
+    const int arow = tid >> 3, aq = tid & 7;
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(X + (int64_t)tm * kQlBM * K, (uint32_t)kQlBM * (uint32_t)K * 4u);
+    const int a_voff = (arow * K + aq * 8) * 4;
+    const int a_lds = arow * BK + (((aq >> 1) ^ swz(arow)) << 4) + 8 * (aq & 1);
+    // B: instruction i of this wave fills rows (wave kBInst + i) 16 + l / 4,
+    // slot chunk l % 4 (the ping-pong kernel's LDS-DMA).
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(B + (int64_t)tn * BN * K, (uint32_t)BN * (uint32_t)K);
+    const int lr = lane >> 2, lc = lane & 3;
+    int b_voff[kBInst];
+#pragma unroll
+    for (int i = 0; i < kBInst; ++i) {
+        const int r = (wave * kBInst + i) * 16 + lr;
+        b_voff[i] = r * K + ((lc ^ swz(r)) << 4);
+    }
+    auto issue = [&](int kt, f32x4 (&xa)[2]) {
+        int8_t* base = lds + (kt % NS) * kStage + kLdsA;
+#pragma unroll
+        for (int i = 0; i < kBInst; ++i) lds_dma16(rb, base + (wave * kBInst + i) * 1024, b_voff[i], kt * BK);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            xa[h] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, a_voff + 16 * h, kt * BK * 4, 0));
+    };
+
+    // Fragments (as the ping-pong kernel): lane l reads 16 bytes of row
+    // r + l % 32 at chunk 2s + l / 32.
+    const int fr = lane & 31, fh = lane >> 5;
+    const int ar = wm * 32 + fr;
+    const int a_off = ar * BK + ((fh ^ swz(ar)) << 4);
+    int b_off[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int r = wn * 32 * NB + b * 32 + fr;
+        b_off[b] = kLdsA + r * BK + ((fh ^ swz(r)) << 4);
+    }
+    i32x16 acc[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[b] = i32x16{0};
+
+    const int nk = K / BK;
+    f32x4 xa[D][2];
+#pragma unroll
+    for (int s = 0; s < D; ++s)
+        if (s < nk) issue(s, xa[s]);
+    for (int k0 = 0; k0 < nk; k0 += D) {
+#pragma unroll
+        for (int j = 0; j < D; ++j) {
+            const int k = k0 + j;
+            if (k >= nk) break;
+            int8_t* stage = lds + (k % NS) * kStage;
+            wait_loads_beyond<kLoads>(min(D - 1, nk - 1 - k));  // this wave's A and B of step k landed
+            const unsigned c0 = kh::quant::pack4(xa[j][0], sc), c1 = kh::quant::pack4(xa[j][1], sc);
+            *reinterpret_cast<u32x2*>(stage + a_lds) = u32x2{c0, c1};
+            __builtin_amdgcn_s_waitcnt(wait_imm(63, 0));
+            __builtin_amdgcn_s_barrier();
+            if (k + D < nk) issue(k + D, xa[j]);
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                const i32x4 fa = *reinterpret_cast<const i32x4*>(stage + (a_off ^ (s << 5)));
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+                    const i32x4 fb = *reinterpret_cast<const i32x4*>(stage + (b_off[b] ^ (s << 5)));
+                    acc[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa, fb, acc[b], 0, 0, 0);
+                }
+            }
+        }
+    }
+
+    unsigned mx = 0;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        mx = max(mx, store_block32_full<FUSED, kh::quant::kOutStore>(ep, (int64_t)tm * kQlBM + wm * 32,
+                                                                      (int64_t)tn * BN + wn * 32 * NB + b * 32, N,
+                                                                      lane, sc.s, acc[b], sc));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (parts) {
+        // Per-workgroup max |out| bits, for a following per-tensor quantize.
+        mx = kh::quant::wave_max(mx);
+        __syncthreads();  // red's scale reduction is read by every wave before this point
+        if (lane == 0) red[wave] = mx;
+        __syncthreads();
+        if (tid == 0) {
+            unsigned m = red[0];
+#pragma unroll
+            for (int w = 1; w < kWaves; ++w) m = max(m, red[w]);
+            parts[blockIdx.x] = m;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Skinny GEMM for decode-style and small shapes (M <= 64): weight streaming.
 //
 // A workgroup owns 16 output columns for all M rows; its SKW waves split K,
@@ -1137,6 +1286,30 @@ bool decode_fits(const float* x, int64_t M, int64_t K, const int8_t* B, int64_t 
            (N + 16) * K <= 0xFFFFFFFFLL && kh::aligned(x, 16) && kh::aligned(B, 16) && kh::aligned(q, 4);
 }
 
+// NB (128-column blocks per tile) of the quantize-on-load kernel for this
+// shape, 0 when it does not take it: M a multiple of 64, N = 128, 256 or a
+// multiple of 384, K of 64, 16-byte aligned X and B, 32-bit offsets.
+int qload_nb(const float* x, const int8_t* b, int64_t M, int64_t N, int64_t K) {
+    if (M <= 0 || M % kQlBM || N <= 0 || K <= 0 || K % 64 || !kh::aligned(x, 16) || !kh::aligned(b, 16)) return 0;
+    if ((int64_t)kQlBM * K * 4 > 0xFFFFFFFFLL || 384 * K > 0x7FFFFFFFLL || M > 0x7FFFFFFFLL) return 0;
+    if ((M / kQlBM) * (N / 128) > 0x7FFFFFFFLL) return 0;
+    if (N == 128 || N == 256) return (int)(N / 128);
+    return N % 384 == 0 ? 3 : 0;
+}
+
+template <int NB>
+int launch_qload(kh::Device* d, const float* x, int64_t M, int64_t N, int64_t K, const unsigned* xparts,
+                 int nxparts, const int8_t* b, const Epilogue& ep, unsigned* parts) {
+    const unsigned grid = (unsigned)((M / kQlBM) * (N / (128 * NB)));
+    if (ep.act != kActNone || ep.residual)
+        gemm_i8_qload_kernel<NB, 5, true><<<grid, 512, 0, d->stream>>>(x, (int)M, (int)N, (int)K, xparts, nxparts, b,
+                                                                       ep, parts);
+    else
+        gemm_i8_qload_kernel<NB, 5, false><<<grid, 512, 0, d->stream>>>(x, (int)M, (int)N, (int)K, xparts, nxparts,
+                                                                        b, ep, parts);
+    return kh::launch_status("gemm_i8_qload");
+}
+
 }  // namespace
 
 extern "C" {
@@ -1233,6 +1406,69 @@ int kh_gemm_i8_quant(const int8_t* a, const int8_t* b_packed, int64_t M, int64_t
     if (!rc) rc = kh_quantize_tensor(out, M * N, q, scale);
     kh_free(tmp);  // stream-ordered reuse: later work is queued behind the quantize
     return rc;
+}
+
+int kh_gemm_i8_qload(const float* x, int64_t M, int64_t N, int64_t K, const unsigned* x_parts, int x_nparts,
+                     const int8_t* b_packed, const double* sb, int sb_per_col, const float* bias, int act,
+                     const float* residual, float* out, double* x_scale, unsigned* absmax_parts, int max_parts,
+                     int* nparts) {
+    KH_REQUIRE(M >= 0 && N >= 0 && K >= 0, "kh_gemm_i8_qload: negative shape");
+    KH_REQUIRE(K <= 133144, "kh_gemm_i8_qload: K > 133144 could overflow the int32 accumulator");
+    KH_REQUIRE(M <= 0xFFFFLL * 128 && N <= 0x7FFFFFFFLL, "kh_gemm_i8_qload: shape too large");
+    KH_REQUIRE(act == kActNone || act == kActGelu, "kh_gemm_i8_qload: unknown activation");
+    KH_REQUIRE(x_parts && x_nparts > 0, "kh_gemm_i8_qload: the producer's absmax partials are required");
+    KH_REQUIRE(!absmax_parts || (nparts && max_parts > 0), "kh_gemm_i8_qload: partials need max_parts and nparts");
+    if (nparts) *nparts = 0;
+    KH_DEVICE_OR_RETURN(d);
+    if (M * K == 0) {
+        // An empty X quantizes with scale 1.0 (quantize.py:68); the product is zero.
+        void* tmp = nullptr;
+        int rc = x_scale ? KH_OK : kh_alloc(sizeof(double), &tmp);
+        if (rc) return rc;
+        double* sc = x_scale ? x_scale : static_cast<double*>(tmp);
+        const double one = 1.0;
+        rc = kh_memcpy_h2d(sc, &one, sizeof(one));
+        if (!rc && M && N)
+            rc = kh_gemm_i8_ex(nullptr, b_packed, M, N, 0, sc, 0, sb, sb_per_col, bias, act, residual, out,
+                               absmax_parts, max_parts, nparts);
+        const int frc = tmp ? kh_free(tmp) : KH_OK;
+        return rc ? rc : frc;
+    }
+    if (N == 0) {
+        // Nothing to multiply; the scale is still the tensor's.
+        if (!x_scale) return KH_OK;
+        void* tmp = nullptr;
+        int rc = kh_alloc((size_t)(M * K), &tmp);
+        if (rc) return rc;
+        rc = kh_quantize_tensor_parts(x, M * K, x_parts, x_nparts, static_cast<int8_t*>(tmp), x_scale);
+        const int frc = kh_free(tmp);
+        return rc ? rc : frc;
+    }
+    KH_REQUIRE(x && b_packed && sb && out, "kh_gemm_i8_qload: null pointer");
+    const int nb = qload_nb(x, b_packed, M, N, K);
+    const int64_t grid = nb ? (M / kQlBM) * (N / (128 * nb)) : 0;
+    if (nb && (!absmax_parts || grid <= max_parts)) {
+        Epilogue ep{nullptr, sb, bias, out, nullptr, 0, sb_per_col, act, residual, nullptr, nullptr, 0, x_scale,
+                    d->fault};
+        int rc = nb == 1   ? launch_qload<1>(d, x, M, N, K, x_parts, x_nparts, b_packed, ep, absmax_parts)
+                 : nb == 2 ? launch_qload<2>(d, x, M, N, K, x_parts, x_nparts, b_packed, ep, absmax_parts)
+                           : launch_qload<3>(d, x, M, N, K, x_parts, x_nparts, b_packed, ep, absmax_parts);
+        if (!rc && absmax_parts) *nparts = (int)grid;
+        return rc;
+    }
+    // Other shapes: the codes (and the scale, when the caller wants none)
+    // through a pooled temporary, then the GEMM.
+    void* tmp = nullptr;
+    int rc = kh_alloc((size_t)(M * K) + 8, &tmp);
+    if (rc) return rc;
+    double* sc = x_scale ? x_scale : static_cast<double*>(tmp);
+    int8_t* q = static_cast<int8_t*>(tmp) + 8;
+    rc = kh_quantize_tensor_parts(x, M * K, x_parts, x_nparts, q, sc);
+    if (!rc)
+        rc = kh_gemm_i8_ex(q, b_packed, M, N, K, sc, 0, sb, sb_per_col, bias, act, residual, out, absmax_parts,
+                           max_parts, nparts);
+    const int frc = kh_free(tmp);  // stream-ordered reuse: later work is queued behind the GEMM
+    return rc ? rc : frc;
 }
 
 // kh_linear_i8's work with the codes and scales in q_scratch / sx_scratch.

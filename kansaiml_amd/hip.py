@@ -323,6 +323,43 @@ def gemm_i8_quant(a: DeviceTensor, b_packed: DeviceTensor, sa: DeviceTensor, sb:
     return q, s
 
 
+def gemm_i8_qload(x: DeviceTensor, parts: AbsmaxParts, b_packed: DeviceTensor, sb: DeviceTensor,
+                  bias: DeviceTensor | None = None, *, act: str | None = None,
+                  residual: DeviceTensor | None = None, absmax: bool = False, want_scale: bool = False):
+    """gemm_i8_fused(quantize_tensor_parts(x, parts)) without writing the
+    activation's codes: x fp32 [M, K] with the absmax partials its producer
+    wrote.  Returns (out, AbsmaxParts | None), plus the activation's scale
+    (float64 [1]) when want_scale."""
+    _need(x, "float32", 2, "gemm_i8_qload(x)")
+    _need(b_packed, "int8", 2, "gemm_i8_qload(b)")
+    if parts is None or parts.count <= 0:
+        raise RuntimeError("gemm_i8_qload: the producer wrote no partials")
+    M, K = x.shape
+    Nn, K2 = b_packed.shape
+    if K != K2:
+        raise RuntimeError(f"gemm_i8_qload: incompatible shapes {x.shape} x {b_packed.shape}^T")
+    if act not in ACTS:
+        raise ValueError(f"gemm_i8_qload: unknown activation {act!r}")
+    sb_mode = _scale_mode(sb, Nn, "gemm_i8_qload(sb)")
+    if bias is not None:
+        _need(bias, "float32", 1, "gemm_i8_qload(bias)")
+        if bias.shape[0] != Nn:
+            raise RuntimeError("gemm_i8_qload: bias must have N entries")
+    if residual is not None:
+        _need(residual, "float32", 2, "gemm_i8_qload(residual)")
+        if list(residual.shape) != [M, Nn]:
+            raise RuntimeError("gemm_i8_qload: residual must be [M, N]")
+    out = DeviceTensor([M, Nn], "float32")
+    scale = DeviceTensor([1], "float64") if want_scale else None
+    out_parts = AbsmaxParts() if absmax else None
+    N.call("kh_gemm_i8_qload", x.ptr, M, Nn, K, parts.buf.ptr, parts.count, b_packed.ptr, sb.ptr, sb_mode,
+           _opt(bias), ACTS[act], _opt(residual), out.ptr, _opt(scale), out_parts.buf.ptr if out_parts else None,
+           ABSMAX_PARTS if out_parts else 0, ctypes.byref(out_parts._n) if out_parts else None)
+    if want_scale:
+        return out, out_parts, scale
+    return out, out_parts
+
+
 def layer_norm_quant(x: DeviceTensor, w: DeviceTensor, b: DeviceTensor, eps: float = 1e-5):
     """quantize_tensor(layer_norm(x)) without writing the fp32 output:
     returns (codes int8 like x, scale float64 [1])."""

@@ -231,10 +231,12 @@ def _is_bias(graph, by_id, x_id, b_id) -> bool:
     return len(xs) == 2 and len(bs) == 1 and xs[1] == bs[0]
 
 
-def quant_fusion(graph, producer_quant: bool | str = False) -> Graph:
+def quant_fusion(graph, producer_quant: bool | str = False, qload: bool = False) -> Graph:
     """Fuses, where the intermediate has no other user:
       int8_matmul -> dequantize [-> add(bias)] [-> gelu] [-> add(x, .)]
                                                  =>  int8_linear
+      with qload=True, also the per-tensor quantize of its activation:
+      quantize -> int8_matmul -> ...             =>  int8_linear (qload)
       matmul -> add(bias)                        =>  matmul_bias
       add(bias) -> relu                          =>  fused_bias_relu
     and, with producer_quant=True (both) or "layer_norm" (the second only),
@@ -242,7 +244,9 @@ def quant_fusion(graph, producer_quant: bool | str = False) -> Graph:
       layer_norm -> quantize (per tensor)        =>  layer_norm_quant
       layer_norm -> quantize (per row)           =>  layer_norm_quant_rows
     int8_linear's attrs record what it absorbed: bias (bool), act ("gelu" or
-    None) and residual (bool; the residual operand comes last).  The *_quant
+    None), residual (bool; the residual operand comes last) and qload (bool:
+    operand 0 is the fp32 activation, quantized per tensor inside the GEMM,
+    kh_gemm_i8_qload, so its codes are never written).  The *_quant
     nodes produce the quantized tensor directly: their kernels run the
     producer twice (absmax, then codes) and never write the fp32 values.
     That saves the fp32 intermediate's memory; on MI355X it saves time for
@@ -265,6 +269,13 @@ def quant_fusion(graph, producer_quant: bool | str = False) -> Graph:
         u = users[nid]
         return u[0] if len(u) == 1 and nid != graph.output else None
 
+    def next_free(nid):
+        """The only user of nid, unless an earlier pattern already took it
+        (e.g. the add of two Linear outputs, claimed as the first one's
+        residual add)."""
+        u = only_user(nid)
+        return u if u is not None and u not in fused and u not in absorbed else None
+
     # Phase 1: find patterns.  fused[last] = (op, [operand ids], attrs);
     # absorbed nodes are dropped.
     fused, absorbed = {}, set()
@@ -286,21 +297,27 @@ def quant_fusion(graph, producer_quant: bool | str = False) -> Graph:
         if n.id in absorbed or n.id in fused:
             continue
         if n.op == "int8_matmul":
-            dq = only_user(n.id)
+            dq = next_free(n.id)
             if dq is not None and by_id[dq].op == "dequantize":
                 chain, ins, attrs = [n.id, dq], list(n.inputs), {"bias": False, "act": None, "residual": False}
-                nxt = only_user(dq)
+                qa = by_id[n.inputs[0]]
+                if (qload and qa.op == "quantize" and qa.attrs.get("granularity", "tensor") == "tensor"
+                        and only_user(qa.id) == n.id and qa.id not in fused):
+                    chain.insert(0, qa.id)
+                    ins[0] = qa.inputs[0]
+                    attrs["qload"] = True
+                nxt = next_free(dq)
                 if nxt is not None and by_id[nxt].op == "add":
                     a_in = by_id[nxt].inputs
                     if a_in[0] == dq and _is_bias(graph, by_id, dq, a_in[1]):
                         chain.append(nxt)
                         ins.append(a_in[1])
                         attrs["bias"] = True
-                        nxt = only_user(nxt)
+                        nxt = next_free(nxt)
                 if nxt is not None and by_id[nxt].op == "gelu":
                     chain.append(nxt)
                     attrs["act"] = "gelu"
-                    nxt = only_user(nxt)
+                    nxt = next_free(nxt)
                 if nxt is not None and by_id[nxt].op == "add":
                     a_in = by_id[nxt].inputs
                     other = a_in[1] if a_in[0] == chain[-1] else a_in[0]
@@ -310,7 +327,7 @@ def quant_fusion(graph, producer_quant: bool | str = False) -> Graph:
                         ins.append(other)
                         attrs["residual"] = True
                 last = chain[-1]
-                q = tensor_quantize(last)
+                q = tensor_quantize(last) if not attrs.get("qload") else None
                 if q is not None:
                     absorbed.update(chain)
                     fused[q] = ("int8_linear_quant", ins, attrs)
@@ -359,9 +376,11 @@ def quant_fusion(graph, producer_quant: bool | str = False) -> Graph:
     out.inputs = [remap[i] for i in graph.inputs]
     out.output = remap[graph.output]
 
-    # Phase 3: producers of a per-tensor quantize write its absmax partials.
+    # Phase 3: producers of a per-tensor quantize (or of a quantize fused
+    # into its int8_linear) write its absmax partials.
     for n in out.nodes:
-        if n.op == "quantize" and n.attrs.get("granularity", "tensor") == "tensor":
+        if ((n.op == "quantize" and n.attrs.get("granularity", "tensor") == "tensor")
+                or (n.op == "int8_linear" and n.attrs.get("qload"))):
             src = out.nodes[n.inputs[0]]
             if src.op in _ABSMAX_PRODUCERS:
                 src.attrs["absmax"] = True
@@ -516,6 +535,25 @@ def _exec(node, vals):
         a, b, sa, sb = _int8_operands(ins[0], ins[1], "int8_matmul")
         _, acc = H.gemm_i8(a, b, want_out=False, want_acc=True)
         return _Acc(acc, sa, sb)
+    if op == "int8_linear" and node.attrs.get("qload"):
+        from .quantize import QTensor
+        x, w = ins[0], ins[1]
+        if not isinstance(w, QTensor) or not w.packed:
+            raise TypeError("int8_linear: expects a packed quantized weight [K,N]")
+        at = node.attrs
+        bias = ins[2] if at.get("bias") else None
+        residual = ins[-1] if at.get("residual") else None
+        parts = getattr(x, "absmax_parts", None)
+        if parts is None:
+            q, s = H.quantize_tensor(x)
+            out, oparts = H.gemm_i8_fused(q, w.codes, s, w.scales, bias, act=at.get("act"), residual=residual,
+                                          absmax=bool(at.get("absmax")))
+            q.release()
+            s.release()
+        else:
+            out, oparts = H.gemm_i8_qload(x, parts, w.codes, w.scales, bias, act=at.get("act"), residual=residual,
+                                          absmax=bool(at.get("absmax")))
+        return _with_parts(out, oparts)
     if op == "int8_linear":
         a, b, sa, sb = _int8_operands(ins[0], ins[1], "int8_linear")
         at = node.attrs

@@ -176,6 +176,11 @@ def _check_node(node, got, ins):
         np.testing.assert_array_equal(got[0], q.reshape(got[0].shape))
         assert got[1][0] == s
     elif op == "int8_linear":
+        if node.attrs.get("qload"):
+            # the activation's per-tensor quantize ran inside the GEMM: the
+            # oracle's quantize of the same fp32 input
+            q, s = O.ko_quantize_tensor(ins[0])
+            ins = [(q.reshape(ins[0].shape), np.array([s]))] + list(ins[1:])
         (qa, sa), (qw, sw) = ins[0], ins[1]
         at = node.attrs
         bias = ins[2] if at.get("bias") else None
@@ -265,7 +270,7 @@ def test_small_model_matches_restatement(G, seq, producer_quant):
     from kansaiml_amd.charlm import CharLM, CharLMWeights
     w = CharLMWeights(layers=2, seq=128, seed=1, bias_std=0.02)
     ids = np.random.Generator(np.random.PCG64(2)).integers(0, 65, (2, seq)).astype(np.int32)
-    model = CharLM(w, producer_quant=producer_quant)
+    model = CharLM(w, producer_quant=producer_quant, qload=True)
     seen = {}
     y = model(ids, observe=lambda node, v: seen.__setitem__(node.id, (node, _host(v))))
     assert y.shape == (2 * seq, 65)
@@ -286,19 +291,25 @@ def test_small_model_matches_restatement(G, seq, producer_quant):
     # ("layer_norm": the LayerNorms only).
     acts = {(n.op, n.attrs.get("act"), bool(n.attrs.get("residual"))) for n in g.nodes
             if n.op in ("int8_linear", "int8_linear_quant")}
+    # The attention output's quantize (and fc1's, unless fc1 emits codes)
+    # runs inside the consuming GEMM (qload).
+    qloads = {by_id[n.inputs[0]].op for n in g.nodes if n.attrs.get("qload")}
     if producer_quant == "layer_norm":
-        assert checked == {"embedding", "layer_norm_quant", "quantize", "int8_linear", "attention"}
+        assert checked == {"embedding", "layer_norm_quant", "int8_linear", "attention"}
+        assert qloads == {"attention", "int8_linear"}
         assert acts == {("int8_linear", None, False), ("int8_linear", "gelu", False), ("int8_linear", None, True)}
         assert all(n.attrs.get("absmax") for n in g.nodes
                    if n.op == "attention" or (n.op == "int8_linear" and n.attrs.get("act")))
     elif producer_quant:
-        assert checked == {"embedding", "layer_norm_quant", "quantize", "int8_linear", "int8_linear_quant",
-                           "attention"}
+        assert checked == {"embedding", "layer_norm_quant", "int8_linear", "int8_linear_quant", "attention"}
+        assert qloads == {"attention"}
         assert acts == {("int8_linear", None, False), ("int8_linear_quant", "gelu", False),
                         ("int8_linear", None, True)}
         assert all(n.attrs.get("absmax") for n in g.nodes if n.op == "attention")
     else:
-        assert checked == {"embedding", "layer_norm", "quantize", "int8_linear", "attention"}
+        # the LayerNorm outputs' quantizes run inside QKV and fc1 as well
+        assert checked == {"embedding", "layer_norm", "int8_linear", "attention"}
+        assert qloads == {"attention", "int8_linear", "layer_norm"}
         assert acts == {("int8_linear", None, False), ("int8_linear", "gelu", False), ("int8_linear", None, True)}
         assert all(n.attrs.get("absmax") for n in g.nodes
                    if n.op in ("layer_norm", "attention") or (n.op == "int8_linear" and n.attrs.get("act")))
@@ -378,7 +389,14 @@ def _check_node_sampled(node, got, ins, gen, nrows=64, nbatches=3):
     rows only); LayerNorm on sampled rows."""
     op = node.op
     if op == "int8_linear":
+        from oracle import oracle as O
         rows = np.sort(gen.choice(got.shape[0], nrows, replace=False))
+        if node.attrs.get("qload"):
+            # the per-tensor scale depends on the whole input: quantize it all
+            q, s = O.ko_quantize_tensor(ins[0])
+            ins = [(q.reshape(ins[0].shape), np.array([s]))] + list(ins[1:])
+            node = type("N", (), {"op": "int8_linear",
+                                  "attrs": {k: v for k, v in node.attrs.items() if k != "qload"}})()
         (qa, sa), w = ins[0], ins[1]
         sub = [(qa[rows], sa[rows] if sa.size > 1 else sa), w] + [
             (v[rows] if (k == len(ins) - 1 and node.attrs.get("residual")) else v) for k, v in enumerate(ins[2:], 2)]
@@ -395,8 +413,8 @@ def _check_node_sampled(node, got, ins, gen, nrows=64, nbatches=3):
         _check_node(node, got, ins)
 
 
-@pytest.mark.parametrize("act_granularity", ["tensor", "row"])
-def test_full_c4_forward(G, act_granularity):
+@pytest.mark.parametrize("act_granularity,qload", [("tensor", False), ("tensor", True), ("row", False)])
+def test_full_c4_forward(G, act_granularity, qload):
     """Config C4 at full size (vocab 65, d 384, 6 heads, 6 layers, FFN 1536,
     seq 256, batch 64), node by node on the GPU's own inputs: every
     quantize / layer_norm_quant(_rows) node exactly and in full against the
@@ -410,7 +428,7 @@ def test_full_c4_forward(G, act_granularity):
     w = CharLMWeights(seed=0)
     B, T = 64, 256
     ids = np.random.Generator(np.random.PCG64(9)).integers(0, 65, (B, T)).astype(np.int32)
-    model = CharLM(w, act_granularity=act_granularity)
+    model = CharLM(w, act_granularity=act_granularity, qload=qload)
     seen = {}
     y = model(ids, observe=lambda node, v: seen.__setitem__(node.id, (node, _host(v))))
     assert y.shape == (B * T, 65) and np.isfinite(y).all()
@@ -426,9 +444,14 @@ def test_full_c4_forward(G, act_granularity):
         counts[node.op] = counts.get(node.op, 0) + 1
     ln = "layer_norm_quant_rows" if act_granularity == "row" else "layer_norm_quant"
     # 6 blocks: 2 LayerNorms, 4 Linears, attention; then the final LayerNorm
-    # and the head.  Per tensor, the attention and fc1 outputs are quantized
-    # by a quantize node (the LayerNorms emit their own codes).
-    assert counts == {"embedding": 1, ln: 13, "int8_linear": 25, "attention": 6, "quantize": 12}, counts
+    # and the head.  The LayerNorms emit their own codes; the attention and
+    # fc1 outputs are quantized by a quantize node, or with qload inside the
+    # O and fc2 GEMMs.
+    if not qload:
+        assert counts == {"embedding": 1, ln: 13, "int8_linear": 25, "attention": 6, "quantize": 12}, counts
+    else:
+        assert counts == {"embedding": 1, ln: 13, "int8_linear": 25, "attention": 6}, counts
+        assert sum(bool(n.attrs.get("qload")) for n in g.nodes) == 12
     np.testing.assert_array_equal(seen[g.output][1].view(np.uint32), y.view(np.uint32))
     del seen
     fp = R.forward(w, ids, quantized=False)

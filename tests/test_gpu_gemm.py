@@ -335,6 +335,84 @@ def test_gemm_i8_quant_edge_cases(hip):
     Nn.synchronize()
 
 
+def _producer_parts(x):
+    """Absmax partials of x as a producer would write them (kh_absmax_parts)."""
+    import ctypes
+    from kansaiml_amd import _native as Nn
+    from kansaiml_amd import hip as H
+    parts = H.AbsmaxParts()
+    Nn.call("kh_absmax_parts", x.ptr, x.numel(), parts.buf.ptr, H.ABSMAX_PARTS, ctypes.byref(parts._n))
+    return parts
+
+
+@pytest.mark.parametrize("M,N,K", [(16384, 384, 1536),  # C4 fc2 (fused kernel, one 384-column tile)
+                                   (16384, 384, 384),   # C4 O
+                                   (512, 128, 64), (256, 256, 640), (1024, 768, 256),  # NB = 1, 2; two tiles
+                                   (100, 384, 384), (256, 200, 128), (128, 384, 96)])  # other shapes: two steps
+def test_gemm_i8_qload_matches_two_steps(hip, M, N, K):
+    """kh_gemm_i8_qload equals kh_quantize_tensor_parts followed by
+    kh_gemm_i8_ex with that scale, bit for bit (plain, bias, GELU and
+    residual epilogues, its own absmax partials), and the oracle's quantize
+    and GEMM on sampled rows."""
+    from kansaiml_amd import _native as Nn
+    H, D = hip
+    gen = np.random.Generator(np.random.PCG64(M * 3 + N * 7 + K))
+    x = (gen.standard_normal((M, K)) * 2).astype(np.float32)
+    x[gen.integers(0, M), gen.integers(0, K)] = 17.0  # the tensor's max, away from the rest
+    bt = gen.integers(-127, 128, (N, K), dtype=np.int8)
+    sb = gen.uniform(1e-4, 1e-3, N)
+    bias = gen.standard_normal(N).astype(np.float32)
+    res = gen.standard_normal((M, N)).astype(np.float32)
+    xd, bd, sbd, biasd, resd = D.from_host(x), D.from_host(bt), D.from_host(sb), D.from_host(bias), D.from_host(res)
+    parts = _producer_parts(xd)
+    q2, s2 = H.quantize_tensor_parts(xd, parts)
+    oq, os_ = O.ko_quantize_tensor(x)
+    np.testing.assert_array_equal(q2.numpy().reshape(-1), oq.reshape(-1))
+    for b_, act, r_ in ((None, None, None), (biasd, None, None), (biasd, "gelu", None), (biasd, None, resd)):
+        out, oparts, sc = H.gemm_i8_qload(xd, parts, bd, sbd, b_, act=act, residual=r_, absmax=True,
+                                          want_scale=True)
+        ref, rparts = H.gemm_i8_fused(q2, bd, s2, sbd, b_, act=act, residual=r_, absmax=True)
+        np.testing.assert_array_equal(bits32(out.numpy()), bits32(ref.numpy()))
+        assert sc.numpy()[0] == s2.numpy()[0] == os_
+        qa, sa_ = H.quantize_tensor_parts(out, oparts)
+        qb, sb_ = H.quantize_tensor(out)
+        np.testing.assert_array_equal(qa.numpy(), qb.numpy())
+        assert sa_.numpy()[0] == sb_.numpy()[0]
+    rows = gen.choice(M, size=min(M, 48), replace=False)
+    eacc = O.ko_gemm_i8(oq.reshape(M, K)[rows], bt)
+    out, _ = H.gemm_i8_qload(xd, parts, bd, sbd, biasd)
+    np.testing.assert_array_equal(bits32(out.numpy()[rows]), bits32(O.ko_epilogue(eacc, [os_], sb, bias)))
+    Nn.synchronize()
+
+
+def test_gemm_i8_qload_ties_and_nonfinite(hip):
+    """Values exactly between two codes (the exact binary64 path, ties to
+    even) give the two-step codes; a NaN in x is reported as ValueError at
+    the next synchronize, as the unfused quantize reports it."""
+    from kansaiml_amd import _native as Nn
+    H, D = hip
+    gen = np.random.Generator(np.random.PCG64(41))
+    M, N, K = 256, 384, 384
+    x = (gen.integers(-126, 126, (M, K)) + 0.5).astype(np.float32)
+    x[3, 7] = 127.0  # scale exactly 1.0: every other value is a tie
+    bt = gen.integers(-127, 128, (N, K), dtype=np.int8)
+    sb = np.full(N, 0.01)
+    xd, bd, sbd = D.from_host(x), D.from_host(bt), D.from_host(sb)
+    parts = _producer_parts(xd)
+    out, _, sc = H.gemm_i8_qload(xd, parts, bd, sbd, want_scale=True)
+    oq, os_ = O.ko_quantize_tensor(x)
+    assert os_ == 1.0 and sc.numpy()[0] == 1.0
+    expect = O.ko_epilogue(O.ko_gemm_i8(oq.reshape(M, K), bt), [1.0], sb, None)
+    np.testing.assert_array_equal(bits32(out.numpy()), bits32(expect))
+    x[100, 5] = np.nan
+    xd = D.from_host(x)
+    parts = _producer_parts(xd)
+    H.gemm_i8_qload(xd, parts, bd, sbd)
+    with pytest.raises(ValueError):
+        Nn.synchronize()
+    Nn.synchronize()
+
+
 @pytest.mark.parametrize("case", ["negative", "threshold", "nan_bias", "inf_bias", "neg_inf_bias"])
 def test_gemm_i8_quant_gelu_absmax_paths(hip, case):
     """The absmax pass of a GELU epilogue takes each lane's largest value's

@@ -162,6 +162,48 @@ def test_quantize_producers_fuse_into_quant_nodes():
     assert "layer_norm" in ops4 and "layer_norm_quant_rows" not in ops4
 
 
+def test_quantize_fuses_into_its_int8_linear_with_qload():
+    """qload=True: a per-tensor quantize whose only reader is an int8 Linear
+    becomes part of it (operand 0 is then the fp32 activation) and the
+    activation's producer writes absmax partials for it; a per-row quantize,
+    a quantize with a second reader, or a quantize a producer already
+    absorbed (producer_quant) is left alone.  Off by default."""
+    w1 = np.zeros((16, 32), np.float32)
+    w2 = np.zeros((32, 16), np.float32)
+    g1, b1 = np.ones(16, np.float32), np.zeros(16, np.float32)
+    bias = np.zeros(32, np.float32)
+
+    def fn(x):
+        h = x.layer_norm(g1, b1)
+        f = h.quantize().int8_matmul(x._coerce(w1).quantize()).dequantize().add(bias).gelu()
+        return f.quantize().int8_matmul(x._coerce(w2).quantize()).dequantize().add(x)
+
+    g = kir.trace(fn, np.zeros((4, 16), np.float32))
+    assert not any(n.attrs.get("qload") for n in kir.quant_fusion(g).nodes)  # off by default
+    f = kir.quant_fusion(g, qload=True)
+    lin = [n for n in f.nodes if n.op == "int8_linear"]
+    assert [bool(n.attrs.get("qload")) for n in lin] == [True, True]
+    assert not [n for n in f.nodes if n.op == "quantize" and f.nodes[n.inputs[0]].op != "constant"]
+    # operand 0 is the fp32 producer, marked to write absmax partials
+    assert [f.nodes[n.inputs[0]].op for n in lin] == ["layer_norm", "int8_linear"]
+    assert all(f.nodes[n.inputs[0]].attrs.get("absmax") for n in lin)
+    assert lin[1].attrs["residual"] and not lin[1].attrs["bias"]
+    # with the LayerNorm emitting its codes, only the second quantize fuses
+    fl = kir.quant_fusion(g, producer_quant="layer_norm", qload=True)
+    assert [bool(n.attrs.get("qload")) for n in fl.nodes if n.op == "int8_linear"] == [False, True]
+    assert "layer_norm_quant" in [n.op for n in fl.nodes]
+
+    def per_row_and_shared(x):
+        q = x.quantize("row").int8_matmul(x._coerce(w1).quantize()).dequantize()
+        t = q.quantize()  # two readers
+        a = t.int8_matmul(x._coerce(w2).quantize()).dequantize()
+        return a.add(t.int8_matmul(x._coerce(np.ones((32, 16), np.float32)).quantize()).dequantize())
+
+    f2 = kir.quant_fusion(kir.trace(per_row_and_shared, np.zeros((4, 16), np.float32)), qload=True)
+    assert not any(n.attrs.get("qload") for n in f2.nodes)
+    assert sum(n.op == "quantize" for n in f2.nodes if n.attrs.get("granularity") == "row") == 1
+
+
 @pytest.mark.parametrize("values,shape", [([1.0, 2.0, 3.0], [2, 2]), ([], [1]), ([1.0], [-1]), ([1.0, 2.0], [1])])
 def test_from_flat_length_mismatch_raises(values, shape):
     """kansai.from_flat throws runtime_error("from_flat: data length does not
