@@ -302,7 +302,7 @@ def quant_fusion(graph, producer_quant: bool | str = False, qload: bool = False)
                 chain, ins, attrs = [n.id, dq], list(n.inputs), {"bias": False, "act": None, "residual": False}
                 qa = by_id[n.inputs[0]]
                 if (qload and qa.op == "quantize" and qa.attrs.get("granularity", "tensor") == "tensor"
-                        and only_user(qa.id) == n.id and qa.id not in fused):
+                        and only_user(qa.id) == n.id and qa.id not in fused and qa.shape[-1] <= _QLOAD_MAX_K):
                     chain.insert(0, qa.id)
                     ins[0] = qa.inputs[0]
                     attrs["qload"] = True
@@ -388,6 +388,12 @@ def quant_fusion(graph, producer_quant: bool | str = False, qload: bool = False)
 
 
 _ABSMAX_PRODUCERS = ("int8_linear", "layer_norm", "attention")
+
+# quant_fusion(qload=True) fuses a quantize into its GEMM only for activations
+# of at most this many columns: on MI355X the fused kernel (one workgroup
+# per CU streaming 64 rows of fp32) beat the two launches at K = 384 (18.5
+# against 20.7 us at M = 16384, N = 384) but not at K = 1536 (49 against 48).
+_QLOAD_MAX_K = 512
 
 
 # ---------------------------------------------------------------------------

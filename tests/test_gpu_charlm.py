@@ -291,12 +291,13 @@ def test_small_model_matches_restatement(G, seq, producer_quant):
     # ("layer_norm": the LayerNorms only).
     acts = {(n.op, n.attrs.get("act"), bool(n.attrs.get("residual"))) for n in g.nodes
             if n.op in ("int8_linear", "int8_linear_quant")}
-    # The attention output's quantize (and fc1's, unless fc1 emits codes)
-    # runs inside the consuming GEMM (qload).
+    # With qload the quantizes of activations of at most 512 columns run
+    # inside the consuming GEMM: the attention output's (and without
+    # producer_quant the LayerNorms'), not fc1's 1536-column output.
     qloads = {by_id[n.inputs[0]].op for n in g.nodes if n.attrs.get("qload")}
     if producer_quant == "layer_norm":
-        assert checked == {"embedding", "layer_norm_quant", "int8_linear", "attention"}
-        assert qloads == {"attention", "int8_linear"}
+        assert checked == {"embedding", "layer_norm_quant", "quantize", "int8_linear", "attention"}
+        assert qloads == {"attention"}
         assert acts == {("int8_linear", None, False), ("int8_linear", "gelu", False), ("int8_linear", None, True)}
         assert all(n.attrs.get("absmax") for n in g.nodes
                    if n.op == "attention" or (n.op == "int8_linear" and n.attrs.get("act")))
@@ -307,9 +308,8 @@ def test_small_model_matches_restatement(G, seq, producer_quant):
                         ("int8_linear", None, True)}
         assert all(n.attrs.get("absmax") for n in g.nodes if n.op == "attention")
     else:
-        # the LayerNorm outputs' quantizes run inside QKV and fc1 as well
-        assert checked == {"embedding", "layer_norm", "int8_linear", "attention"}
-        assert qloads == {"attention", "int8_linear", "layer_norm"}
+        assert checked == {"embedding", "layer_norm", "quantize", "int8_linear", "attention"}
+        assert qloads == {"attention", "layer_norm"}
         assert acts == {("int8_linear", None, False), ("int8_linear", "gelu", False), ("int8_linear", None, True)}
         assert all(n.attrs.get("absmax") for n in g.nodes
                    if n.op in ("layer_norm", "attention") or (n.op == "int8_linear" and n.attrs.get("act")))
@@ -445,13 +445,13 @@ def test_full_c4_forward(G, act_granularity, qload):
     ln = "layer_norm_quant_rows" if act_granularity == "row" else "layer_norm_quant"
     # 6 blocks: 2 LayerNorms, 4 Linears, attention; then the final LayerNorm
     # and the head.  The LayerNorms emit their own codes; the attention and
-    # fc1 outputs are quantized by a quantize node, or with qload inside the
-    # O and fc2 GEMMs.
+    # fc1 outputs are quantized by a quantize node, or with qload the
+    # attention output inside the O GEMM.
     if not qload:
         assert counts == {"embedding": 1, ln: 13, "int8_linear": 25, "attention": 6, "quantize": 12}, counts
     else:
-        assert counts == {"embedding": 1, ln: 13, "int8_linear": 25, "attention": 6}, counts
-        assert sum(bool(n.attrs.get("qload")) for n in g.nodes) == 12
+        assert counts == {"embedding": 1, ln: 13, "int8_linear": 25, "attention": 6, "quantize": 6}, counts
+        assert sum(bool(n.attrs.get("qload")) for n in g.nodes) == 6
     np.testing.assert_array_equal(seen[g.output][1].view(np.uint32), y.view(np.uint32))
     del seen
     fp = R.forward(w, ids, quantized=False)
