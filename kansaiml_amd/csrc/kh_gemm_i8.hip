@@ -1416,7 +1416,8 @@ int kh_gemm_i8_qload(const float* x, int64_t M, int64_t N, int64_t K, const unsi
     KH_REQUIRE(K <= 133144, "kh_gemm_i8_qload: K > 133144 could overflow the int32 accumulator");
     KH_REQUIRE(M <= 0xFFFFLL * 128 && N <= 0x7FFFFFFFLL, "kh_gemm_i8_qload: shape too large");
     KH_REQUIRE(act == kActNone || act == kActGelu, "kh_gemm_i8_qload: unknown activation");
-    KH_REQUIRE(x_parts && x_nparts > 0, "kh_gemm_i8_qload: the producer's absmax partials are required");
+    KH_REQUIRE(M * K == 0 || (x && x_parts && x_nparts > 0),
+               "kh_gemm_i8_qload: x and the producer's absmax partials are required");
     KH_REQUIRE(!absmax_parts || (nparts && max_parts > 0), "kh_gemm_i8_qload: partials need max_parts and nparts");
     if (nparts) *nparts = 0;
     KH_DEVICE_OR_RETURN(d);
@@ -1444,7 +1445,7 @@ int kh_gemm_i8_qload(const float* x, int64_t M, int64_t N, int64_t K, const unsi
         const int frc = kh_free(tmp);
         return rc ? rc : frc;
     }
-    KH_REQUIRE(x && b_packed && sb && out, "kh_gemm_i8_qload: null pointer");
+    KH_REQUIRE(b_packed && sb && out, "kh_gemm_i8_qload: null pointer");
     const int nb = qload_nb(x, b_packed, M, N, K);
     const int64_t grid = nb ? (M / kQlBM) * (N / (128 * nb)) : 0;
     if (nb && (!absmax_parts || grid <= max_parts)) {
