@@ -186,13 +186,22 @@ __device__ __forceinline__ unsigned gelu_absmax_bits(const float (&y)[16]) {
 // are scalar (8*(r/4) + r%4 rows of N floats), so no element needs address
 // arithmetic.  Same arithmetic, in the same order, as store_block32_impl.
 // (rowblk, colblk): the block's first row and column; N <= 2^24.
+// The column scale sb[j] and bias[j] of lane l's column colblk + l % 32 (0
+// without them), loaded by the kernels before their main loop.
+struct ColEpi {
+    double sb;
+    float bias;
+};
+__device__ __forceinline__ ColEpi col_epi(const Epilogue& ep, int64_t j) {
+    return ColEpi{ep.sb ? ep.sb[ep.sb_per_col ? j : 0] : 0.0, ep.bias ? ep.bias[j] : 0.0f};
+}
+
 template <bool FUSED, int MODE, bool ROWSA = false>
 __device__ __forceinline__ unsigned store_block32_full(const Epilogue& ep, int64_t rowblk, int64_t colblk, int N,
                                                        int lane, double sa, const i32x16& v,
-                                                       const kh::quant::Scale& sc) {
+                                                       const kh::quant::Scale& sc, ColEpi ce) {
     const int fr = lane & 31, fh = lane >> 5;
-    const int64_t j = colblk + fr;
-    const double sbj = ep.sb ? ep.sb[ep.sb_per_col ? j : 0] : 0.0;
+    const double sbj = ce.sb;
     const double s = sa * sbj;
     const int64_t base = rowblk * N + colblk;
     const uint32_t span = (uint32_t)N * 32u * 4u;  // the block's 32 rows, in bytes
@@ -224,9 +233,8 @@ __device__ __forceinline__ unsigned store_block32_full(const Epilogue& ep, int64
         for (int r = 0; r < 16; ++r) y[r] = (float)((double)v[r] * s);
     }
     if (ep.bias) {
-        const float bj = ep.bias[j];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) y[r] = y[r] + bj;
+        for (int r = 0; r < 16; ++r) y[r] = y[r] + ce.bias;
     }
     if constexpr (FUSED && MODE == kh::quant::kOutMaxOnly) {
         if (ep.act == kActGelu && !ep.residual) return gelu_absmax_bits(y);
@@ -533,6 +541,15 @@ __global__ __launch_bounds__(512, BN == 256 ? 2 : ((BM == 256 || NS >= 4 || (FUS
     // 16 bytes of row r + l % 32 at chunk 2s + l / 32, i.e. LDS byte
     // r * 64 + (((l / 32) ^ swz) << 4), with bit 5 flipped for s = 1.
     const int fr = lane & 31, fh = lane >> 5;
+    // The full-tile epilogue's column scales, biases and activation scale,
+    // requested before the main loop (the epilogue then waits for nothing).
+    ColEpi ce[kTN];
+    double sa_t = 0.0;
+    if constexpr (EPI != kEpiGeneral) {
+#pragma unroll
+        for (int b = 0; b < kTN; ++b) ce[b] = col_epi(ep, (int64_t)tn * BN + wn * kWaveN + b * 32 + fr);
+        if constexpr (EPI == kEpiFull) sa_t = ep.sa[0];
+    }
     int a_off[kTM], b_off[kTN];
 #pragma unroll
     for (int a = 0; a < kTM; ++a) {
@@ -599,14 +616,13 @@ __global__ __launch_bounds__(512, BN == 256 ? 2 : ((BM == 256 || NS >= 4 || (FUS
     const bool full = rows_a == BM && rows_b == BN;
     if constexpr (EPI != kEpiGeneral) {
         constexpr bool kRows = EPI == kEpiFullRows;
-        const double sa = kRows ? 0.0 : ep.sa[0];
 #pragma unroll
         for (int a = 0; a < kTM; ++a)
 #pragma unroll
             for (int b = 0; b < kTN; ++b) {
                 mx = max(mx, store_block32_full<FUSED, MODE, kRows>(ep, (int64_t)tm * BM + wm * kWaveM + a * 32,
                                                                     (int64_t)tn * BN + wn * kWaveN + b * 32, N,
-                                                                    lane, sa, acc[a][b], sc));
+                                                                    lane, sa_t, acc[a][b], sc, ce[b]));
                 __builtin_amdgcn_sched_barrier(0);
             }
     } else if (full && !ep.acc && !ep.sa_per_row && (MODE != kh::quant::kOutStore || ep.out) && N <= (1 << 24)) {
@@ -615,9 +631,9 @@ __global__ __launch_bounds__(512, BN == 256 ? 2 : ((BM == 256 || NS >= 4 || (FUS
         for (int a = 0; a < kTM; ++a)
 #pragma unroll
             for (int b = 0; b < kTN; ++b) {
-                mx = max(mx, store_block32_full<FUSED, MODE>(ep, (int64_t)tm * BM + wm * kWaveM + a * 32,
-                                                             (int64_t)tn * BN + wn * kWaveN + b * 32, N, lane, sa,
-                                                             acc[a][b], sc));
+                const int64_t cb = (int64_t)tn * BN + wn * kWaveN + b * 32;
+                mx = max(mx, store_block32_full<FUSED, MODE>(ep, (int64_t)tm * BM + wm * kWaveM + a * 32, cb, N,
+                                                             lane, sa, acc[a][b], sc, col_epi(ep, cb + fr)));
                 __builtin_amdgcn_sched_barrier(0);
             }
     } else if (full && !ep.acc && ep.sa_per_row && MODE == kh::quant::kOutStore && ep.out && N <= (1 << 24)) {
@@ -625,9 +641,9 @@ __global__ __launch_bounds__(512, BN == 256 ? 2 : ((BM == 256 || NS >= 4 || (FUS
         for (int a = 0; a < kTM; ++a)
 #pragma unroll
             for (int b = 0; b < kTN; ++b) {
-                mx = max(mx, store_block32_full<FUSED, MODE, true>(ep, (int64_t)tm * BM + wm * kWaveM + a * 32,
-                                                                   (int64_t)tn * BN + wn * kWaveN + b * 32, N, lane,
-                                                                   0.0, acc[a][b], sc));
+                const int64_t cb = (int64_t)tn * BN + wn * kWaveN + b * 32;
+                mx = max(mx, store_block32_full<FUSED, MODE, true>(ep, (int64_t)tm * BM + wm * kWaveM + a * 32, cb, N,
+                                                                   lane, 0.0, acc[a][b], sc, col_epi(ep, cb + fr)));
                 __builtin_amdgcn_sched_barrier(0);
             }
     } else if (full) {
@@ -759,6 +775,9 @@ __global__ __launch_bounds__(512, 2) void gemm_i8_qload_kernel(const float* __re
     i32x16 acc[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[b] = i32x16{0};
+    ColEpi ce[NB];  // requested before the main loop
+#pragma unroll
+    for (int b = 0; b < NB; ++b) ce[b] = col_epi(ep, (int64_t)tn * BN + wn * 32 * NB + b * 32 + fr);
 
     const int nk = K / BK;
     f32x4 xa[D][2];
@@ -794,7 +813,7 @@ __global__ __launch_bounds__(512, 2) void gemm_i8_qload_kernel(const float* __re
     for (int b = 0; b < NB; ++b) {
         mx = max(mx, store_block32_full<FUSED, kh::quant::kOutStore>(ep, (int64_t)tm * kQlBM + wm * 32,
                                                                       (int64_t)tn * BN + wn * 32 * NB + b * 32, N,
-                                                                      lane, sc.s, acc[b], sc));
+                                                                      lane, sc.s, acc[b], sc, ce[b]));
         __builtin_amdgcn_sched_barrier(0);
     }
     if (parts) {
