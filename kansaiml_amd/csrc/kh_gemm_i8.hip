@@ -865,6 +865,8 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_i8_skinny_kernel(const
     // compiler load every kernel argument before the first weight load
     // instead of after a loop-skip branch.
     __builtin_assume(K >= 64 * kSkinnyWaves * C);
+    // Activation loads in batches of up to 4 steps, each batch issued whole
+    // before its MFMAs (all C at once measured slower at N = 11008).
     constexpr int AC = C < 4 ? C : 4;
     const int kper = K / kSkinnyWaves;  // a multiple of 64 * C; exactly 64 * C when ONE
     const int k_begin = wave * kper;
@@ -875,7 +877,13 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_i8_skinny_kernel(const
     for (int u = 0; u < NT; ++u) b_off[u] = min(n0 + u * 16 + (lane & 15), N - 1) * K + kg;
     int a_off[MT];
 #pragma unroll
-    for (int t = 0; t < MT; ++t) a_off[t] = (t * 16 + (lane & 15)) * K + kg;
+    for (int t = 0; t < MT; ++t) {
+        a_off[t] = (t * 16 + (lane & 15)) * K + kg;
+        // Kept in a register from here: recomputed later, the offset was
+        // built from a register the compiler shared with a loaded epilogue
+        // operand, and waited for every load in flight.
+        asm volatile("" : "+v"(a_off[t]));
+    }
 
     i32x4v acc[MT][NT];
 #pragma unroll
@@ -917,6 +925,10 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_i8_skinny_kernel(const
 #pragma unroll
                 for (int c = 0; c < AC; ++c)
                     a[t][c] = __builtin_amdgcn_raw_buffer_load_b128(ra, a_off[t], k0 + 64 * (c0 + c), 0);
+            // All of the batch's loads ahead of its MFMAs (left to itself the
+            // scheduler issues each load just before its MFMA: one L2 round
+            // trip per step).
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int c = 0; c < AC; ++c)
 #pragma unroll
