@@ -837,7 +837,11 @@ __global__ __launch_bounds__(512, 2) void gemm_i8_qload_kernel(const float* __re
 // A workgroup owns 16 output columns for all M rows; its SKW waves split K,
 // each streaming its slice of those 16 packed weight rows (16 B per lane per
 // 64-k step) through v_mfma_i32_16x16x64_i8 with up to two 16-row tiles of
-// activations.  Each wave takes its slice in chunks of C steps (8 where the
+// activations.  Where the slice is one chunk of 4 or 8 steps (K = 2048 or
+// 4096) and a workgroup has one column tile, the weights are read whole rows
+// at a time (2 rows x 512 B per wave instruction at K = 4096, the pattern of
+// a plain streaming read) and rearranged into B fragments through the wave's
+// own LDS region; otherwise each load is one B fragment (16 rows x 64 B).  Each wave takes its slice in chunks of C steps (8 where the
 // slice allows) and issues all of a chunk's loads, the weights first and
 // then the activations, before its first MFMA (scheduling barriers keep the
 // compiler from interleaving them with the MFMAs' waits), so the HBM stream
@@ -857,6 +861,11 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_i8_skinny_kernel(const
                                                                            int N, int K, Epilogue ep) {
     static_assert(MT * NT <= kSkinnyWaves, "one epilogue wave per 16x16 tile");
     __shared__ i32x4v red[kSkinnyWaves][MT * NT][64];
+    // TP: the wave's weight slice is read whole rows at a time (16 / C rows
+    // x 64 C bytes per instruction) and turned into B fragments through the
+    // wave's own LDS region, half of the steps at a time.
+    constexpr bool TP = ONE && NT == 1 && (C == 4 || C == 8);
+    __shared__ i32x4v wt[TP ? kSkinnyWaves : 1][TP ? C / 2 : 1][64];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n0 = blockIdx.x * 16 * NT;
@@ -909,6 +918,46 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_i8_skinny_kernel(const
             res[r] = ep.residual ? ep.residual[i * N + ejc] : 0.0f;
         }
     };
+    auto chunk_tp = [&](int k0) {
+        constexpr int R = 16 / C;  // rows per load instruction
+        i32x4v b[C];
+        const int ch = lane % (4 * C);  // the 16-byte chunk of its rows this lane reads
+#pragma unroll
+        for (int i = 0; i < C; ++i)
+            b[i] = __builtin_amdgcn_raw_buffer_load_b128(rb, min(n0 + i * R + lane / (4 * C), N - 1) * K + ch * 16,
+                                                         k0, 0);
+        prefetch_epilogue();
+        __builtin_amdgcn_sched_barrier(0);
+        i32x4v a[MT][C];
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int c = 0; c < C; ++c) a[t][c] = __builtin_amdgcn_raw_buffer_load_b128(ra, a_off[t], k0 + 64 * c, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        // Slot of fragment lane l in step st's 1 KiB block: l with bits 0-1
+        // XORed by l / 16 and bits 2-3 by st, so a write quarter (one row, 4
+        // steps x 4 chunks) and a read quarter (16 rows, one chunk) each
+        // cover the 16 distinct 16-byte bank groups.
+        auto slot = [](int l, int st) { return l ^ ((l >> 4) & 3) ^ ((st & 3) << 2); };
+        const int st = ch >> 2, q = ch & 3;
+        i32x4v bf[C];
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            if ((st >= C / 2) == (half == 1)) {
+#pragma unroll
+                for (int i = 0; i < C; ++i)
+                    wt[wave][st % (C / 2)][slot(i * R + lane / (4 * C) + 16 * q, st)] = b[i];
+            }
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int c = 0; c < C / 2; ++c) bf[half * (C / 2) + c] = wt[wave][c][slot(lane, half * (C / 2) + c)];
+            asm volatile("" ::: "memory");
+        }
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+            for (int t = 0; t < MT; ++t) acc[t][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t][c], bf[c], acc[t][0], 0, 0, 0);
+    };
     auto chunk = [&](int k0) {
         i32x4v b[NT][C];
 #pragma unroll
@@ -940,7 +989,9 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_i8_skinny_kernel(const
     };
     // A wave's whole slice as one chunk where it fits (measured ~1 us faster
     // than the same loads under a loop, even one that runs once).
-    if constexpr (ONE) {
+    if constexpr (TP) {
+        chunk_tp(k_begin);
+    } else if constexpr (ONE) {
         chunk(k_begin);
     } else {
         prefetch_epilogue();
