@@ -312,7 +312,7 @@ def bench_skinny(steps, warmup, rows=None):
             out_rows.append({"M": M, "K": K, "N": N, "us": round(us, 2), "us_stream": round(us_stream, 2),
                              "us_single": round(us_single, 2),
                              "GB/s": round(gbs, 1), "TOPS": round(2.0 * M * N * K / (us * 1e-6) / 1e12, 2),
-                             "path": "fused decode kernel" if M <= 2 else "quantize_rows + skinny GEMM",
+                             "path": "fused decode kernel" if M <= 3 else "quantize_rows + skinny GEMM",
                              "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                                           "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
                                           "traffic": measured_traffic(key), "traffic_key": key}})
@@ -740,7 +740,7 @@ def _summarize_traffic(root, traffic):
     cmds = [profile_command("fetch"), profile_command("write")]
     if c5:
         body += ("\n\nC5 rows (`kh_linear_i8`, per call: the per-row quantize and the skinny GEMM for M > 2, the "
-                 "fused decode kernel for M <= 2; algorithmic bytes N*K + 8N + 6MK + 4MN):\n\n"
+                 "fused decode kernel for M <= 3; algorithmic bytes N*K + 8N + 6MK + 4MN):\n\n"
                  + _md_table(["row", "kernels", "FETCH_SIZE KiB", "WRITE_SIZE KiB", "HBM MB/call", "algorithmic MB",
                               "ratio"], c5))
         cmds += [profile_command(f"c5_{M}_{K}_{N}_{w}") for M, K, N in C5_ROWS for w in ("fetch", "write")]

@@ -237,7 +237,9 @@ int kh_gemm_i8_qload(const float* x, int64_t M, int64_t N, int64_t K, const unsi
 /* Per-token activation quantize fused into the GEMM's producer: x fp32
  * [M, K] is quantized per row into q_scratch (int8 [M, K]) and
  * sx_scratch (binary64 [M]), then kh_gemm_i8 runs with sa = sx_scratch
- * (per row).  The decode-style entry point of config C5. */
+ * (per row).  The decode-style entry point of config C5.  One launch for
+ * M <= 3 (M <= 2 with K = 2048, 4096 or 8192; M = 3 with K = 2048 or
+ * 4096, 16-byte aligned x and b_packed), two otherwise. */
 int kh_linear_i8(const float* x, int64_t M, int64_t K, const int8_t* b_packed, int64_t N,
                  const double* sb, int sb_per_col, const float* bias,
                  int8_t* q_scratch, double* sx_scratch, float* out);

@@ -1184,9 +1184,10 @@ int launch_gemm(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, int6
 }
 
 // ---------------------------------------------------------------------------
-// Decode Linear for one or two tokens (kh_linear_i8 with M <= 2): the per-token
-// quantize of the fp32 activations is fused into the weight-streaming GEMV,
-// so a decode step is one launch instead of two dependent ones.
+// Decode Linear for one to three tokens (kh_linear_i8 with M <= 3): the
+// per-token quantize of the fp32 activations is fused into the weight-
+// streaming GEMV, so a decode step is one launch instead of two dependent
+// ones.
 //
 // A workgroup (8 waves) owns 16 consecutive weight rows (output columns), 16K
 // contiguous bytes, and reads them 8 KiB per load instruction -- the fastest
@@ -1196,8 +1197,9 @@ int launch_gemm(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, int6
 // k offset 16 * (t % (K / 16)), the same offset in every instruction; the
 // products are VALU v_dot4_i32_i8 against the lane's 16 activation codes
 // (read once from LDS), exact in int32 in any order.  Each row's lanes are
-// whole waves: a wave sums its lanes by shuffles, the row's waves through
-// LDS.  Each workgroup loads the fp32 activations first (L2-resident after
+// whole waves: a wave sums its lanes in the VALU (for up to two tokens one
+// wave_sum per partial, for MAXM = 4 token rows the transposed butterfly over
+// half of the rows' partials at a time), the row's waves through LDS.  Each workgroup loads the fp32 activations first (L2-resident after
 // the first workgroup), then issues all of its weight loads, so the
 // in-order vmcnt wait for the activations does not wait for the weights;
 // while the weights stream in it reduces each row's absmax (wave shuffles
@@ -1222,9 +1224,14 @@ __global__ __launch_bounds__(512) void linear_i8_decode_kernel(const float* __re
     constexpr int kRowsPerInst = T / kLanesPerRow;
     constexpr int kWavesPerRow = kLanesPerRow / 64;
     static_assert(XH >= 1 && MAXM * XH <= 32 && kRowsPerInst * S == 16 && kWavesPerRow >= 1, "shape");
+    // More than two tokens: the partial products of half the wave's rows at
+    // a time (MAXM * S / 2 per lane) summed by the transposed butterfly.
+    constexpr bool kTransposed = MAXM > 2;
+    constexpr int kHalfP = MAXM * S / 2;
     __shared__ __attribute__((aligned(16))) int8_t codes[MAXM * K];
     __shared__ unsigned rmax[W][MAXM];
-    __shared__ int red[W][MAXM][S];
+    __shared__ int red[kTransposed ? 1 : W][MAXM][S];
+    __shared__ int redt[kTransposed ? W : 1][2][64];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1312,26 +1319,46 @@ __global__ __launch_bounds__(512) void linear_i8_decode_kernel(const float* __re
 #pragma unroll
     for (int m = 0; m < MAXM; ++m)
         a[m] = (m < M) ? *reinterpret_cast<const i32x4*>(codes + m * K + kk) : i32x4{0, 0, 0, 0};
-    int p[MAXM][S];
+    if constexpr (kTransposed) {
+        // Value m * S / 2 + j of half h: token m against instruction
+        // h * S / 2 + j (int32 sums are exact in any order).
 #pragma unroll
-    for (int i = 0; i < S; ++i)
+        for (int h = 0; h < 2; ++h) {
+            int p[kHalfP];
 #pragma unroll
-        for (int m = 0; m < MAXM; ++m) {
-            p[m][i] = 0;
+            for (int m = 0; m < MAXM; ++m)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) p[m][i] = __builtin_amdgcn_sdot4(a[m][e], b[i][e], p[m][i], false);
+                for (int j = 0; j < S / 2; ++j) {
+                    int acc = 0;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_sdot4(a[m][e], b[h * (S / 2) + j][e], acc, false);
+                    p[m * (S / 2) + j] = acc;
+                }
+            kh::lanes::wave_sum_transposed(p, lane);
+            redt[wave][h][lane] = p[0];
         }
-    // Wave sums of all S * MAXM partials, in the VALU (independent chains
-    // the compiler interleaves; int32 sums are exact in any order).
+    } else {
+        int p[MAXM][S];
 #pragma unroll
-    for (int m = 0; m < MAXM; ++m)
+        for (int i = 0; i < S; ++i)
 #pragma unroll
-        for (int i = 0; i < S; ++i) p[m][i] = kh::lanes::wave_sum(p[m][i]);
-    if (lane == 0) {
+            for (int m = 0; m < MAXM; ++m) {
+                p[m][i] = 0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) p[m][i] = __builtin_amdgcn_sdot4(a[m][e], b[i][e], p[m][i], false);
+            }
+        // Wave sums of all S * MAXM partials, in the VALU (independent chains
+        // the compiler interleaves; int32 sums are exact in any order).
 #pragma unroll
         for (int m = 0; m < MAXM; ++m)
 #pragma unroll
-            for (int i = 0; i < S; ++i) red[wave][m][i] = p[m][i];
+            for (int i = 0; i < S; ++i) p[m][i] = kh::lanes::wave_sum(p[m][i]);
+        if (lane == 0) {
+#pragma unroll
+            for (int m = 0; m < MAXM; ++m)
+#pragma unroll
+                for (int i = 0; i < S; ++i) red[wave][m][i] = p[m][i];
+        }
     }
     __syncthreads();
     if (tid >= 16 * MAXM) return;
@@ -1342,8 +1369,15 @@ __global__ __launch_bounds__(512) void linear_i8_decode_kernel(const float* __re
     if (m >= M || n >= N) return;
     const int i = erow / kRowsPerInst, sub = erow % kRowsPerInst;
     int sum = 0;
+    if constexpr (kTransposed) {
+        const int h = i / (S / 2);
+        const int l = kh::lanes::transposed_lane<kHalfP>(m * (S / 2) + i % (S / 2));
 #pragma unroll
-    for (int w = 0; w < kWavesPerRow; ++w) sum += red[sub * kWavesPerRow + w][m][i];
+        for (int w = 0; w < kWavesPerRow; ++w) sum += redt[sub * kWavesPerRow + w][h][l];
+    } else {
+#pragma unroll
+        for (int w = 0; w < kWavesPerRow; ++w) sum += red[sub * kWavesPerRow + w][m][i];
+    }
     unsigned mb = rmax[0][m];
 #pragma unroll
     for (int w = 1; w < W; ++w) mb = max(mb, rmax[w][m]);
@@ -1359,16 +1393,24 @@ int launch_decode(kh::Device* d, const float* x, int64_t M, const int8_t* B, int
     if (M == 1)
         linear_i8_decode_kernel<S, 1><<<blocks, 512, 0, d->stream>>>(x, (int)M, B, (int)N, sb, sb_per_col, bias, out, q,
                                                                       sx, d->fault);
-    else
+    else if (M == 2)
         linear_i8_decode_kernel<S, 2><<<blocks, 512, 0, d->stream>>>(x, (int)M, B, (int)N, sb, sb_per_col, bias, out, q,
+                                                                      sx, d->fault);
+    else if constexpr (S <= 8)
+        linear_i8_decode_kernel<S, 4><<<blocks, 512, 0, d->stream>>>(x, (int)M, B, (int)N, sb, sb_per_col, bias, out, q,
                                                                       sx, d->fault);
     return kh::launch_status("linear_i8_decode");
 }
 
-// True when the fused decode kernel covers this call.
+// True when the fused decode kernel covers this call: one or two tokens
+// with K = 2048, 4096 or 8192, three with K = 2048 or 4096.  Back to back
+// against the two-launch path (N = 4096 / 11008, K = 4096): M = 3 8.1 / 12.6
+// against 9.3 / 14.3 us; M = 4 8.4 / 15.9 against 9.4 / 15.0; M = 8 (the
+// same design with 8 token rows) 11.9 / 23.4 against 9.8 / 15.7.
 bool decode_fits(const float* x, int64_t M, int64_t K, const int8_t* B, int64_t N, const int8_t* q) {
-    return M >= 1 && M <= 2 && (K == 2048 || K == 4096 || K == 8192) && N >= 1 &&
-           (N + 16) * K <= 0xFFFFFFFFLL && kh::aligned(x, 16) && kh::aligned(B, 16) && kh::aligned(q, 4);
+    const bool k_ok = M <= 2 ? (K == 2048 || K == 4096 || K == 8192) : (K == 2048 || K == 4096);
+    return M >= 1 && M <= 3 && k_ok && N >= 1 && (N + 16) * K <= 0xFFFFFFFFLL && kh::aligned(x, 16) &&
+           kh::aligned(B, 16) && kh::aligned(q, 4);
 }
 
 // NB (128-column blocks per tile) of the quantize-on-load kernel for this

@@ -182,6 +182,37 @@ def test_linear_i8_decode_fused(hip, M, K, N):
         np.testing.assert_array_equal(bits32(out.numpy()), bits32(expect))
 
 
+@pytest.mark.parametrize("M,K,N", [(3, 4096, 4096), (3, 4096, 11008), (3, 2048, 1000), (3, 2048, 17),
+                                   (3, 4096, 33), (8, 4096, 11008), (5, 2048, 1000), (8, 2048, 17), (7, 4096, 33),
+                                   (4, 4096, 4096), (6, 2048, 4096)])
+def test_linear_i8_decode_fused_tokens(hip, M, K, N):
+    """kh_linear_i8 for 3 <= M <= 8 tokens (K = 2048 or 4096): the one-launch
+    decode kernel for M = 3 (its lanes' partial products summed by the
+    transposed butterfly), per-row quantize plus the skinny GEMM above.
+    Outputs, codes and per-token scales bit-exact against the oracle, with an
+    all-zero row, a row of exact ties (the binary64 fallback), a per-tensor
+    weight scale and no bias, and N not a multiple of the 16-row weight
+    tile."""
+    H, D = hip
+    gen = np.random.Generator(np.random.PCG64(M * 7919 + K + N + 3))
+    x = gen.standard_normal((M, K), dtype=np.float32)
+    x[1] = 0.0                                            # zero row: scale 1.0, codes 0
+    x[M - 1, : K // 2] = np.float32(0.5)                  # 0.5 / (1 / 127) = 63.5: exact ties
+    x[M - 1, K // 2:] = np.float32(-1.0)                  # row max 1.0, so the scale is 1/127
+    qw = gen.integers(-127, 128, (N, K), dtype=np.int8)
+    sw = gen.uniform(1e-3, 1e-2, N)
+    bias = gen.standard_normal(N).astype(np.float32)
+    eq, esx = O.ko_quantize_rows(x)
+    for sb, bb in ((sw, bias), (sw[:1], None)):
+        print(f"decode M={M} K={K} N={N} per_col={len(sb) > 1} bias={bb is not None}", flush=True)
+        out, q, sx = H.linear_i8(D.from_host(x), D.from_host(qw), D.from_host(np.asarray(sb, np.float64)),
+                                 D.from_host(bb) if bb is not None else None, return_codes=True)
+        np.testing.assert_array_equal(q.numpy(), eq)
+        np.testing.assert_array_equal(sx.numpy().view(np.uint64), np.asarray(esx, np.float64).view(np.uint64))
+        expect = O.ko_epilogue(O.ko_gemm_i8(eq, qw), esx, sb, bb)
+        np.testing.assert_array_equal(bits32(out.numpy()), bits32(expect))
+
+
 def test_dequantize_acc_matches_fused(hip):
     H, D = hip
     gen = np.random.Generator(np.random.PCG64(9))
