@@ -858,7 +858,7 @@ __global__ __launch_bounds__(512, 2) void gemm_i8_qload_kernel(const float* __re
 typedef int i32x4v __attribute__((ext_vector_type(4)));
 constexpr int kSkinnyWaves = 8;
 
-template <int MT, int NT, int C, bool ONE>
+template <int MT, int NT, int C, bool ONE, bool LEAN = false>
 __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_i8_skinny_kernel(const int8_t* __restrict__ A,
                                                                            const int8_t* __restrict__ B, int M,
                                                                            int N, int K, Epilogue ep) {
@@ -867,7 +867,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_i8_skinny_kernel(const
     // TP: the wave's weight slice is read whole rows at a time (16 / C rows
     // x 64 C bytes per instruction) and turned into B fragments through the
     // wave's own LDS region, half of the steps at a time.
-    constexpr bool TP = ONE && NT == 1 && (C == 4 || C == 8);
+    constexpr bool TP = ONE && NT == 1 && MT <= 2 && (C == 4 || C == 8);
     __shared__ i32x4v wt[TP ? kSkinnyWaves : 1][TP ? C / 2 : 1][64];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -931,11 +931,15 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_i8_skinny_kernel(const
                                                          k0, 0);
         prefetch_epilogue();
         __builtin_amdgcn_sched_barrier(0);
+        // The activation steps, all ahead of the MFMAs, or with LEAN (two
+        // row tiles on a grid of more than one workgroup per CU) four at a
+        // time: 144 -> 114 VGPRs for two row tiles, two workgroups per CU.
+        constexpr int AB = LEAN && C > 4 ? 4 : C;
         i32x4v a[MT][C];
 #pragma unroll
         for (int t = 0; t < MT; ++t)
 #pragma unroll
-            for (int c = 0; c < C; ++c) a[t][c] = __builtin_amdgcn_raw_buffer_load_b128(ra, a_off[t], k0 + 64 * c, 0);
+            for (int c = 0; c < AB; ++c) a[t][c] = __builtin_amdgcn_raw_buffer_load_b128(ra, a_off[t], k0 + 64 * c, 0);
         __builtin_amdgcn_sched_barrier(0);
         // Slot of fragment lane l in step st's 1 KiB block: l with bits 0-1
         // XORed by l / 16 and bits 2-3 by st, so a write quarter (one row, 4
@@ -957,9 +961,23 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_i8_skinny_kernel(const
             asm volatile("" ::: "memory");
         }
 #pragma unroll
-        for (int c = 0; c < C; ++c)
+        for (int c = 0; c < AB; ++c)
 #pragma unroll
             for (int t = 0; t < MT; ++t) acc[t][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t][c], bf[c], acc[t][0], 0, 0, 0);
+        if constexpr (AB < C) {
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int c = AB; c < C; ++c)
+                    a[t][c] = __builtin_amdgcn_raw_buffer_load_b128(ra, a_off[t], k0 + 64 * c, 0);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int c = AB; c < C; ++c)
+#pragma unroll
+                for (int t = 0; t < MT; ++t)
+                    acc[t][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t][c], bf[c], acc[t][0], 0, 0, 0);
+        }
     };
     auto chunk = [&](int k0) {
         i32x4v b[NT][C];
@@ -1032,39 +1050,36 @@ bool skinny_fits(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t
 int launch_skinny(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
                   const Epilogue& ep) {
     const int64_t steps = K / (64 * kSkinnyWaves);  // 64-k steps per wave
-    // 32 columns per workgroup (each activation fragment feeds two weight
-    // tiles, halving the activation reads from L2) for two row tiles, where
-    // that still leaves a workgroup per CU and the slice is one chunk of 4 or
-    // 8 steps.  With one row tile the activation reads are small and the
-    // halved workgroup count costs more than it saves (measured).
-    const bool wide = M > 16 && N >= 32LL * d->cus && (steps == 4 || steps == 8);
-    auto go = [&](auto mt, auto nt, auto c, auto one) {
+    // One 16-column tile per workgroup.  (32 columns, each activation
+    // fragment feeding two weight tiles, measured faster for two row tiles
+    // at N = 11008 before the whole-row weight reads; with them the
+    // 16-column tiles with LEAN loads are faster: 22.96 -> 21.37 us.)
+    const bool lean = M > 16 && (N + 15) / 16 > d->cus;
+    auto go = [&](auto mt, auto nt, auto c, auto one, auto leanv) {
         constexpr int NT = decltype(nt)::value;
         const unsigned blocks = (unsigned)((N + 16 * NT - 1) / (16 * NT));
-        gemm_i8_skinny_kernel<decltype(mt)::value, NT, decltype(c)::value, decltype(one)::value>
-            <<<blocks, kSkinnyWaves * 64, 0, d->stream>>>(A, B, (int)M, (int)N, (int)K, ep);
+        gemm_i8_skinny_kernel<decltype(mt)::value, NT, decltype(c)::value, decltype(one)::value,
+                              decltype(leanv)::value><<<blocks, kSkinnyWaves * 64, 0, d->stream>>>(
+            A, B, (int)M, (int)N, (int)K, ep);
     };
     auto pick = [&](auto mt) {
         using T = std::true_type;
         using F = std::false_type;
         using N1 = std::integral_constant<int, 1>;
-        using N2 = std::integral_constant<int, 2>;
-        if (wide) {
-            if (steps == 4) return go(mt, N2(), std::integral_constant<int, 4>(), T());
-            return go(mt, N2(), std::integral_constant<int, 8>(), T());
-        }
         switch (steps) {
-            case 1: return go(mt, N1(), std::integral_constant<int, 1>(), T());
-            case 2: return go(mt, N1(), std::integral_constant<int, 2>(), T());
-            case 4: return go(mt, N1(), std::integral_constant<int, 4>(), T());
-            case 8: return go(mt, N1(), std::integral_constant<int, 8>(), T());
-            case 16: return go(mt, N1(), std::integral_constant<int, 16>(), T());
+            case 1: return go(mt, N1(), std::integral_constant<int, 1>(), T(), F());
+            case 2: return go(mt, N1(), std::integral_constant<int, 2>(), T(), F());
+            case 4: return go(mt, N1(), std::integral_constant<int, 4>(), T(), F());
+            case 8:
+                if (lean) return go(mt, N1(), std::integral_constant<int, 8>(), T(), T());
+                return go(mt, N1(), std::integral_constant<int, 8>(), T(), F());
+            case 16: return go(mt, N1(), std::integral_constant<int, 16>(), T(), F());
             default: break;
         }
-        if (steps % 8 == 0) go(mt, N1(), std::integral_constant<int, 8>(), F());
-        else if (steps % 4 == 0) go(mt, N1(), std::integral_constant<int, 4>(), F());
-        else if (steps % 2 == 0) go(mt, N1(), std::integral_constant<int, 2>(), F());
-        else go(mt, N1(), std::integral_constant<int, 1>(), F());
+        if (steps % 8 == 0) go(mt, N1(), std::integral_constant<int, 8>(), F(), F());
+        else if (steps % 4 == 0) go(mt, N1(), std::integral_constant<int, 4>(), F(), F());
+        else if (steps % 2 == 0) go(mt, N1(), std::integral_constant<int, 2>(), F(), F());
+        else go(mt, N1(), std::integral_constant<int, 1>(), F(), F());
     };
     if (M <= 16) pick(std::integral_constant<int, 1>());
     else if (M <= 32) pick(std::integral_constant<int, 2>());
