@@ -688,13 +688,23 @@ def _summarize_trace(root):
     stats = _find(os.path.join(root, "trace"), "kernel_stats.csv")
     if not stats:
         return
+    # Median per kernel from the dispatch trace: the average also counts each
+    # leg's warm-up launches, made while the shader clock is still ramping.
+    trace = _find(os.path.join(root, "trace"), "kernel_trace.csv")
+    durs = {}
+    for r in (_read_csv(trace) if trace else []):
+        durs.setdefault(r["Kernel_Name"], []).append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
     rows = [(f"`{_short(r['Name'])[:90]}`", r["Calls"], f"{float(r['AverageNs']) / 1e3:.2f}",
+             f"{float(np.median(durs[r['Name']])) / 1e3:.2f}" if r["Name"] in durs else "",
              f"{float(r['MinNs']) / 1e3:.2f}", f"{float(r['MaxNs']) / 1e3:.2f}", f"{float(r['Percentage']):.1f}")
             for r in _read_csv(stats)]
     _write_profile("bench_kernels_mi355x.md", "Kernel trace of `bench.py` on one MI355X (gfx950)",
                    [profile_command("trace")],
-                   "Every bench leg (`run_kernel_stats.csv`); durations include the profiler's per-dispatch "
-                   "timestamps.\n\n" + _md_table(["kernel", "calls", "avg us", "min us", "max us", "% time"], rows))
+                   "Every bench leg (`run_kernel_stats.csv`, medians from `run_kernel_trace.csv`); durations include "
+                   "the profiler's per-dispatch timestamps. The average counts each leg's warm-up launches (this "
+                   "run warms each leg for 10 ms, while the shader clock is still ramping), so the median is the "
+                   "figure to set beside the bench line's timed steps.\n\n"
+                   + _md_table(["kernel", "calls", "avg us", "median us", "min us", "max us", "% time"], rows))
 
 
 def _summarize_traffic(root, traffic):
