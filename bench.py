@@ -364,11 +364,13 @@ def bench_c1(steps, warmup):
     """Config C1, the reference's CPU-runnable case: an int8 quantized Linear,
     x fp32 [64, 512] ~N(0,1), W fp32 [512, 512] ~N(0, 0.02), bias zeros,
     per-tensor scales for x and W (seed 0; W quantized once at construction).
-    Latency-bound, so reported as microseconds per call: the two kernels
-    back to back (one-launch per-tensor quantize of x; the skinny int8 GEMM
-    with the dequantize and bias fused), replayed as a HIP graph
-    (time_graph) and issued from Python (`us_kernels_stream`), and the eager
-    QLinear call (Python dispatch and output allocation included)."""
+    Latency-bound, so reported as microseconds per call: kh_linear_i8_tensor
+    (one launch: every workgroup quantizes x per tensor and runs its columns
+    of the skinny int8 GEMM with the dequantize and bias fused) back to back,
+    replayed as a HIP graph (time_graph) and issued from Python
+    (`us_kernels_stream`); the same Linear as two launches (kh_quantize_tensor
+    then kh_gemm_i8, `us_two_launch`); and the eager QLinear call (Python
+    dispatch and output allocation included)."""
     from kansaiml_amd import _native as Nn
     from kansaiml_amd.device import DeviceTensor as D
     from kansaiml_amd.quantize import QLinear
@@ -379,23 +381,31 @@ def bench_c1(steps, warmup):
     wq, ws, bd = layer.qweight.codes, layer.qweight.scales, layer.bias
     quant = Nn.lib().kh_quantize_tensor
     gemm = Nn.lib().kh_gemm_i8
+    lin = Nn.lib().kh_linear_i8_tensor
     qargs = (xd.ptr, 64 * 512, q.ptr, s.ptr)
     gargs = (q.ptr, wq.ptr, 64, 512, 512, s.ptr, 0, ws.ptr, 0, bd.ptr, out.ptr, None)
+    largs = (xd.ptr, 64, 512, wq.ptr, 512, ws.ptr, 0, bd.ptr, q.ptr, s.ptr, out.ptr)
 
     def kernels():
+        lin(*largs)
+
+    def two_launch():
         quant(*qargs)
         gemm(*gargs)
 
-    Nn.call("kh_quantize_tensor", *qargs)  # checked once; the timed calls skip the status check
+    Nn.call("kh_linear_i8_tensor", *largs)  # checked once; the timed calls skip the status check
+    Nn.call("kh_quantize_tensor", *qargs)
     Nn.call("kh_gemm_i8", *gargs)
 
     us_stream = time_kernel(kernels, steps, warmup, tag="c1_kernels") * 1e3
     us_kernels = time_graph(kernels, steps)
+    time_kernel(two_launch, steps, warmup, tag="c1_two_launch")
+    us_two = time_graph(two_launch, steps)
     us_eager = time_kernel(lambda: layer(xd), steps, warmup, tag="c1_eager") * 1e3
     ops = 2 * 64 * 512 * 512
     return {"workload": "C1 int8 quantized Linear x[64,512] @ W[512,512] + b, per-tensor scales (seed 0)",
             "us_kernels_back_to_back": round(us_kernels, 2), "us_kernels_stream": round(us_stream, 2),
-            "us_eager_call": round(us_eager, 2), "ops": ops,
+            "us_two_launch": round(us_two, 2), "us_eager_call": round(us_eager, 2), "ops": ops,
             "TOPS_kernels": round(ops / (us_kernels * 1e-6) / 1e12, 3), "bound": "latency"}
 
 
@@ -1147,8 +1157,9 @@ def main():
     if "c1" in only:
         log("C1 int8 quantized Linear ...")
         c1 = bench_c1(max(50, args.steps), args.warmup)
-        log(f"C1: {c1['us_kernels_back_to_back']:.2f} us per call (kernels back to back as a graph; "
-            f"{c1['us_kernels_stream']:.2f} us issued from Python), {c1['us_eager_call']:.2f} us eager")
+        log(f"C1: {c1['us_kernels_back_to_back']:.2f} us per call (one launch, back to back as a graph; "
+            f"{c1['us_kernels_stream']:.2f} us issued from Python; two launches {c1['us_two_launch']:.2f} us), "
+            f"{c1['us_eager_call']:.2f} us eager")
     skinny = None
     if "skinny" in only:
         log("skinny decode GEMMs C5 ...")

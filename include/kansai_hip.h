@@ -244,6 +244,19 @@ int kh_linear_i8(const float* x, int64_t M, int64_t K, const int8_t* b_packed, i
                  const double* sb, int sb_per_col, const float* bias,
                  int8_t* q_scratch, double* sx_scratch, float* out);
 
+/* The int8 Linear with a per-tensor activation scale (config C1's QLinear
+ * with act_granularity "tensor"): x fp32 [M, K] quantized with one scale
+ * over the whole tensor (quantize.py:50-70) into q_scratch (int8 [M, K]) and
+ * sx_scratch[0] (binary64), then kh_gemm_i8 with sa = that scale, per-tensor
+ * (qlinear, quantize.py:115-122, with the dequantize and bias fused).  One
+ * launch for M <= 64, K = 512, 1024, 2048 or 4096 and M * K <= 32768
+ * (every workgroup quantizes the whole of x itself); kh_quantize_tensor then
+ * kh_gemm_i8 otherwise.  A NaN/inf in x reports KH_ERR_NONFINITE at the next
+ * synchronize. */
+int kh_linear_i8_tensor(const float* x, int64_t M, int64_t K, const int8_t* b_packed, int64_t N,
+                        const double* sb, int sb_per_col, const float* bias,
+                        int8_t* q_scratch, double* sx_scratch, float* out);
+
 /* kh_linear_i8 for callers that cannot allocate device memory (code under
  * HIP graph capture, tight decode loops, harnesses that forbid hipMalloc).
  * No counterpart in the reference.  The per-row codes and scales go to a

@@ -85,6 +85,7 @@ _SIGNATURES = {
     "kh_attention_ex": [_vp, _int, _int, _int, _int, _int, _vp, _vp, _int, ctypes.POINTER(ctypes.c_int)],
     "kh_linear_i8": [_vp, _i64, _i64, _vp, _i64, _vp, _int, _vp, _vp, _vp, _vp],
     "kh_linear_i8_noalloc": [_vp, _i64, _i64, _vp, _i64, _vp, _int, _vp, _vp],
+    "kh_linear_i8_tensor": [_vp, _i64, _i64, _vp, _i64, _vp, _int, _vp, _vp, _vp, _vp],
     "kh_matmul_f32": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "kh_probe_mfma_i8": [_vp, _i64, _i64, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)],
     "kh_probe_stream_read": [_vp, _i64],

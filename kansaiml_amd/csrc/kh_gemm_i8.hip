@@ -1428,6 +1428,164 @@ bool decode_fits(const float* x, int64_t M, int64_t K, const int8_t* B, int64_t 
            kh::aligned(B, 16) && kh::aligned(q, 4);
 }
 
+// ---------------------------------------------------------------------------
+// Small int8 Linear with a per-tensor activation scale in one launch
+// (kh_linear_i8_tensor; config C1's x [64, 512]): quantize.py:50-70 on the
+// whole of x, then the GEMM with the dequantize and bias fused.  x is at most
+// kTensorSmallElems values, so every workgroup reads all of it (an L2 hit
+// after the first few), reduces the absmax over the workgroup and writes the
+// codes into LDS itself: no workgroup waits for another and there is no
+// second launch.  The GEMM is the skinny kernel's: 16 output columns per
+// workgroup, the 8 waves splitting K into C 64-k steps each, MT 16-row tiles
+// of v_mfma_i32_16x16x64_i8 with the A fragments read from LDS (chunk j of
+// row m at chunk j ^ (m & 15), so a fragment's 16 rows fall on distinct
+// banks), partial sums reduced through LDS.  Each wave issues its share of
+// x first and its weight fragments after it, so the in-order vmcnt wait for
+// x does not wait for the weights.  Workgroup 0 writes the codes and the
+// scale (the outputs kh_linear_i8_tensor documents); an undecided element
+// takes the exact path inside pack4.
+// ---------------------------------------------------------------------------
+constexpr int kTensorSmallElems = 32768;
+
+template <int MT, int C>
+__global__ __launch_bounds__(512) void linear_i8_tensor_small_kernel(const float* __restrict__ x, int M,
+                                                                     const int8_t* __restrict__ B, int N,
+                                                                     const double* __restrict__ sb, int sb_per_col,
+                                                                     const float* __restrict__ bias,
+                                                                     float* __restrict__ out, int8_t* __restrict__ q_out,
+                                                                     double* __restrict__ sx_out,
+                                                                     unsigned* __restrict__ fault) {
+    using namespace kh::quant;
+    constexpr int W = kSkinnyWaves, T = W * 64;
+    constexpr int K = 64 * W * C;
+    constexpr int XH = kTensorSmallElems / 4 / T;  // float4 of x per thread at most
+    __shared__ __attribute__((aligned(16))) int8_t codes[kTensorSmallElems];
+    __shared__ i32x4v red[W][MT][64];
+    __shared__ unsigned wmax[W];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n0 = blockIdx.x * 16;
+    const int nx4 = M * K / 4;  // float4 of x
+
+    // x: float4 tid + T h (past the end: zeros from the resource bound).
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)nx4 * 16u);
+    f32x4 xv[XH];
+#pragma unroll
+    for (int h = 0; h < XH; ++h)
+        xv[h] = (h * T < nx4) ? __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (tid + h * T) * 16,
+                                                                                                 0, 0))
+                              : f32x4{0.f, 0.f, 0.f, 0.f};
+    // The epilogue's column operands, then the weight fragments of this
+    // wave's K slice (16 rows x 64 B per instruction; rows past N read row N-1).
+    const int ej = min(n0 + (lane & 15), N - 1);
+    const double sbj = sb[sb_per_col ? ej : 0];
+    const float bj = bias ? bias[ej] : 0.0f;
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(B, (uint32_t)N * (uint32_t)K);
+    const int kg = (lane >> 4) * 16;
+    const int k_begin = wave * 64 * C;
+    i32x4v b[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) b[c] = __builtin_amdgcn_raw_buffer_load_b128(rb, ej * K + kg, k_begin + 64 * c, 0);
+    __builtin_amdgcn_sched_barrier(0);
+
+    AbsMax am;
+#pragma unroll
+    for (int h = 0; h < XH; ++h) am.add4(xv[h]);
+    const unsigned wb = wave_max(am.bits());
+    if (lane == 0) wmax[wave] = wb;
+    __builtin_amdgcn_s_waitcnt(wait_imm(63, 0));
+    __builtin_amdgcn_s_barrier();
+    unsigned mb = wmax[0];
+#pragma unroll
+    for (int w = 1; w < W; ++w) mb = max(mb, wmax[w]);
+    const Scale sc = make_scale(mb);
+    if (blockIdx.x == 0 && tid == 0) {
+        *sx_out = sc.s;
+        if (sc.bad) flag_nonfinite(fault);
+    }
+    // Element 4 e4 is row e4 / (K / 4), column 4 (e4 % (K / 4)).
+    auto code_at = [](int e4) {
+        const int m = e4 / (K / 4), k4 = e4 % (K / 4);
+        return m * K + ((((k4 >> 2) ^ (m & 15))) << 4) + ((k4 & 3) << 2);
+    };
+#pragma unroll
+    for (int h = 0; h < XH; ++h) {
+        const int e4 = tid + h * T;
+        if (h * T < nx4 && e4 < nx4) {
+            const unsigned w4 = pack4(xv[h], sc);
+            *reinterpret_cast<unsigned*>(codes + code_at(e4)) = w4;
+            if (blockIdx.x == 0) *reinterpret_cast<unsigned*>(q_out + (int64_t)e4 * 4) = w4;
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(wait_imm(63, 0));
+    __builtin_amdgcn_s_barrier();
+
+    // A fragments: lane l holds 16 codes of row 16 t + l % 16 (zero past M)
+    // at k = k_begin + 64 c + 16 (l / 16).
+    i32x4v acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = i32x4v{0, 0, 0, 0};
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            const int row = t * 16 + (lane & 15);
+            i32x4v a = i32x4v{0, 0, 0, 0};
+            if (row < M) a = *reinterpret_cast<const i32x4v*>(codes + code_at(row * (K / 4) + ((k_begin + 64 * c + kg) >> 2)));
+            acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[c], acc[t], 0, 0, 0);
+        }
+#pragma unroll
+    for (int t = 0; t < MT; ++t) red[wave][t][lane] = acc[t];
+    __syncthreads();
+    if (wave >= MT) return;
+    const int j = n0 + (lane & 15);
+    if (j >= N) return;
+    i32x4v sum = red[0][wave][lane];
+#pragma unroll
+    for (int w = 1; w < W; ++w) sum += red[w][wave][lane];
+    // 16x16 MFMA result layout: register r of lane l holds row 4*(l/16) + r.
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int i = wave * 16 + 4 * (lane >> 4) + r;
+        if (i >= M) continue;
+        float y = (float)((double)sum[r] * (sc.s * sbj));
+        if (bias) y = y + bj;
+        out[(int64_t)i * N + j] = y;
+    }
+}
+
+// True when the one-launch per-tensor Linear covers this call.
+bool tensor_small_fits(const float* x, int64_t M, int64_t K, const int8_t* B, int64_t N, const int8_t* q) {
+    return M >= 1 && M <= 64 && (K == 512 || K == 1024 || K == 2048 || K == 4096) && M * K <= kTensorSmallElems &&
+           N >= 1 &&
+           N * K <= 0xFFFFFFFFLL && N <= 0x7FFFFFFF && kh::aligned(x, 16) && kh::aligned(B, 16) && kh::aligned(q, 4);
+}
+
+int launch_tensor_small(kh::Device* d, const float* x, int64_t M, int64_t K, const int8_t* B, int64_t N,
+                        const double* sb, int sb_per_col, const float* bias, float* out, int8_t* q, double* sx) {
+    const unsigned blocks = (unsigned)((N + 15) / 16);
+    auto go = [&](auto mt, auto c) {
+        linear_i8_tensor_small_kernel<decltype(mt)::value, decltype(c)::value><<<blocks, 512, 0, d->stream>>>(
+            x, (int)M, B, (int)N, sb, sb_per_col, bias, out, q, sx, d->fault);
+    };
+    auto pick_c = [&](auto mt) {
+        switch (K / 512) {
+            case 1: return go(mt, std::integral_constant<int, 1>());
+            case 2: return go(mt, std::integral_constant<int, 2>());
+            case 4: return go(mt, std::integral_constant<int, 4>());
+            case 8: return go(mt, std::integral_constant<int, 8>());
+            default: break;
+        }
+    };
+    const int64_t c = K / 512;
+    if (c != 1 && c != 2 && c != 4 && c != 8) return kh::fail(KH_ERR_INVALID_ARG, "linear_i8_tensor: internal K case");
+    if (M <= 16) pick_c(std::integral_constant<int, 1>());
+    else if (M <= 32) pick_c(std::integral_constant<int, 2>());
+    else pick_c(std::integral_constant<int, 4>());
+    return kh::launch_status("linear_i8_tensor_small");
+}
+
 // NB (128-column blocks per tile) of the quantize-on-load kernel for this
 // shape, 0 when it does not take it: M a multiple of 64, N = 128, 256 or a
 // multiple of 384, K of 64, 16-byte aligned X and B, 32-bit offsets.
@@ -1631,6 +1789,21 @@ static int linear_i8_impl(const float* x, int64_t M, int64_t K, const int8_t* b_
     int rc = kh_quantize_rows(x, M, K, q_scratch, sx_scratch);
     if (rc) return rc;
     return kh_gemm_i8(q_scratch, b_packed, M, N, K, sx_scratch, 1, sb, sb_per_col, bias, out, nullptr);
+}
+
+int kh_linear_i8_tensor(const float* x, int64_t M, int64_t K, const int8_t* b_packed, int64_t N, const double* sb,
+                        int sb_per_col, const float* bias, int8_t* q_scratch, double* sx_scratch, float* out) {
+    KH_REQUIRE(out, "kh_linear_i8_tensor: null out");
+    KH_REQUIRE(M >= 0 && K >= 0 && N >= 0, "kh_linear_i8_tensor: negative shape");
+    if (M >= 1 && N >= 1 && x && b_packed && sb && q_scratch && sx_scratch &&
+        tensor_small_fits(x, M, K, b_packed, N, q_scratch)) {
+        KH_DEVICE_OR_RETURN(d);
+        return launch_tensor_small(d, x, M, K, b_packed, N, sb, sb_per_col, bias, out, q_scratch, sx_scratch);
+    }
+    KH_REQUIRE(M * K == 0 || (M <= INT64_MAX / K), "kh_linear_i8_tensor: M * K overflows");
+    int rc = kh_quantize_tensor(x, M * K, q_scratch, sx_scratch);
+    if (rc) return rc;
+    return kh_gemm_i8(q_scratch, b_packed, M, N, K, sx_scratch, 0, sb, sb_per_col, bias, out, nullptr);
 }
 
 int kh_linear_i8(const float* x, int64_t M, int64_t K, const int8_t* b_packed, int64_t N, const double* sb,

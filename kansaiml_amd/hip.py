@@ -179,10 +179,38 @@ def linear_i8(x: DeviceTensor, b_packed: DeviceTensor, sb: DeviceTensor,
     if K != K2:
         raise RuntimeError(f"linear_i8: incompatible shapes {x.shape} x {b_packed.shape}^T")
     sb_mode = _scale_mode(sb, Nn, "linear_i8(sb)")
+    if bias is not None:
+        _need(bias, "float32", 1, "linear_i8(bias)")
+        if bias.shape[0] != Nn:
+            raise RuntimeError("linear_i8: bias must have N entries")
     q = DeviceTensor([M, K], "int8")
     sx = DeviceTensor([M], "float64")
     out = DeviceTensor([M, Nn], "float32")
     N.call("kh_linear_i8", x.ptr, M, K, b_packed.ptr, Nn, sb.ptr, sb_mode, _opt(bias), q.ptr, sx.ptr, out.ptr)
+    return (out, q, sx) if return_codes else out
+
+
+def linear_i8_tensor(x: DeviceTensor, b_packed: DeviceTensor, sb: DeviceTensor,
+                     bias: DeviceTensor | None = None, return_codes: bool = False):
+    """Per-tensor dynamic quantize of x [M, K] fp32 (one scale), then the int8
+    GEMM with the fused epilogue: QLinear(mode="int8",
+    act_granularity="tensor").  With return_codes, also returns the codes
+    (int8 [M, K]) and the scale (float64 [1])."""
+    _need(x, "float32", 2, "linear_i8_tensor(x)")
+    _need(b_packed, "int8", 2, "linear_i8_tensor(w)")
+    M, K = x.shape
+    Nn, K2 = b_packed.shape
+    if K != K2:
+        raise RuntimeError(f"linear_i8_tensor: incompatible shapes {x.shape} x {b_packed.shape}^T")
+    sb_mode = _scale_mode(sb, Nn, "linear_i8_tensor(sb)")
+    if bias is not None:
+        _need(bias, "float32", 1, "linear_i8_tensor(bias)")
+        if bias.shape[0] != Nn:
+            raise RuntimeError("linear_i8_tensor: bias must have N entries")
+    q = DeviceTensor([M, K], "int8")
+    sx = DeviceTensor([1], "float64")
+    out = DeviceTensor([M, Nn], "float32")
+    N.call("kh_linear_i8_tensor", x.ptr, M, K, b_packed.ptr, Nn, sb.ptr, sb_mode, _opt(bias), q.ptr, sx.ptr, out.ptr)
     return (out, q, sx) if return_codes else out
 
 

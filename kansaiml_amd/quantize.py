@@ -191,9 +191,7 @@ class QLinear:
         xd = to_device(x, "float32")
         if self.act_granularity == "row":
             return H.linear_i8(xd, self.qweight.codes, self.qweight.scales, self.bias)
-        q, s = H.quantize_tensor(xd)
-        out, _ = H.gemm_i8(q.reshape(xd.shape), self.qweight.codes, s, self.qweight.scales, self.bias)
-        return out
+        return H.linear_i8_tensor(xd, self.qweight.codes, self.qweight.scales, self.bias)
 
     def _trace(self, x):
         """Records this layer into x's graph.  x is a value of this package's

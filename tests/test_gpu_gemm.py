@@ -213,6 +213,36 @@ def test_linear_i8_decode_fused_tokens(hip, M, K, N):
         np.testing.assert_array_equal(bits32(out.numpy()), bits32(expect))
 
 
+@pytest.mark.parametrize("M,K,N", [(64, 512, 512), (1, 512, 17), (16, 4096, 100), (17, 1024, 512),
+                                   (33, 512, 1000), (64, 512, 33), (8, 2048, 4096), (40, 1536, 64)])
+def test_linear_i8_tensor(hip, M, K, N):
+    """kh_linear_i8_tensor (QLinear int8 with a per-tensor activation scale):
+    the one-launch kernel (M <= 64, K = 512, 1024, 2048 or 4096, M*K <=
+    32768) and the two-launch path beyond it ((16, 4096): M*K too large;
+    (40, 1536): K not a power of two) give the oracle's codes, scale and
+    outputs bit for bit, with a
+    per-tensor and a per-column weight scale, no bias, an all-zero input
+    (scale 1.0) and exact ties (binary64 fallback)."""
+    H, D = hip
+    gen = np.random.Generator(np.random.PCG64(M * 131 + K + N))
+    x = gen.standard_normal((M, K), dtype=np.float32)
+    x[0, :4] = np.float32(0.5)                            # with absmax 1.0 below: 63.5, an exact tie
+    x[M - 1, -1] = np.float32(-1.0)
+    x = np.clip(x, -1.0, 1.0).astype(np.float32)          # absmax exactly 1.0: scale 1/127
+    qw = gen.integers(-127, 128, (N, K), dtype=np.int8)
+    sw = gen.uniform(1e-3, 1e-2, N)
+    bias = gen.standard_normal(N).astype(np.float32)
+    for xin, sb, bb in ((x, sw, bias), (x, sw[:1], None), (np.zeros_like(x), sw, bias)):
+        print(f"linear_i8_tensor M={M} K={K} N={N} per_col={len(sb) > 1} bias={bb is not None}", flush=True)
+        out, q, s = H.linear_i8_tensor(D.from_host(xin), D.from_host(qw), D.from_host(np.asarray(sb, np.float64)),
+                                       D.from_host(bb) if bb is not None else None, return_codes=True)
+        eq, es = O.ko_quantize_tensor(xin)
+        np.testing.assert_array_equal(q.numpy().reshape(M, K), eq.reshape(M, K))
+        np.testing.assert_array_equal(s.numpy().view(np.uint64), np.asarray([es], np.float64).view(np.uint64))
+        expect = O.ko_epilogue(O.ko_gemm_i8(eq.reshape(M, K), qw), np.full(M, es), sb, bb)
+        np.testing.assert_array_equal(bits32(out.numpy()), bits32(expect))
+
+
 def test_dequantize_acc_matches_fused(hip):
     H, D = hip
     gen = np.random.Generator(np.random.PCG64(9))
