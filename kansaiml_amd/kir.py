@@ -550,6 +550,10 @@ def _exec(node, vals):
         bias = ins[2] if at.get("bias") else None
         residual = ins[-1] if at.get("residual") else None
         parts = getattr(x, "absmax_parts", None)
+        if parts is None and not at.get("act") and residual is None and not at.get("absmax"):
+            # No producer partials and a plain epilogue: kh_linear_i8_tensor
+            # (one launch for small activations, C1's shape).
+            return H.linear_i8_tensor(x, w.codes, w.scales, bias)
         if parts is None:
             q, s = H.quantize_tensor(x)
             out, oparts = H.gemm_i8_fused(q, w.codes, s, w.scales, bias, act=at.get("act"), residual=residual,

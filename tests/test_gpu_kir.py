@@ -76,6 +76,11 @@ def test_c1_int8_linear_through_run_hip(K):
     np.testing.assert_array_equal(bits32(layer(x).numpy()), bits32(ey))
     y_unfused = kir.run_hip(kir.trace(layer, x), x)
     np.testing.assert_array_equal(bits32(y_unfused), bits32(ey))
+    # with the quantize fused into the GEMM too (quant_fusion(qload=True):
+    # one launch, kh_linear_i8_tensor, for an activation with no producer)
+    gq = kir.quant_fusion(kir.trace(layer, x), qload=True)
+    assert [n.op for n in gq.nodes if n.attrs.get("qload")] == ["int8_linear"]
+    np.testing.assert_array_equal(bits32(kir.run_hip(gq, x)), bits32(ey))
     # and stays within quantization error of the fp32 reference x @ W + b
     ref = O.ref_add_bias(O.ref_matmul(x, w), b) if O.ref_available() else x @ w + b
     assert np.abs(y - ref).max() < 0.05 * np.abs(ref).max()
