@@ -510,7 +510,6 @@ def bench_c4(steps, warmup):
     model = CharLM(w)
     ids = D.from_host(np.random.Generator(np.random.PCG64(9)).integers(0, 65, (64, 256)).astype(np.int32))
     eager = time_kernel(lambda: model.forward(ids, to_host=False), steps, warmup, tag="c4_eager")
-    model_row = CharLM(w, act_granularity="row")
     if GRAPH_TIMING:
         g = model.capture(64, 256)
         ms = time_kernel(lambda: g(ids, to_host=False), steps, warmup, tag="c4_graph")
@@ -520,17 +519,17 @@ def bench_c4(steps, warmup):
     breakdown = c4_gemm_breakdown(model, ids, ms, steps)
     # the same forward with per-token activation scales (an option beside
     # the reference's per-tensor configuration), replayed as a HIP graph
+    ms_row = None  # a profiled run traces the configured (per-tensor) forward only
     if GRAPH_TIMING:
-        gr = model_row.capture(64, 256)
+        gr = CharLM(w, act_granularity="row").capture(64, 256)
         ms_row = time_kernel(lambda: gr(ids, to_host=False), steps, warmup, tag="c4_graph_per_token")
         gr.close()
-    else:
-        ms_row = time_kernel(lambda: model_row.forward(ids, to_host=False), steps, warmup, tag="c4_eager_per_token")
     ops = int8_linear_ops(w, 64, 256)
     return {"workload": "C4 int8 char-LM forward, batch 64 x seq 256 (16384 tokens), 6 layers, d 384",
             "timing": "HIP graph replay" if GRAPH_TIMING else "eager (profiled run: no graph launches)",
             "ms_per_forward": round(ms, 4), "tokens_per_s": round(64 * 256 / (ms * 1e-3), 1),
-            "ms_per_forward_eager": round(eager, 4), "ms_per_forward_per_token_scales": round(ms_row, 4),
+            "ms_per_forward_eager": round(eager, 4),
+            "ms_per_forward_per_token_scales": round(ms_row, 4) if ms_row is not None else None,
             "int8_linear_ops": ops, "int8_linear_TOPS_over_forward": round(ops / (ms * 1e-3) / 1e12, 2),
             "attention_fp32_flops_full_square": attention_flops(w, 64, 256), **breakdown}
 
@@ -582,9 +581,10 @@ ALGO_BYTES = {"gemm_i8_8192": 2 * 8192 * 8192 + 4 * 8192 * 8192, "quant_rows_163
 #   rocprofv3 <profiler args> -d OUT/<name> -o run --output-format csv -- python3 bench.py <bench args>
 # (`bench.py --profile-commands OUT` prints them).  One counter group per run:
 # a pass may hold at most 8 SQ_, 4 TCC_, 4 TCP_, 2 TA_, 2 TD_ and 2 GRBM_ counters.
-_GEMM_ARGS = "--only gemm --steps 3 --warmup 1 --no-cpu --warm-ms 0"
-_C4_ARGS = "--only c4 --steps 4 --warmup 2 --no-cpu --warm-ms 0"
-_TRAFFIC_ARGS = "--only gemm,quant,f32,copy --steps 3 --warmup 1 --no-cpu --warm-ms 0"
+# Every run passes --no-graph-timing: no HIP graph is launched under the profiler.
+_GEMM_ARGS = "--only gemm --steps 3 --warmup 1 --no-cpu --warm-ms 0 --no-graph-timing"
+_C4_ARGS = "--only c4 --steps 4 --warmup 2 --no-cpu --warm-ms 0 --no-graph-timing"
+_TRAFFIC_ARGS = "--only gemm,quant,f32,copy --steps 3 --warmup 1 --no-cpu --warm-ms 0 --no-graph-timing"
 PROFILE_RUNS = {
     "trace": ("--kernel-trace --stats", "--no-cpu --warm-ms 10 --no-graph-timing"),
     "fetch": ("--pmc FETCH_SIZE", _TRAFFIC_ARGS),
