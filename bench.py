@@ -891,9 +891,8 @@ def _summarize_c4_forward(root):
         total += per
     table.sort(key=lambda t: -t[0])
     body = (f"Workload: config C4 (vocab 65, d_model 384, 6 heads, 6 layers, FFN 1536, batch 64 x seq 256), the "
-            f"default `CharLM` forward run eagerly (the kernels a HIP-graph replay launches, without the replay's "
-            f"64 KB id copy: rocprofv3's kernel trace has crashed inside hipGraphLaunch).  The trace is split into "
-            f"forwards at each embedding "
+            f"default `CharLM` forward run eagerly (the kernels a HIP-graph replay launches; rocprofv3's kernel "
+            f"trace has crashed inside hipGraphLaunch).  The trace is split into forwards at each embedding "
             f"launch; the {len(good)} segments holding exactly one forward's {mode} launches give the medians "
             f"below (durations include the profiler's per-dispatch timestamps).\n\n"
             + _md_table(["kernel", "WGs", "launches per forward", "us each", "us per forward"], [t[1] for t in table])
