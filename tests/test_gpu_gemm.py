@@ -214,7 +214,8 @@ def test_linear_i8_decode_fused_tokens(hip, M, K, N):
 
 
 @pytest.mark.parametrize("M,K,N", [(64, 512, 512), (1, 512, 17), (16, 4096, 100), (17, 1024, 512),
-                                   (33, 512, 1000), (64, 512, 33), (8, 2048, 4096), (40, 1536, 64)])
+                                   (33, 512, 1000), (64, 512, 33), (8, 2048, 4096), (40, 1536, 64),
+                                   (8, 4096, 300), (3, 4096, 16)])
 def test_linear_i8_tensor(hip, M, K, N):
     """kh_linear_i8_tensor (QLinear int8 with a per-tensor activation scale):
     the one-launch kernel (M <= 64, K = 512, 1024, 2048 or 4096, M*K <=
