@@ -244,6 +244,40 @@ def test_linear_i8_tensor(hip, M, K, N):
         np.testing.assert_array_equal(bits32(out.numpy()), bits32(expect))
 
 
+@pytest.mark.parametrize("bad", [np.nan, np.inf, -np.inf])
+def test_linear_i8_paths_report_nonfinite(hip, bad):
+    """A NaN or infinite activation reaches a quantizer on every kh_linear_i8 /
+    kh_linear_i8_tensor path (one-launch decode for M = 1 and 3, per-row
+    quantize + skinny GEMM for M = 8, the one-launch and two-launch per-tensor
+    Linear): the next synchronize raises ValueError, as the reference's
+    round(nan) does, and clears the report, so a clean call afterwards is
+    exact."""
+    from kansaiml_amd import _native as Nn
+    H, D = hip
+    gen = np.random.Generator(np.random.PCG64(99))
+    cases = [("row", 1, 4096, 64), ("row", 3, 2048, 48), ("row", 8, 4096, 32),
+             ("tensor", 64, 512, 40), ("tensor", 16, 4096, 24)]
+    for gran, M, K, N_ in cases:
+        print(f"nonfinite {gran} M={M} K={K} N={N_} value={bad}", flush=True)
+        x = gen.standard_normal((M, K), dtype=np.float32)
+        qw = D.from_host(gen.integers(-127, 128, (N_, K), dtype=np.int8))
+        sw = D.from_host(gen.uniform(1e-3, 1e-2, N_))
+        fn = H.linear_i8 if gran == "row" else H.linear_i8_tensor
+        xbad = x.copy()
+        xbad[M - 1, K // 3] = np.float32(bad)
+        fn(D.from_host(xbad), qw, sw)
+        with pytest.raises(ValueError):
+            Nn.synchronize()
+        out = fn(D.from_host(x), qw, sw).numpy()
+        if gran == "row":
+            eq, esx = O.ko_quantize_rows(x)
+        else:
+            eq, es = O.ko_quantize_tensor(x)
+            eq, esx = eq.reshape(M, K), np.full(M, es)
+        np.testing.assert_array_equal(bits32(out), bits32(O.ko_epilogue(O.ko_gemm_i8(eq, qw.numpy()), esx,
+                                                                         sw.numpy(), None)))
+
+
 def test_dequantize_acc_matches_fused(hip):
     H, D = hip
     gen = np.random.Generator(np.random.PCG64(9))
