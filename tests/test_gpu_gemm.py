@@ -155,7 +155,7 @@ def test_linear_i8_per_token(hip):
 
 
 @pytest.mark.parametrize("M,K,N", [(1, 4096, 4096), (2, 4096, 11008), (1, 2048, 1000), (2, 8192, 33),
-                                   (1, 8192, 4096), (2, 2048, 17)])
+                                   (1, 8192, 4096), (2, 2048, 17), (1, 8192, 1), (2, 4096, 2)])
 def test_linear_i8_decode_fused(hip, M, K, N):
     """The fused one-launch decode path of kh_linear_i8 (M <= 2): outputs,
     activation codes and per-token scales bit-exact against the oracle, with
@@ -184,7 +184,7 @@ def test_linear_i8_decode_fused(hip, M, K, N):
 
 @pytest.mark.parametrize("M,K,N", [(3, 4096, 4096), (3, 4096, 11008), (3, 2048, 1000), (3, 2048, 17),
                                    (3, 4096, 33), (8, 4096, 11008), (5, 2048, 1000), (8, 2048, 17), (7, 4096, 33),
-                                   (4, 4096, 4096), (6, 2048, 4096)])
+                                   (4, 4096, 4096), (6, 2048, 4096), (3, 2048, 1), (3, 4096, 5), (2, 8192, 3)])
 def test_linear_i8_decode_fused_tokens(hip, M, K, N):
     """kh_linear_i8 for 3 <= M <= 8 tokens (K = 2048 or 4096): the one-launch
     decode kernel for M = 3 (its lanes' partial products summed by the
