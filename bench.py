@@ -582,7 +582,7 @@ ALGO_BYTES = {"gemm_i8_8192": 2 * 8192 * 8192 + 4 * 8192 * 8192, "quant_rows_163
 # (`bench.py --profile-commands OUT` prints them).  One counter group per run:
 # a pass may hold at most 8 SQ_, 4 TCC_, 4 TCP_, 2 TA_, 2 TD_ and 2 GRBM_ counters.
 # Every run passes --no-graph-timing: no HIP graph is launched under the profiler.
-_GEMM_ARGS = "--only gemm --steps 3 --warmup 1 --no-cpu --warm-ms 0 --no-graph-timing"
+_GEMM_ARGS = "--only gemm --steps 10 --warmup 1 --no-cpu --warm-ms 50 --no-graph-timing"
 _C4_ARGS = "--only c4 --steps 4 --warmup 2 --no-cpu --warm-ms 0 --no-graph-timing"
 _TRAFFIC_ARGS = "--only gemm,quant,f32,copy --steps 3 --warmup 1 --no-cpu --warm-ms 0 --no-graph-timing"
 PROFILE_RUNS = {
