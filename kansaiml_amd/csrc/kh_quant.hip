@@ -171,27 +171,34 @@ __global__ __launch_bounds__(256) void quant_tensor_kernel(const float* __restri
                                                            const unsigned* __restrict__ partials, int nparts,
                                                            unsigned* __restrict__ fault) {
     __shared__ unsigned red[4];
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    const int64_t n4 = n >> 2;
+    const f32x4* x4 = reinterpret_cast<const f32x4*>(x);
+    // kTensorUnroll float4 per thread in flight before the first code is
+    // stored (one load at a time per wave left HBM idle between them).  The
+    // first batch is requested before the partials, so the workgroup waits
+    // for one memory round trip before its first store, not two.
+    constexpr int U = kTensorUnroll;
+    const int64_t first = (int64_t)blockIdx.x * 256 * U + threadIdx.x;
+    f32x4 v[U];
+    auto load = [&](int64_t i0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t i = i0 + (int64_t)u * 256;
+            v[u] = i < n4 ? x4[i] : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    if (VEC) load(first);
     const unsigned mb = block_reduce_partials(partials, nparts, red);
     const Scale sc = make_scale(mb);
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         scale[0] = sc.s;
         if (sc.bad) flag_nonfinite(fault);
     }
-    const int64_t stride = (int64_t)gridDim.x * 256;
     if (VEC) {
-        const int64_t n4 = n >> 2;
-        const f32x4* x4 = reinterpret_cast<const f32x4*>(x);
         unsigned* q4 = reinterpret_cast<unsigned*>(q);
-        // kTensorUnroll float4 per thread in flight before the first code is
-        // stored (one load at a time per wave left HBM idle between them).
-        constexpr int U = kTensorUnroll;
-        for (int64_t i0 = (int64_t)blockIdx.x * 256 * U + threadIdx.x; i0 < n4; i0 += stride * U) {
-            f32x4 v[U];
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int64_t i = i0 + (int64_t)u * 256;
-                v[u] = i < n4 ? x4[i] : f32x4{0.f, 0.f, 0.f, 0.f};
-            }
+        for (int64_t i0 = first; i0 < n4; i0 += stride * U) {
+            if (i0 != first) load(i0);
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int64_t i = i0 + (int64_t)u * 256;

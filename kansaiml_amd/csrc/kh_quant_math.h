@@ -138,16 +138,16 @@ __device__ __forceinline__ unsigned pack4(f32x4 v, const Scale& sc) {
 // LDS); every thread gets the max bits.
 __device__ __forceinline__ unsigned block_reduce_partials(const unsigned* __restrict__ partials, int count,
                                                           unsigned* red) {
-    // Eight independent loads in flight per thread (the partials are L2
-    // resident; a dependent chain of loads would be latency-bound).
+    // Eight loads per thread issued before any is used (the partials are L2
+    // resident; loads that each wait for the one before are one L2 round
+    // trip apiece).  An index past the end reads the last partial again,
+    // which leaves the maximum unchanged.
     unsigned m8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     const int step = blockDim.x;
-    int i = threadIdx.x;
-    for (; i + 7 * step < count; i += 8 * step) {
+    for (int i = threadIdx.x; i < count; i += 8 * step) {
 #pragma unroll
-        for (int u = 0; u < 8; ++u) m8[u] = max(m8[u], partials[i + u * step]);
+        for (int u = 0; u < 8; ++u) m8[u] = max(m8[u], partials[min(i + u * step, count - 1)]);
     }
-    for (; i < count; i += step) m8[0] = max(m8[0], partials[i]);
     unsigned mb = max(max(max(m8[0], m8[1]), max(m8[2], m8[3])), max(max(m8[4], m8[5]), max(m8[6], m8[7])));
     mb = wave_max(mb);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x / 64] = mb;
