@@ -133,18 +133,22 @@ __device__ __forceinline__ unsigned pack4(f32x4 v, const Scale& sc) {
     return pack4_checked(v, sc);
 }
 
-// Reduces per-workgroup absmax partials[0..count) across the block (any
-// multiple of 64 threads up to 1024; `red` holds blockDim.x / 64 words of
-// LDS); every thread gets the max bits.
-__device__ __forceinline__ unsigned block_reduce_partials(const unsigned* __restrict__ partials, int count,
-                                                          unsigned* red) {
-    // Eight loads per thread issued before any is used (the partials are L2
-    // resident; loads that each wait for the one before are one L2 round
-    // trip apiece).  An index past the end reads the last partial again,
-    // which leaves the maximum unchanged.
-    unsigned m8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+// block_reduce_partials in two halves, so a kernel can issue other loads
+// around the partials' and wait for all of them together.  The first issues
+// this thread's first eight loads (an index past the end reads the last
+// partial again, which leaves the maximum unchanged; count >= 1).
+__device__ __forceinline__ void partials_first_loads(const unsigned* __restrict__ partials, int count,
+                                                     unsigned (&m8)[8]) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) m8[u] = partials[min((int)threadIdx.x + u * (int)blockDim.x, count - 1)];
+}
+
+// The second: the rest of the partials, eight loads at a time, then the
+// workgroup's maximum (every thread of the workgroup calls it).
+__device__ __forceinline__ unsigned partials_finish(const unsigned* __restrict__ partials, int count,
+                                                    unsigned (&m8)[8], unsigned* red) {
     const int step = blockDim.x;
-    for (int i = threadIdx.x; i < count; i += 8 * step) {
+    for (int i = threadIdx.x + 8 * step; i < count; i += 8 * step) {
 #pragma unroll
         for (int u = 0; u < 8; ++u) m8[u] = max(m8[u], partials[min(i + u * step, count - 1)]);
     }
@@ -155,6 +159,19 @@ __device__ __forceinline__ unsigned block_reduce_partials(const unsigned* __rest
     mb = red[0];
     for (int i = 1; i < (int)(blockDim.x / 64); ++i) mb = max(mb, red[i]);
     return mb;
+}
+
+// Reduces per-workgroup absmax partials[0..count) across the block (any
+// multiple of 64 threads up to 1024; `red` holds blockDim.x / 64 words of
+// LDS); every thread gets the max bits.
+__device__ __forceinline__ unsigned block_reduce_partials(const unsigned* __restrict__ partials, int count,
+                                                          unsigned* red) {
+    // Eight loads per thread issued before any is used: the partials are L2
+    // resident, and loads that each wait for the one before cost one L2
+    // round trip apiece.
+    unsigned m8[8];
+    partials_first_loads(partials, count, m8);
+    return partials_finish(partials, count, m8, red);
 }
 
 // What a kernel producing the input of a per-tensor quantize does with each

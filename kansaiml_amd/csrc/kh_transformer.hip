@@ -303,31 +303,40 @@ __device__ __forceinline__ unsigned layernorm_rows_vec(const float* __restrict__
 // eps) are computed once per pair; the reductions stay in the VALU
 // (kh::lanes::half_sum).  Otherwise as layernorm_rows_vec: all loads before any
 // arithmetic, the centred values multiplied by the correctly rounded
-// 1 / sqrt(var + eps), rows >= `rows` computed on zeros.  Leaves the
-// normalized values in v and each pair's largest |value| bits in rm.
+// 1 / sqrt(var + eps).  Rows >= `rows` are computed on a copy of the last row
+// and their results discarded (each row's sums stay within its half-wave).
+// Leaves the normalized values in v and each pair's largest |value| bits in rm.
 constexpr int kLnPairs = kLnRowsPerWave / 2;
 
 template <int KH>
-__device__ __forceinline__ void layernorm_half_values(const float* __restrict__ x, int64_t row0, int64_t rows, int D,
-                                                      const float* __restrict__ w, const float* __restrict__ b,
-                                                      float eps, kh::quant::f32x4 (&v)[kLnPairs][KH],
-                                                      unsigned (&rm)[kLnPairs], int lane) {
+__device__ __forceinline__ void layernorm_half_loads(const float* __restrict__ x, int64_t row0, int64_t rows, int D,
+                                                     const float* __restrict__ w, const float* __restrict__ b,
+                                                     kh::quant::f32x4 (&v)[kLnPairs][KH], kh::quant::f32x4 (&wv)[KH],
+                                                     kh::quant::f32x4 (&bv)[KH], int lane) {
     using kh::quant::f32x4;
     constexpr int P = kLnPairs;
     const int half = lane >> 5, hl = lane & 31;
 #pragma unroll
     for (int p = 0; p < P; ++p) {
-        const int64_t row = row0 + 2 * p + half;
+        // A row past the end loads the last row (rows >= 1): every load is
+        // unconditional, so no branch splits them and they all go out before
+        // the first wait.
+        const int64_t row = min(row0 + 2 * p + half, rows - 1);
 #pragma unroll
-        for (int i = 0; i < KH; ++i)
-            v[p][i] = row < rows ? reinterpret_cast<const f32x4*>(x + row * D)[hl + 32 * i] : f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < KH; ++i) v[p][i] = reinterpret_cast<const f32x4*>(x + row * D)[hl + 32 * i];
     }
-    f32x4 wv[KH], bv[KH];
 #pragma unroll
     for (int i = 0; i < KH; ++i) {
         wv[i] = reinterpret_cast<const f32x4*>(w)[hl + 32 * i];
         bv[i] = reinterpret_cast<const f32x4*>(b)[hl + 32 * i];
     }
+}
+
+template <int KH>
+__device__ __forceinline__ void layernorm_half_math(int D, float eps, kh::quant::f32x4 (&v)[kLnPairs][KH],
+                                                    const kh::quant::f32x4 (&wv)[KH],
+                                                    const kh::quant::f32x4 (&bv)[KH], unsigned (&rm)[kLnPairs]) {
+    constexpr int P = kLnPairs;
     float mean[P], inv[P];
 #pragma unroll
     for (int p = 0; p < P; ++p) {
@@ -359,21 +368,38 @@ __device__ __forceinline__ void layernorm_half_values(const float* __restrict__ 
     }
 }
 
-// layernorm_half_values, then MODE's output; returns this lane's largest
-// |out| bits over its rows < `rows`.
+// layernorm_half_loads and layernorm_half_math, then MODE's output; returns
+// this lane's largest |out| bits over its rows < `rows`.  MODE kOutQuant
+// reduces the pass-1 partials qparts[0..nqparts) to the tensor's scale here
+// (workgroup 0 stores it to *scales; `red`: 4 words of LDS), with their
+// loads issued behind the rows': the LayerNorm arithmetic waits only for the
+// rows, and one memory round trip covers both.  kLnRowQuant stores each
+// row's scale to scales[row].  Every thread of the workgroup calls it.
 template <int KH, int MODE>
 __device__ __forceinline__ unsigned layernorm_rows_half(const float* __restrict__ x, int64_t row0, int64_t rows,
                                                         int D, const float* __restrict__ w,
                                                         const float* __restrict__ b, float eps,
                                                         float* __restrict__ out, int8_t* __restrict__ q,
-                                                        const kh::quant::Scale& sc, double* __restrict__ rscales,
+                                                        const unsigned* __restrict__ qparts, int nqparts,
+                                                        unsigned* red, double* __restrict__ scales,
                                                         unsigned* __restrict__ fault, int lane) {
     using namespace kh::quant;
     constexpr int P = kLnPairs;
     const int half = lane >> 5, hl = lane & 31;
-    f32x4 v[P][KH];
+    f32x4 v[P][KH], wv[KH], bv[KH];
     unsigned rm[P];
-    layernorm_half_values<KH>(x, row0, rows, D, w, b, eps, v, rm, lane);
+    layernorm_half_loads<KH>(x, row0, rows, D, w, b, v, wv, bv, lane);
+    unsigned m8[8];
+    if constexpr (MODE == kOutQuant) partials_first_loads(qparts, nqparts, m8);
+    layernorm_half_math<KH>(D, eps, v, wv, bv, rm);
+    Scale sc{};
+    if constexpr (MODE == kOutQuant) {
+        sc = make_scale(partials_finish(qparts, nqparts, m8, red));
+        if (blockIdx.x == 0 && threadIdx.x == 0) {
+            *scales = sc.s;
+            if (sc.bad) flag_nonfinite(fault);
+        }
+    }
     unsigned mx = 0;
 #pragma unroll
     for (int p = 0; p < P; ++p) {
@@ -383,7 +409,7 @@ __device__ __forceinline__ unsigned layernorm_rows_half(const float* __restrict_
             const Scale rs = make_scale(kh::lanes::half_max(rm[p]));
             if (row >= rows) continue;
             if (hl == 0) {
-                rscales[row] = rs.s;
+                scales[row] = rs.s;
                 if (rs.bad) flag_nonfinite(fault);
             }
 #pragma unroll
@@ -403,8 +429,9 @@ __device__ __forceinline__ unsigned layernorm_rows_half(const float* __restrict_
 
 // A 256-thread workgroup normalizes kLnRowsPerBlock rows, each wave one row
 // at a time, and (when parts is given) writes the max |out| of its rows.
-// MODE kOutQuant first reduces the pass-1 partials qparts[0..nqparts) to the
-// tensor's scale (workgroup 0 stores it to *qscale).
+// MODE kOutQuant reduces the pass-1 partials qparts[0..nqparts) to the
+// tensor's scale (workgroup 0 stores it to *qscale): first, or on the
+// two-rows-per-wave path once its row loads are issued.
 constexpr int kLnRowsPerBlock = 16;
 
 // KV: 0 for the scalar path, else float4 columns per lane of the vectorized
@@ -421,7 +448,7 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict_
     __shared__ unsigned wmax[4];
     const int lane = threadIdx.x & 63;
     Scale sc{};
-    if (MODE == kOutQuant) {
+    if (MODE == kOutQuant && !(KV > 0 && HALF)) {
         sc = make_scale(block_reduce_partials(qparts, nqparts, wmax));
         if (blockIdx.x == 0 && threadIdx.x == 0) {
             *qscale = sc.s;
@@ -433,7 +460,8 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict_
         static_assert(kLnRowsPerBlock == 4 * kLnRowsPerWave, "four waves");
         const int64_t row0 = (int64_t)blockIdx.x * kLnRowsPerBlock + (threadIdx.x >> 6) * kLnRowsPerWave;
         if constexpr (HALF)
-            mx = layernorm_rows_half<KV, MODE>(x, row0, rows, D, w, b, eps, out, q, sc, qscale, fault, lane);
+            mx = layernorm_rows_half<KV, MODE>(x, row0, rows, D, w, b, eps, out, q, qparts, nqparts, wmax, qscale,
+                                               fault, lane);
         else
             mx = layernorm_rows_vec<KV, MODE>(x, row0, rows, D, w, b, eps, out, q, sc, qscale, fault, lane);
     } else {
