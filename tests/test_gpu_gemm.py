@@ -340,6 +340,7 @@ def test_matmul_f32_c3b_full_size(hip):
 @pytest.mark.parametrize("M,N,K", [(512, 512, 256),      # ping-pong, full tiles
                                    (300, 1152, 384),     # ping-pong, partial tiles
                                    (130, 70, 80),        # general kernel (K % 64 != 0)
+                                   (16384, 65, 384),     # ping-pong, one partial column tile (a vocabulary head)
                                    (8, 512, 512)])       # skinny kernel
 @pytest.mark.parametrize("row_scales", [False, True])
 def test_gemm_i8_fused_epilogues(hip, M, N, K, row_scales):
