@@ -100,6 +100,32 @@ def test_quantize_tensor_vs_oracle(hip, n):
     np.testing.assert_array_equal(bits32(H.dequantize_tensor(q, s).numpy()), bits32(O.ko_dequantize_tensor(eq, es)))
 
 
+@pytest.mark.parametrize("count", [1, 3, 255, 2049, 5000])
+def test_quantize_tensor_parts_any_partial_count(hip, count):
+    """kh_quantize_tensor_parts takes the tensor's scale from any number of
+    producer partials: one, fewer than a workgroup has threads, and several
+    rounds of eight loads per thread, with the largest partial first, in the
+    middle or last.  Every other partial is |0.25|, below the tensor's
+    absmax, so a partial left out of the maximum changes the scale and every
+    code."""
+    from kansaiml_amd import _native as Nn
+    H, D = hip
+    gen = np.random.Generator(np.random.PCG64(count + 17))
+    x = gen.standard_normal(70001, dtype=np.float32)
+    eq, es = O.ko_quantize_tensor(x)
+    top = np.abs(x).max().astype(np.float32).view(np.uint32)
+    xd = D.from_host(x)
+    for pos in sorted({0, count // 2, count - 1}):
+        print(f"partials count={count} max at {pos}", flush=True)
+        parts = np.full(count, np.float32(0.25).view(np.uint32), np.uint32)
+        parts[pos] = top
+        pd = D.from_host(parts.view(np.int32))
+        q, sc = D([x.size], "int8"), D([1], "float64")
+        Nn.call("kh_quantize_tensor_parts", xd.ptr, x.size, pd.ptr, count, q.ptr, sc.ptr)
+        np.testing.assert_array_equal(q.numpy(), eq)
+        assert sc.numpy()[0] == es
+
+
 @pytest.mark.parametrize("k,n", [(512, 512), (4096, 4096), (384, 1536), (1536, 384), (19, 15), (100, 65)])
 def test_quantize_weight_packed_vs_oracle(hip, k, n):
     H, D = hip
