@@ -87,6 +87,12 @@ int kh_pool_trim(void);
 /* bytes currently handed out, bytes cached in free lists, number of
  * hipMalloc calls made so far. */
 int kh_pool_stats(size_t* in_use, size_t* cached, size_t* driver_allocs);
+/* The library's own scratch area (absmax partials and the like, outside the
+ * pool): its size in bytes, the number of requests made of it so far and
+ * the number of hipMalloc calls it made.  No reference counterpart: the
+ * reference has no device scratch; it lets a caller check that a call used
+ * none (kh_linear_i8_noalloc). */
+int kh_scratch_stats(size_t* bytes, size_t* requests, size_t* driver_allocs);
 
 /* Copies.  kh_memcpy_h2d / kh_memcpy_d2h are synchronous with respect to
  * the host (they order after queued work on the library stream), as the

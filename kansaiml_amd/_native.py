@@ -51,6 +51,7 @@ _SIGNATURES = {
     "kh_free": [_vp],
     "kh_pool_trim": [],
     "kh_pool_stats": [ctypes.POINTER(_size), ctypes.POINTER(_size), ctypes.POINTER(_size)],
+    "kh_scratch_stats": [ctypes.POINTER(_size), ctypes.POINTER(_size), ctypes.POINTER(_size)],
     "kh_memcpy_h2d": [_vp, _vp, _size],
     "kh_memcpy_d2h": [_vp, _vp, _size],
     "kh_memcpy_d2d": [_vp, _vp, _size],
@@ -181,6 +182,12 @@ def pool_stats() -> dict:
     a, b, c = _size(), _size(), _size()
     call("kh_pool_stats", ctypes.byref(a), ctypes.byref(b), ctypes.byref(c))
     return {"in_use": a.value, "cached": b.value, "driver_allocs": c.value}
+
+
+def scratch_stats() -> dict:
+    a, b, c = _size(), _size(), _size()
+    call("kh_scratch_stats", ctypes.byref(a), ctypes.byref(b), ctypes.byref(c))
+    return {"bytes": a.value, "requests": b.value, "driver_allocs": c.value}
 
 
 class Event:

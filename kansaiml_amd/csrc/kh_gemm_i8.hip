@@ -628,7 +628,10 @@ __global__ __launch_bounds__(512, BN == 256 ? 2 : ((BM == 256 || NS >= 4 || (FUS
                                                                     lane, sa_t, acc[a][b], sc, ce[b]));
                 __builtin_amdgcn_sched_barrier(0);
             }
-    } else if (full && !ep.acc && !ep.sa_per_row && (MODE != kh::quant::kOutStore || ep.out) && N <= (1 << 24)) {
+    } else if (full && !ep.acc && !ep.sa_per_row && (MODE != kh::quant::kOutStore || ep.out) && N <= (1 << 24) &&
+               (MODE != kh::quant::kOutQuant || ((N & 3) == 0 && ((uintptr_t)ep.q & 3) == 0))) {
+        // (The quantize pass of store_block32_full writes a dword of four
+        // codes per lane: it needs every row of q 4-byte aligned.)
         const double sa = ep.sa[0];
 #pragma unroll
         for (int a = 0; a < kTM; ++a)
@@ -1411,9 +1414,14 @@ int launch_decode(kh::Device* d, const float* x, int64_t M, const int8_t* B, int
     else if (M == 2)
         linear_i8_decode_kernel<S, 2><<<blocks, 512, 0, d->stream>>>(x, (int)M, B, (int)N, sb, sb_per_col, bias, out, q,
                                                                       sx, d->fault);
-    else if constexpr (S <= 8)
+    else if constexpr (S <= 8) {
+        if (M > 3) return kh::fail(KH_ERR_INVALID_ARG, "linear_i8_decode: more than three tokens");
         linear_i8_decode_kernel<S, 4><<<blocks, 512, 0, d->stream>>>(x, (int)M, B, (int)N, sb, sb_per_col, bias, out, q,
                                                                       sx, d->fault);
+    } else {
+        // The four-row kernel's activations do not fit its registers at this K.
+        return kh::fail(KH_ERR_INVALID_ARG, "linear_i8_decode: three tokens need K <= 4096");
+    }
     return kh::launch_status("linear_i8_decode");
 }
 

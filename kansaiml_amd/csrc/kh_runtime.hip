@@ -59,6 +59,8 @@ struct DeviceSlot {
     std::mutex scratch_mu;
     void* scratch = nullptr;
     size_t scratch_bytes = 0;
+    size_t scratch_requests = 0;  // scratch_area calls
+    size_t scratch_mallocs = 0;   // hipMalloc calls made for the scratch area
     std::vector<void*> retired_scratch;  // outgrown while graphs that use it were alive
     bool ready = false;
 };
@@ -182,6 +184,7 @@ Device* current_initialized() {
 void* scratch_area(Device* d, size_t bytes) {
     DeviceSlot& s = g_slots[d->id];
     std::lock_guard<std::mutex> lk(s.scratch_mu);
+    ++s.scratch_requests;
     if (bytes <= s.scratch_bytes) return s.scratch;
     size_t want = bytes < (1u << 20) ? (1u << 20) : size_class(bytes);
     bool capturing, graphs;
@@ -212,6 +215,7 @@ void* scratch_area(Device* d, size_t bytes) {
         s.scratch_bytes = 0;
     }
     void* p = nullptr;
+    ++s.scratch_mallocs;
     if (hip_status(hipMalloc(&p, want), "hipMalloc(scratch)") != KH_OK) return nullptr;
     s.scratch = p;
     s.scratch_bytes = want;
@@ -389,6 +393,16 @@ int kh_pool_stats(size_t* in_use, size_t* cached, size_t* driver_allocs) {
     if (in_use) *in_use = pool.in_use;
     if (cached) *cached = pool.cached;
     if (driver_allocs) *driver_allocs = pool.driver_allocs;
+    return KH_OK;
+}
+
+int kh_scratch_stats(size_t* bytes, size_t* requests, size_t* driver_allocs) {
+    KH_DEVICE_OR_RETURN(d);
+    kh::DeviceSlot& slot = kh::g_slots[d->id];
+    std::lock_guard<std::mutex> lk(slot.scratch_mu);
+    if (bytes) *bytes = slot.scratch_bytes;
+    if (requests) *requests = slot.scratch_requests;
+    if (driver_allocs) *driver_allocs = slot.scratch_mallocs;
     return KH_OK;
 }
 

@@ -116,13 +116,13 @@ def test_gemm_i8_c3a_full_size(hip):
     np.testing.assert_array_equal(acc[::97][:, cols], eacc_c)
 
 
+@pytest.mark.parametrize("K,N", [(4096, 11008), (4096, 4096)])
 @pytest.mark.parametrize("M", [1, 3, 8, 16, 17, 32, 33, 48, 64])
-def test_skinny_per_token_and_per_channel(hip, M):
+def test_skinny_per_token_and_per_channel(hip, M, K, N):
     """Config C5 shapes through kh_linear_i8: per-token activations, per-output-
-    channel weights with 0.5% outlier columns x20, K=4096, N=11008."""
+    channel weights with 0.5% outlier columns x20, K=4096, N=11008 and 4096."""
     H, D = hip
-    K, N = 4096, 11008
-    gen = np.random.Generator(np.random.PCG64(100 + M))
+    gen = np.random.Generator(np.random.PCG64(100 + M + N))
     x = gen.standard_normal((M, K), dtype=np.float32)
     w = gen.standard_normal((K, N), dtype=np.float32) * np.float32(0.02)
     cols = gen.choice(N, size=N // 200, replace=False)
@@ -135,6 +135,66 @@ def test_skinny_per_token_and_per_channel(hip, M):
     np.testing.assert_array_equal(qw.numpy(), eqw)
     qx, sx = O.ko_quantize_rows(x)
     expect = O.ko_epilogue(O.ko_gemm_i8(qx, eqw), sx, esw, bias)
+    np.testing.assert_array_equal(bits32(out), bits32(expect))
+
+
+_C5_WEIGHTS = {}
+
+
+def _c5_weights(H, D, K, N):
+    """C5's weights (N(0, 0.02), 0.5 % of the columns x20) as per-output-
+    channel codes packed [N, K] and their binary64 scales, on the device and
+    from the oracle (built once per shape)."""
+    if (K, N) not in _C5_WEIGHTS:
+        gen = np.random.Generator(np.random.PCG64(K + 7 * N))
+        w = gen.standard_normal((K, N), dtype=np.float32) * np.float32(0.02)
+        w[:, gen.choice(N, size=N // 200, replace=False)] *= np.float32(20.0)
+        eqw, esw = O.ko_quantize_cols_packed(w)
+        _C5_WEIGHTS[(K, N)] = (D.from_host(eqw), D.from_host(esw), eqw, esw)
+    return _C5_WEIGHTS[(K, N)]
+
+
+def _c5_activations(gen, M, K):
+    """fp32 activations ~N(0, 1) with the rows a per-token quantizer must get
+    right: row 0 all zeros (scale 1.0, codes 0), row 1 exact ties (max 127
+    gives scale 1.0 and the other values k + 1/2, rounded to even), row 2
+    near-ties (the binary32 neighbours of k + 1/2 at scale 1.0) and the
+    last row a single outlier."""
+    x = gen.standard_normal((M, K), dtype=np.float32)
+    if M >= 2:
+        x[0] = 0.0
+    if M >= 3:
+        k = gen.integers(-126, 126, K).astype(np.float32)
+        x[1] = k + np.float32(0.5)
+        x[1, 0] = 127.0
+    if M >= 4:
+        k = gen.integers(-126, 126, K).astype(np.float32) + np.float32(0.5)
+        x[2] = np.where(gen.integers(0, 2, K) == 1, np.nextafter(k, np.float32(200)),
+                        np.nextafter(k, np.float32(-200)))
+        x[2, 5] = -127.0
+    if M >= 5:
+        x[M - 1, K // 2] = np.float32(-50.0)
+    return x
+
+
+@pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 11008)])
+@pytest.mark.parametrize("M", [2, 3, 4, 5, 8, 16, 17, 31, 32])
+def test_c5_linear_i8_special_rows(hip, M, K, N):
+    """Config C5 through kh_linear_i8 at every decode-path M: codes, scales
+    and outputs bit-exact against the oracle's per-row quantize, int32 GEMM
+    and binary64 epilogue, with a zero row, an exact-tie row, a near-tie row
+    and an outlier row among the tokens."""
+    H, D = hip
+    qwd, swd, eqw, esw = _c5_weights(H, D, K, N)
+    gen = np.random.Generator(np.random.PCG64(1000 + M + N))
+    x = _c5_activations(gen, M, K)
+    bias = gen.standard_normal(N).astype(np.float32)
+    out, q, sx = H.linear_i8(D.from_host(x), qwd, swd, D.from_host(bias), return_codes=True)
+    out = out.numpy()
+    eq, es = O.ko_quantize_rows(x)
+    np.testing.assert_array_equal(q.numpy(), eq)
+    np.testing.assert_array_equal(sx.numpy().view(np.uint64), es.view(np.uint64))
+    expect = O.ko_epilogue(O.ko_gemm_i8(eq, eqw), es, esw, bias)
     np.testing.assert_array_equal(bits32(out), bits32(expect))
 
 
@@ -255,7 +315,8 @@ def test_linear_i8_paths_report_nonfinite(hip, bad):
     from kansaiml_amd import _native as Nn
     H, D = hip
     gen = np.random.Generator(np.random.PCG64(99))
-    cases = [("row", 1, 4096, 64), ("row", 3, 2048, 48), ("row", 8, 4096, 32),
+    cases = [("row", 1, 4096, 64), ("row", 3, 2048, 48), ("row", 8, 4096, 32), ("row", 17, 4096, 4096),
+             ("row", 32, 4096, 11008),
              ("tensor", 64, 512, 40), ("tensor", 16, 4096, 24)]
     for gran, M, K, N_ in cases:
         print(f"nonfinite {gran} M={M} K={K} N={N_} value={bad}", flush=True)
@@ -383,6 +444,7 @@ def test_gemm_i8_fused_epilogues(hip, M, N, K, row_scales):
 @pytest.mark.parametrize("M,N,K", [(16384, 1536, 384),   # C4 fc1: ping-pong, two passes
                                    (300, 1152, 384),     # partial tiles
                                    (1000, 1000, 1536),   # K > 512: the passes still take 128x128 tiles
+                                   (256, 258, 128),      # N % 4 == 2: full interior tiles store codes bytewise
                                    (130, 70, 80),        # general kernel (K % 64 != 0): fp32 temporary
                                    (8, 512, 512)])       # skinny kernel: fp32 temporary
 def test_gemm_i8_quant_matches_unfused(hip, M, N, K):

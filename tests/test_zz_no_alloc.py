@@ -4,7 +4,8 @@ Called through the C ABI.  Its output must equal kh_linear_i8's bit for bit
 (both are the per-token quantize, the exact int32 GEMM and the binary64
 dequantize epilogue), on two calls in a row, the second with a smaller input
 (the fixed scratch array keeps the first call's codes), with no pool
-allocation meanwhile.  Sizes beyond the fixed array are rejected."""
+allocation and no use of the library's scratch area meanwhile.  Sizes beyond
+the fixed array are rejected."""
 
 import ctypes
 
@@ -59,12 +60,16 @@ def test_noalloc_matches_linear_i8(lib, first, second):
     outs = [D.empty([c["M"], c["N"]], "float32") for c in cases]
     N.synchronize()
     before = N.pool_stats()
+    scratch_before = N.scratch_stats()
     for c, out in zip(cases, outs):
         print(f"noalloc M={c['M']} K={c['K']} N={c['N']}", flush=True)
         N.call("kh_linear_i8_noalloc", c["x"].ptr, c["M"], c["K"], c["w"].ptr, c["N"], c["sb"].ptr, c["per_col"],
                c["bias"].ptr, out.ptr)
     N.synchronize()
     assert N.pool_stats() == before, "the no-alloc entry point drew from the pool"
+    # The library scratch (outside the pool) is neither requested nor grown:
+    # a path through it would count a request even where it no longer grows.
+    assert N.scratch_stats() == scratch_before, "the no-alloc entry point used the library scratch"
     for w, out in zip(want, outs):
         np.testing.assert_array_equal(out.numpy().view(np.uint32), w)
 
