@@ -256,8 +256,9 @@ def bench_skinny(steps, warmup, rows=None):
     {1, 8, 32}, (K, N) in {(4096, 4096), (4096, 11008)}.  Copies of the
     quantized weight are rotated so more than 512 MB of distinct weights pass
     through HBM (beyond the 256 MB Infinity Cache).  `us` is the average over
-    `steps` dependent calls back to back (a decode loop's layer calls),
-    recorded as a HIP graph and replayed (time_graph); `us_stream` is the
+    max(steps, copies) dependent calls back to back (a decode loop's layer
+    calls), recorded as a HIP graph and replayed (time_graph), so one replay
+    walks every copy; `us_stream` is the
     same calls issued one by one from Python between one pair of HIP events;
     `us_single` brackets each call with its own events (launch latency
     included, host gaps excluded)."""
@@ -272,6 +273,9 @@ def bench_skinny(steps, warmup, rows=None):
         ws = [q0] + [D([N, K], "int8") for _ in range(copies - 1)]
         for w in ws[1:]:
             Nn.call("kh_memcpy_d2d", w.ptr, q0.ptr, N * K)
+        # A replayed graph holds at least one call per copy, so every replay
+        # streams all > 512 MB of distinct weights whatever --steps is.
+        gsteps = max(steps, copies)
         bias = D.from_host(np.zeros(N, np.float32))
         for M in (1, 8, 32):
             if (M, K, N) not in want:
@@ -301,7 +305,7 @@ def bench_skinny(steps, warmup, rows=None):
             e1.record()
             Nn.synchronize()
             us_stream = e0.elapsed_ms(e1) / steps * 1e3
-            us = time_graph(call, steps)
+            us = time_graph(call, gsteps)
             evs = [(Nn.Event(), Nn.Event()) for _ in range(steps)]
             for a, b in evs:
                 a.record()
@@ -334,7 +338,7 @@ def bench_skinny(steps, warmup, rows=None):
             i_read[0] += 1
 
         warm_up(read, max(3, warmup), tag=f"c5_read_N{N}")
-        read_us = time_graph(read, steps)
+        read_us = time_graph(read, gsteps)
         read_gbs = N * K / (read_us * 1e-6) / 1e9
         for r in out_rows:
             if r["K"] == K and r["N"] == N:

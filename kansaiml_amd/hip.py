@@ -31,16 +31,40 @@ def _opt(t):
     return t.ptr if t is not None else None
 
 
+def _rows(t: DeviceTensor, dtype: str, what: str):
+    """An activation of rank >= 2 read as the 2-D matrix it is in memory:
+    (rows, cols, leading shape), rows = the product of every axis but the
+    last.  The reference's batched matmul with a rank-2 right operand
+    (core/src/Tensor.cpp:364-441) reads that one matrix for every batch
+    index, which is the 2-D GEMM of these rows; a per-token quantize or a
+    LayerNorm is per row either way."""
+    _need(t, dtype, None, what)
+    if len(t.shape) < 2:
+        raise RuntimeError(f"{what}: expected a tensor of rank >= 2, got shape {t.shape}")
+    lead = list(t.shape[:-1])
+    rows = 1
+    for d in lead:
+        rows *= d
+    return rows, t.shape[-1], lead
+
+
+def _need_residual(residual: DeviceTensor, lead: list, n: int, what: str):
+    _need(residual, "float32", None, f"{what}(residual)")
+    if list(residual.shape) != lead + [n]:
+        raise RuntimeError(f"{what}: residual must be {lead + [n]}, got {residual.shape}")
+
+
 def _need_ln_params(x: DeviceTensor, w: DeviceTensor, b: DeviceTensor, what: str):
-    """LayerNorm operands: x [rows, D] fp32 and weight, bias fp32 [D].  The C
-    ABI cannot see buffer sizes, so a short weight or bias would be read out
-    of bounds on the device: refuse it here."""
-    _need(x, "float32", 2, f"{what}(x)")
+    """LayerNorm operands: x [..., D] fp32 (rows = every leading axis) and
+    weight, bias fp32 [D].  The C ABI cannot see buffer sizes, so a short
+    weight or bias would be read out of bounds on the device: refuse it
+    here.  Returns (rows, D)."""
+    rows, D, _ = _rows(x, "float32", f"{what}(x)")
     _need(w, "float32", 1, f"{what}(weight)")
     _need(b, "float32", 1, f"{what}(bias)")
-    D = x.shape[1]
     if w.shape[0] != D or b.shape[0] != D:
         raise RuntimeError(f"{what}: weight and bias must have {D} entries, got {w.shape} and {b.shape}")
+    return rows, D
 
 
 # ---------------------------------------------------------------------------
@@ -57,9 +81,9 @@ def quantize_tensor(x: DeviceTensor):
 
 
 def quantize_rows(x: DeviceTensor):
-    """Per-row (per-token) symmetric int8 of a 2-D tensor: (codes, scales[rows])."""
-    _need(x, "float32", 2, "quantize_rows")
-    rows, cols = x.shape
+    """Per-row (per-token) symmetric int8 of a tensor of rank >= 2, a row
+    being the last axis: (codes like x, scales [rows])."""
+    rows, cols, _ = _rows(x, "float32", "quantize_rows")
     q = DeviceTensor(x.shape, "int8")
     s = DeviceTensor([rows], "float64")
     N.call("kh_quantize_rows", x.ptr, rows, cols, q.ptr, s.ptr)
@@ -95,9 +119,8 @@ def dequantize_tensor(q: DeviceTensor, scale: DeviceTensor) -> DeviceTensor:
 
 
 def dequantize_rows(q: DeviceTensor, scales: DeviceTensor) -> DeviceTensor:
-    _need(q, "int8", 2, "dequantize_rows")
+    rows, cols, _ = _rows(q, "int8", "dequantize_rows")
     _need(scales, "float64", 1, "dequantize_rows(scales)")
-    rows, cols = q.shape
     if scales.shape[0] != rows:
         raise RuntimeError("dequantize_rows: one scale per row required")
     out = DeviceTensor(q.shape, "float32")
@@ -133,11 +156,11 @@ def _scale_mode(s: DeviceTensor, count: int, what: str) -> int:
 def gemm_i8(a: DeviceTensor, b_packed: DeviceTensor, sa: DeviceTensor | None = None,
             sb: DeviceTensor | None = None, bias: DeviceTensor | None = None, *,
             want_out: bool = True, want_acc: bool = False):
-    """a [M, K] int8, b_packed [N, K] int8 -> out fp32 [M, N] (fused
-    dequantize + bias) and/or acc int32 [M, N].  Returns (out, acc)."""
-    _need(a, "int8", 2, "gemm_i8(a)")
+    """a [..., M, K] int8 (every leading axis folded into the rows),
+    b_packed [N, K] int8 -> out fp32 [..., M, N] (fused dequantize + bias)
+    and/or acc int32 [..., M, N].  Returns (out, acc)."""
+    M, K, lead = _rows(a, "int8", "gemm_i8(a)")
     _need(b_packed, "int8", 2, "gemm_i8(b)")
-    M, K = a.shape
     Nn, K2 = b_packed.shape
     if K != K2:
         raise RuntimeError(f"gemm_i8: incompatible shapes {a.shape} x {b_packed.shape}^T")
@@ -149,8 +172,8 @@ def gemm_i8(a: DeviceTensor, b_packed: DeviceTensor, sa: DeviceTensor | None = N
         _need(bias, "float32", 1, "gemm_i8(bias)")
         if bias.shape[0] != Nn:
             raise RuntimeError("gemm_i8: bias must have N entries")
-    out = DeviceTensor([M, Nn], "float32") if want_out else None
-    acc = DeviceTensor([M, Nn], "int32") if want_acc else None
+    out = DeviceTensor(lead + [Nn], "float32") if want_out else None
+    acc = DeviceTensor(lead + [Nn], "int32") if want_acc else None
     N.call("kh_gemm_i8", a.ptr, b_packed.ptr, M, Nn, K, _opt(sa) if want_out else None, sa_mode,
            _opt(sb) if want_out else None, sb_mode, _opt(bias), _opt(out), _opt(acc))
     return out, acc
@@ -158,23 +181,22 @@ def gemm_i8(a: DeviceTensor, b_packed: DeviceTensor, sa: DeviceTensor | None = N
 
 def dequantize_acc(acc: DeviceTensor, sa: DeviceTensor, sb: DeviceTensor,
                    bias: DeviceTensor | None = None) -> DeviceTensor:
-    _need(acc, "int32", 2, "dequantize_acc")
-    M, Nn = acc.shape
+    M, Nn, _ = _rows(acc, "int32", "dequantize_acc")
     sa_mode = _scale_mode(sa, M, "dequantize_acc(sa)")
     sb_mode = _scale_mode(sb, Nn, "dequantize_acc(sb)")
-    out = DeviceTensor([M, Nn], "float32")
+    out = DeviceTensor(acc.shape, "float32")
     N.call("kh_dequantize_acc", acc.ptr, M, Nn, sa.ptr, sa_mode, sb.ptr, sb_mode, _opt(bias), out.ptr)
     return out
 
 
 def linear_i8(x: DeviceTensor, b_packed: DeviceTensor, sb: DeviceTensor,
               bias: DeviceTensor | None = None, return_codes: bool = False):
-    """Per-token dynamic quantize of x [M, K] fp32, then the int8 GEMM with
-    the fused epilogue.  With return_codes, also returns the activation codes
-    (int8 [M, K]) and per-token scales (float64 [M]) the call produced."""
-    _need(x, "float32", 2, "linear_i8(x)")
+    """Per-token dynamic quantize of x [..., K] fp32 (M = every leading axis),
+    then the int8 GEMM with the fused epilogue: out [..., N].  With
+    return_codes, also returns the activation codes (int8, x's shape) and
+    per-token scales (float64 [M]) the call produced."""
+    M, K, lead = _rows(x, "float32", "linear_i8(x)")
     _need(b_packed, "int8", 2, "linear_i8(w)")
-    M, K = x.shape
     Nn, K2 = b_packed.shape
     if K != K2:
         raise RuntimeError(f"linear_i8: incompatible shapes {x.shape} x {b_packed.shape}^T")
@@ -183,9 +205,9 @@ def linear_i8(x: DeviceTensor, b_packed: DeviceTensor, sb: DeviceTensor,
         _need(bias, "float32", 1, "linear_i8(bias)")
         if bias.shape[0] != Nn:
             raise RuntimeError("linear_i8: bias must have N entries")
-    q = DeviceTensor([M, K], "int8")
+    q = DeviceTensor(x.shape, "int8")
     sx = DeviceTensor([M], "float64")
-    out = DeviceTensor([M, Nn], "float32")
+    out = DeviceTensor(lead + [Nn], "float32")
     N.call("kh_linear_i8", x.ptr, M, K, b_packed.ptr, Nn, sb.ptr, sb_mode, _opt(bias), q.ptr, sx.ptr, out.ptr)
     return (out, q, sx) if return_codes else out
 
@@ -194,11 +216,11 @@ def linear_i8_tensor(x: DeviceTensor, b_packed: DeviceTensor, sb: DeviceTensor,
                      bias: DeviceTensor | None = None, return_codes: bool = False):
     """Per-tensor dynamic quantize of x [M, K] fp32 (one scale), then the int8
     GEMM with the fused epilogue: QLinear(mode="int8",
-    act_granularity="tensor").  With return_codes, also returns the codes
-    (int8 [M, K]) and the scale (float64 [1])."""
-    _need(x, "float32", 2, "linear_i8_tensor(x)")
+    act_granularity="tensor").  x [..., K] gives out [..., N].  With
+    return_codes, also returns the codes (int8, x's shape) and the scale
+    (float64 [1])."""
+    M, K, lead = _rows(x, "float32", "linear_i8_tensor(x)")
     _need(b_packed, "int8", 2, "linear_i8_tensor(w)")
-    M, K = x.shape
     Nn, K2 = b_packed.shape
     if K != K2:
         raise RuntimeError(f"linear_i8_tensor: incompatible shapes {x.shape} x {b_packed.shape}^T")
@@ -207,9 +229,9 @@ def linear_i8_tensor(x: DeviceTensor, b_packed: DeviceTensor, sb: DeviceTensor,
         _need(bias, "float32", 1, "linear_i8_tensor(bias)")
         if bias.shape[0] != Nn:
             raise RuntimeError("linear_i8_tensor: bias must have N entries")
-    q = DeviceTensor([M, K], "int8")
+    q = DeviceTensor(x.shape, "int8")
     sx = DeviceTensor([1], "float64")
-    out = DeviceTensor([M, Nn], "float32")
+    out = DeviceTensor(lead + [Nn], "float32")
     N.call("kh_linear_i8_tensor", x.ptr, M, K, b_packed.ptr, Nn, sb.ptr, sb_mode, _opt(bias), q.ptr, sx.ptr, out.ptr)
     return (out, q, sx) if return_codes else out
 
@@ -219,19 +241,24 @@ def linear_i8_tensor(x: DeviceTensor, b_packed: DeviceTensor, sb: DeviceTensor,
 # ---------------------------------------------------------------------------
 
 def matmul(a: DeviceTensor, b: DeviceTensor, bias: DeviceTensor | None = None) -> DeviceTensor:
-    """kan::metal_matmul's contract (core/src/MetalOps.cpp:10-17): 2-D,
-    a.shape[1] == b.shape[0], else RuntimeError("incompatible shapes")."""
-    _need(a, "float32", 2, "matmul(a)")
-    _need(b, "float32", 2, "matmul(b)")
-    if a.shape[1] != b.shape[0]:
+    """kan::metal_matmul's contract (core/src/MetalOps.cpp:10-17) --
+    a.shape[-1] == b.shape[0], else RuntimeError("incompatible shapes") --
+    with a of any rank >= 2 against a 2-D b: Tensor::matmul's batched path
+    with a shared right operand (core/src/Tensor.cpp:364-441), out
+    [..., M, N].  A batched right operand has no HIP kernel here."""
+    M, K, lead = _rows(a, "float32", "matmul(a)")
+    _need(b, "float32", None, "matmul(b)")
+    if len(b.shape) != 2:
+        raise NotImplementedError(f"matmul: a batched right operand {b.shape} has no HIP kernel (the int8 path's "
+                                  "weights are 2-D)")
+    if K != b.shape[0]:
         raise RuntimeError("matmul: incompatible shapes")
-    M, K = a.shape
     Nn = b.shape[1]
     if bias is not None:
         _need(bias, "float32", 1, "matmul(bias)")
         if bias.shape[0] != Nn:
             raise RuntimeError("matmul: bias must have N entries")
-    out = DeviceTensor([M, Nn], "float32")
+    out = DeviceTensor(lead + [Nn], "float32")
     N.call("kh_matmul_f32", a.ptr, b.ptr, out.ptr, M, K, Nn, _opt(bias))
     return out
 
@@ -247,12 +274,14 @@ def add(a: DeviceTensor, b: DeviceTensor) -> DeviceTensor:
 
 
 def add_bias(x: DeviceTensor, bias: DeviceTensor, relu: bool = False) -> DeviceTensor:
-    _need(x, "float32", 2, "add_bias")
+    """x [..., F] + bias [F] (Tensor.cpp:158-166, the bias broadcast over
+    every leading axis), optionally followed by relu."""
+    rows, F, _ = _rows(x, "float32", "add_bias")
     _need(bias, "float32", 1, "add_bias(bias)")
-    if bias.shape[0] != x.shape[1]:
+    if bias.shape[0] != F:
         raise RuntimeError("add_bias: bias must have features entries")
     out = DeviceTensor(x.shape, "float32")
-    N.call("kh_add_bias", x.ptr, bias.ptr, out.ptr, x.shape[0], x.shape[1], 1 if relu else 0)
+    N.call("kh_add_bias", x.ptr, bias.ptr, out.ptr, rows, F, 1 if relu else 0)
     return out
 
 
@@ -294,10 +323,10 @@ def gemm_i8_fused(a: DeviceTensor, b_packed: DeviceTensor, sa: DeviceTensor, sb:
                   residual: DeviceTensor | None = None, absmax: bool = False):
     """gemm_i8's fp32 output with the following elementwise steps fused into
     its epilogue (bias, then act, then residual + y) and optionally the
-    absmax partials of the result.  Returns (out, AbsmaxParts | None)."""
-    _need(a, "int8", 2, "gemm_i8(a)")
+    absmax partials of the result.  a [..., M, K] gives out [..., M, N].
+    Returns (out, AbsmaxParts | None)."""
+    M, K, lead = _rows(a, "int8", "gemm_i8(a)")
     _need(b_packed, "int8", 2, "gemm_i8(b)")
-    M, K = a.shape
     Nn, K2 = b_packed.shape
     if K != K2:
         raise RuntimeError(f"gemm_i8: incompatible shapes {a.shape} x {b_packed.shape}^T")
@@ -310,10 +339,8 @@ def gemm_i8_fused(a: DeviceTensor, b_packed: DeviceTensor, sa: DeviceTensor, sb:
         if bias.shape[0] != Nn:
             raise RuntimeError("gemm_i8: bias must have N entries")
     if residual is not None:
-        _need(residual, "float32", 2, "gemm_i8(residual)")
-        if list(residual.shape) != [M, Nn]:
-            raise RuntimeError("gemm_i8_fused: residual must be [M, N]")
-    out = DeviceTensor([M, Nn], "float32")
+        _need_residual(residual, lead, Nn, "gemm_i8_fused")
+    out = DeviceTensor(lead + [Nn], "float32")
     parts = AbsmaxParts() if absmax else None
     N.call("kh_gemm_i8_ex", a.ptr, b_packed.ptr, M, Nn, K, sa.ptr, sa_mode, sb.ptr, sb_mode, _opt(bias), ACTS[act],
            _opt(residual), out.ptr, parts.buf.ptr if parts else None, ABSMAX_PARTS if parts else 0,
@@ -325,10 +352,9 @@ def gemm_i8_quant(a: DeviceTensor, b_packed: DeviceTensor, sa: DeviceTensor, sb:
                   bias: DeviceTensor | None = None, *, act: str | None = None,
                   residual: DeviceTensor | None = None):
     """quantize_tensor(gemm_i8_fused(...)) without writing the fp32 result:
-    returns (codes int8 [M, N], scale float64 [1])."""
-    _need(a, "int8", 2, "gemm_i8(a)")
+    returns (codes int8 [..., M, N], scale float64 [1])."""
+    M, K, lead = _rows(a, "int8", "gemm_i8(a)")
     _need(b_packed, "int8", 2, "gemm_i8(b)")
-    M, K = a.shape
     Nn, K2 = b_packed.shape
     if K != K2:
         raise RuntimeError(f"gemm_i8: incompatible shapes {a.shape} x {b_packed.shape}^T")
@@ -341,10 +367,8 @@ def gemm_i8_quant(a: DeviceTensor, b_packed: DeviceTensor, sa: DeviceTensor, sb:
         if bias.shape[0] != Nn:
             raise RuntimeError("gemm_i8: bias must have N entries")
     if residual is not None:
-        _need(residual, "float32", 2, "gemm_i8(residual)")
-        if list(residual.shape) != [M, Nn]:
-            raise RuntimeError("gemm_i8_quant: residual must be [M, N]")
-    q = DeviceTensor([M, Nn], "int8")
+        _need_residual(residual, lead, Nn, "gemm_i8_quant")
+    q = DeviceTensor(lead + [Nn], "int8")
     s = DeviceTensor([1], "float64")
     N.call("kh_gemm_i8_quant", a.ptr, b_packed.ptr, M, Nn, K, sa.ptr, sa_mode, sb.ptr, sb_mode, _opt(bias),
            ACTS[act], _opt(residual), q.ptr, s.ptr)
@@ -355,14 +379,13 @@ def gemm_i8_qload(x: DeviceTensor, parts: AbsmaxParts, b_packed: DeviceTensor, s
                   bias: DeviceTensor | None = None, *, act: str | None = None,
                   residual: DeviceTensor | None = None, absmax: bool = False, want_scale: bool = False):
     """gemm_i8_fused(quantize_tensor_parts(x, parts)) without writing the
-    activation's codes: x fp32 [M, K] with the absmax partials its producer
-    wrote.  Returns (out, AbsmaxParts | None), plus the activation's scale
-    (float64 [1]) when want_scale."""
-    _need(x, "float32", 2, "gemm_i8_qload(x)")
+    activation's codes: x fp32 [..., M, K] with the absmax partials its
+    producer wrote.  Returns (out, AbsmaxParts | None), plus the
+    activation's scale (float64 [1]) when want_scale."""
+    M, K, lead = _rows(x, "float32", "gemm_i8_qload(x)")
     _need(b_packed, "int8", 2, "gemm_i8_qload(b)")
     if parts is None or parts.count <= 0:
         raise RuntimeError("gemm_i8_qload: the producer wrote no partials")
-    M, K = x.shape
     Nn, K2 = b_packed.shape
     if K != K2:
         raise RuntimeError(f"gemm_i8_qload: incompatible shapes {x.shape} x {b_packed.shape}^T")
@@ -374,10 +397,8 @@ def gemm_i8_qload(x: DeviceTensor, parts: AbsmaxParts, b_packed: DeviceTensor, s
         if bias.shape[0] != Nn:
             raise RuntimeError("gemm_i8_qload: bias must have N entries")
     if residual is not None:
-        _need(residual, "float32", 2, "gemm_i8_qload(residual)")
-        if list(residual.shape) != [M, Nn]:
-            raise RuntimeError("gemm_i8_qload: residual must be [M, N]")
-    out = DeviceTensor([M, Nn], "float32")
+        _need_residual(residual, lead, Nn, "gemm_i8_qload")
+    out = DeviceTensor(lead + [Nn], "float32")
     scale = DeviceTensor([1], "float64") if want_scale else None
     out_parts = AbsmaxParts() if absmax else None
     N.call("kh_gemm_i8_qload", x.ptr, M, Nn, K, parts.buf.ptr, parts.count, b_packed.ptr, sb.ptr, sb_mode,
@@ -391,20 +412,19 @@ def gemm_i8_qload(x: DeviceTensor, parts: AbsmaxParts, b_packed: DeviceTensor, s
 def layer_norm_quant(x: DeviceTensor, w: DeviceTensor, b: DeviceTensor, eps: float = 1e-5):
     """quantize_tensor(layer_norm(x)) without writing the fp32 output:
     returns (codes int8 like x, scale float64 [1])."""
-    _need_ln_params(x, w, b, "layer_norm_quant")
+    rows, D = _need_ln_params(x, w, b, "layer_norm_quant")
     q = DeviceTensor(x.shape, "int8")
     s = DeviceTensor([1], "float64")
-    N.call("kh_layernorm_quant", x.ptr, x.shape[0], x.shape[1], w.ptr, b.ptr, eps, q.ptr, s.ptr)
+    N.call("kh_layernorm_quant", x.ptr, rows, D, w.ptr, b.ptr, eps, q.ptr, s.ptr)
     return q, s
 
 
 def layer_norm_quant_rows(x: DeviceTensor, w: DeviceTensor, b: DeviceTensor, eps: float = 1e-5):
     """LayerNorm with its output quantized per row in one pass (the fp32
-    values are never stored).  Returns (codes int8 [rows, D], scales float64
+    values are never stored).  Returns (codes int8 like x, scales float64
     [rows])."""
-    _need_ln_params(x, w, b, "layer_norm_quant_rows")
-    rows, D = x.shape
-    q = DeviceTensor([rows, D], "int8")
+    rows, D = _need_ln_params(x, w, b, "layer_norm_quant_rows")
+    q = DeviceTensor(x.shape, "int8")
     s = DeviceTensor([rows], "float64")
     N.call("kh_layernorm_quant_rows", x.ptr, rows, D, w.ptr, b.ptr, eps, q.ptr, s.ptr)
     return q, s
@@ -412,10 +432,10 @@ def layer_norm_quant_rows(x: DeviceTensor, w: DeviceTensor, b: DeviceTensor, eps
 
 def layer_norm(x: DeviceTensor, w: DeviceTensor, b: DeviceTensor, eps: float = 1e-5, *, absmax: bool = False):
     """LayerNorm over the last axis (nn.py:308-331).  Returns (out, AbsmaxParts | None)."""
-    _need_ln_params(x, w, b, "layer_norm")
+    rows, D = _need_ln_params(x, w, b, "layer_norm")
     out = DeviceTensor(x.shape, "float32")
     parts = AbsmaxParts() if absmax else None
-    N.call("kh_layernorm_ex", x.ptr, x.shape[0], x.shape[1], w.ptr, b.ptr, eps, out.ptr,
+    N.call("kh_layernorm_ex", x.ptr, rows, D, w.ptr, b.ptr, eps, out.ptr,
            parts.buf.ptr if parts else None, ABSMAX_PARTS if parts else 0, ctypes.byref(parts._n) if parts else None)
     return out, parts
 

@@ -131,27 +131,34 @@ class TraceValue:
         return self._emit("relu", [self], self.shape)
 
     def matmul(self, other):
+        """Tensor::matmul's shape rules (kir.py:164-181): 2-D x 2-D, or the
+        batched path with the leading axes broadcast.  run_hip runs an
+        operand of any rank >= 2 against a 2-D right operand (a Linear's
+        weight) as the 2-D GEMM of its rows; a batched right operand traces
+        but has no HIP kernel."""
         other = self._coerce(other)
-        if len(self.shape) != 2 or len(other.shape) != 2:
-            raise ValueError(f"matmul: the HIP path traces 2-D operands, got {self.shape} vs {other.shape}")
-        if self.shape[1] != other.shape[0]:
+        if len(self.shape) < 2 or len(other.shape) < 2:
+            raise ValueError(f"matmul: both operands must be at least 2D, got {self.shape} vs {other.shape}")
+        if self.shape[-1] != other.shape[-2]:
             raise ValueError(f"matmul: incompatible shapes {self.shape} vs {other.shape}")
-        return self._emit("matmul", [self, other], [self.shape[0], other.shape[1]])
+        batch = _broadcast(self.shape[:-2], other.shape[:-2], "matmul")
+        return self._emit("matmul", [self, other], batch + [self.shape[-2], other.shape[-1]])
 
     def quantize(self, granularity: str = "tensor"):
         if granularity not in ("tensor", "row"):
             raise ValueError(f"quantize: granularity must be 'tensor' or 'row', got {granularity!r}")
-        if granularity == "row" and len(self.shape) != 2:
-            raise ValueError("quantize: per-row granularity needs a 2-D value")
+        if granularity == "row" and len(self.shape) < 2:
+            raise ValueError("quantize: per-row granularity needs a value of rank >= 2 (a row is the last axis)")
         return self._emit("quantize", [self], self.shape, "int8", granularity=granularity)
 
     def int8_matmul(self, other):
         other = self._coerce(other)
         if self.dtype != "int8" or other.dtype != "int8":
             raise ValueError("int8_matmul: both operands must be quantized (int8)")
-        if len(self.shape) != 2 or len(other.shape) != 2 or self.shape[1] != other.shape[0]:
-            raise ValueError(f"int8_matmul: incompatible shapes {self.shape} vs {other.shape}")
-        return self._emit("int8_matmul", [self, other], [self.shape[0], other.shape[1]], "int32")
+        if len(self.shape) < 2 or len(other.shape) != 2 or self.shape[-1] != other.shape[0]:
+            raise ValueError(f"int8_matmul: incompatible shapes {self.shape} vs {other.shape} (activations of "
+                             "rank >= 2 against a 2-D weight)")
+        return self._emit("int8_matmul", [self, other], self.shape[:-1] + [other.shape[1]], "int32")
 
     def dequantize(self):
         if self.dtype not in ("int8", "int32"):
@@ -171,8 +178,8 @@ class TraceValue:
 
     def layer_norm(self, weight, bias, eps: float = 1e-5):
         weight, bias = self._coerce(weight), self._coerce(bias)
-        if len(self.shape) != 2 or weight.shape != [self.shape[1]] or bias.shape != [self.shape[1]]:
-            raise ValueError("layer_norm: expects [rows, D] with weight and bias of shape [D]")
+        if len(self.shape) < 2 or weight.shape != [self.shape[-1]] or bias.shape != [self.shape[-1]]:
+            raise ValueError("layer_norm: expects [..., D] with weight and bias of shape [D]")
         return self._emit("layer_norm", [self, weight, bias], self.shape, eps=float(eps))
 
     def gelu(self):
@@ -228,7 +235,7 @@ def _users(graph) -> dict:
 
 def _is_bias(graph, by_id, x_id, b_id) -> bool:
     xs, bs = by_id[x_id].shape, by_id[b_id].shape
-    return len(xs) == 2 and len(bs) == 1 and xs[1] == bs[0]
+    return len(xs) >= 2 and len(bs) == 1 and xs[-1] == bs[0]
 
 
 def quant_fusion(graph, producer_quant: bool | str = False, qload: bool = False) -> Graph:
@@ -488,8 +495,8 @@ def _dequantize(v):
 def _add(a, b):
     if list(a.shape) == list(b.shape):
         return H.add(a, b)
-    if len(a.shape) == 2 and len(b.shape) == 1 and a.shape[1] == b.shape[0]:
-        return H.add_bias(a, b)
+    if len(a.shape) >= 2 and len(b.shape) == 1 and a.shape[-1] == b.shape[0]:
+        return H.add_bias(a, b)  # [..., N] + [N]: the bias over every leading axis
     raise NotImplementedError(f"run_hip: add with broadcast {a.shape} + {b.shape} has no HIP kernel")
 
 

@@ -41,8 +41,8 @@ class QTensor:
     """int8 codes + binary64 scales on the device.
 
     granularity: "tensor" (one scale, the reference's only kind), "row" (one
-    per row of a 2-D tensor) or "col" (one per column of an [in, out]
-    weight).  packed: codes stored K-contiguous [out, in] for the GEMM (the
+    per row along the last axis: per token of [batch, seq, d] activations)
+    or "col" (one per column of an [in, out] weight).  packed: codes stored K-contiguous [out, in] for the GEMM (the
     logical shape stays [in, out])."""
 
     __slots__ = ("codes", "scales", "shape", "granularity", "packed", "owned")
@@ -59,13 +59,14 @@ class QTensor:
     # -- construction ------------------------------------------------------
     @staticmethod
     def from_tensor(tensor, granularity: str = "tensor") -> "QTensor":
-        """quantize.py:95-98.  granularity "row" quantizes each row of a 2-D
-        tensor separately."""
+        """quantize.py:95-98.  granularity "row" quantizes each row (the last
+        axis, every leading axis folded into the rows) separately; a 1-D
+        tensor is one row."""
         x = to_device(tensor, "float32")
         if granularity == "tensor":
             q, s = H.quantize_tensor(x)
         elif granularity == "row":
-            q, s = H.quantize_rows(x.reshape(x.shape if len(x.shape) == 2 else [1, x.numel()]))
+            q, s = H.quantize_rows(x if len(x.shape) >= 2 else x.reshape([1, x.numel()]))
         else:
             raise ValueError(f"from_tensor: granularity must be 'tensor' or 'row', got {granularity!r}")
         N.synchronize()  # NaN/inf -> ValueError here, as in the reference

@@ -224,6 +224,10 @@ def ref():
         R.kref_matmul.restype = None
         R.kref_add_bias_broadcast.argtypes = [vp, vp, vp, i64, i64]
         R.kref_add_bias_broadcast.restype = None
+        R.kref_batched_matmul_shared.argtypes = [vp, vp, vp, i64, i64, i64, i64]
+        R.kref_batched_matmul_shared.restype = None
+        R.kref_add_broadcast_rank3.argtypes = [vp, vp, vp, i64, i64, i64]
+        R.kref_add_broadcast_rank3.restype = None
         _ref = R
     return _ref
 
@@ -243,6 +247,29 @@ def ref_add_bias(x, bias):
     x, bias = _f32c(x), _f32c(bias)
     out = np.empty(x.shape, np.float32)
     ref().kref_add_bias_broadcast(_ptr(x), _ptr(bias), _ptr(out), x.shape[0], x.shape[1])
+    return out
+
+
+def ref_batched_matmul(a, b):
+    """kan::cpu::batched_matmul (backend/cpu/src/Ops.cpp:427-437) as
+    Tensor::matmul's batched path calls it for a [batch, M, K] left operand
+    and a shared 2-D right operand (core/src/Tensor.cpp:364-393)."""
+    a, b = _f32c(a), _f32c(b)
+    B, M, K = a.shape
+    _, N = b.shape
+    out = np.empty((B, M, N), np.float32)
+    ref().kref_batched_matmul_shared(_ptr(a), _ptr(b), _ptr(out), B, M, K, N)
+    return out
+
+
+def ref_add_broadcast(x, bias):
+    """kan::cpu::add_broadcast (backend/cpu/src/Ops.cpp:121-125) for
+    [batch, M, N] + [N], the general path Tensor::add takes for a rank-3
+    activation plus a bias (core/src/Tensor.cpp:158-166)."""
+    x, bias = _f32c(x), _f32c(bias)
+    B, M, N = x.shape
+    out = np.empty(x.shape, np.float32)
+    ref().kref_add_broadcast_rank3(_ptr(x), _ptr(bias), _ptr(out), B, M, N)
     return out
 
 

@@ -121,6 +121,60 @@ def test_weight_only_qlinear_matches_reference_semantics(K):
     np.testing.assert_array_equal(bits32(kir.run_hip(g, x)), bits32(y))
 
 
+@pytest.mark.parametrize("act,wg", [("row", "col"), ("tensor", "col"), ("tensor", "tensor")])
+def test_qlinear_int8_rank3_activations(K, act, wg):
+    """A [batch, seq, d] = [4, 64, 384] activation (the reference applies its
+    Linears to such tensors, nn.py:80-81, 412-414) through QLinear(mode="int8"),
+    eager, traced, traced and fused, and planned: output [4, 64, N],
+    bit-exact against the oracle's int8 Linear of the flattened [256, 384]
+    rows (per-token scales are per row of the last axis)."""
+    kir, Q, N = K
+    gen = np.random.Generator(np.random.PCG64(31))
+    x = gen.standard_normal((4, 64, 384), dtype=np.float32)
+    w = gen.standard_normal((384, 1152), dtype=np.float32) * np.float32(0.02)
+    b = gen.standard_normal(1152).astype(np.float32)
+    layer = Q.QLinear(Linear(w, b), mode="int8", act_granularity=act, weight_granularity=wg)
+    ey = O.int8_linear(x.reshape(256, 384), w, b, x_gran=act, w_gran=wg)[0].reshape(4, 64, 1152)
+    y = layer(x).numpy()
+    assert y.shape == (4, 64, 1152)
+    np.testing.assert_array_equal(bits32(y), bits32(ey))
+    g = kir.trace(layer, x)
+    assert g.nodes[g.output].shape == [4, 64, 1152]
+    np.testing.assert_array_equal(bits32(kir.run_hip(g, x)), bits32(ey))
+    f = kir.quant_fusion(g)
+    assert [n.op for n in f.nodes if n.op == "int8_linear"] == ["int8_linear"]
+    np.testing.assert_array_equal(bits32(kir.run_hip(f, x)), bits32(ey))
+    plan = kir.plan_memory(f)
+    np.testing.assert_array_equal(bits32(kir.run_hip_planned(f, plan, None, x)), bits32(ey))
+
+
+def test_qlinear_weight_only_rank3_matches_reference_build(K):
+    """quantize.py:115-122 on a [4, 64, 384] activation: x.matmul(dequantize(W))
+    .add(bias) through the reference's batched path (Tensor.cpp:364-393) and
+    general broadcast add (Tensor.cpp:158-166), compiled from its Ops.cpp,
+    against the HIP path eager and traced: within the fp32 matmul's rounding
+    bound, and the rank-3 call bit-identical to the same rows as a 2-D call."""
+    kir, Q, N = K
+    gen = np.random.Generator(np.random.PCG64(32))
+    x = gen.standard_normal((4, 64, 384), dtype=np.float32)
+    w = gen.standard_normal((384, 384), dtype=np.float32) * np.float32(0.02)
+    b = gen.standard_normal(384).astype(np.float32)
+    layer = Q.QLinear(Linear(w, b))
+    y = layer(x).numpy()
+    assert y.shape == (4, 64, 384)
+    np.testing.assert_array_equal(bits32(y), bits32(layer(x.reshape(256, 384)).numpy().reshape(4, 64, 384)))
+    f = kir.quant_fusion(kir.trace(layer, x))
+    np.testing.assert_array_equal(bits32(kir.run_hip(f, x)), bits32(y))
+    qw, sw = O.ko_quantize_tensor(w)
+    wdeq = O.ko_dequantize_tensor(qw, sw)
+    if O.ref_available():
+        ref = O.ref_add_broadcast(O.ref_batched_matmul(x, wdeq), b)
+    else:
+        ref = O.ko_add_bias(O.ko_matmul_f32(x.reshape(256, 384), wdeq), b).reshape(4, 64, 384)
+    bound = 2 * 384 * np.finfo(np.float32).eps * (np.abs(x) @ np.abs(wdeq) + np.abs(b))
+    assert (np.abs(y - ref) <= bound).all()
+
+
 def test_planned_equals_unplanned_and_pool_converges(K):
     kir, Q, N = K
     gen = np.random.Generator(np.random.PCG64(7))

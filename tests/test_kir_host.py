@@ -66,6 +66,41 @@ def test_trace_shape_errors():
         kir.trace(lambda x: x.quantize("col"), np.zeros((4, 4), np.float32))
 
 
+def test_trace_rank3_activations():
+    """[batch, seq, d] activations (nn.py:80-81, 412-414): Tensor::matmul's
+    batched shapes (kir.py:164-181), the per-token quantize over the last
+    axis, [B, T, N] + [N] as a bias, and the int8 chain still fusing into one
+    int8_linear of the rank-3 shape."""
+    bias = np.zeros(8, np.float32)
+    w = np.zeros((16, 8), np.float32)
+    x3 = np.zeros((2, 5, 16), np.float32)
+
+    g = kir.trace(lambda x: x.matmul(w).add(bias), x3)
+    assert [n.shape for n in g.nodes if n.op in ("matmul", "add")] == [[2, 5, 8], [2, 5, 8]]
+    f = kir.quant_fusion(g)
+    assert [n.op for n in f.nodes if n.op not in ("placeholder", "constant")] == ["matmul_bias"]
+
+    for gran in ("tensor", "row"):
+        g = kir.trace(lambda x, wq: _linear_int8(x, wq.quantize("tensor"), bias, gran), x3, w)
+        mm = [n for n in g.nodes if n.op == "int8_matmul"][0]
+        assert mm.shape == [2, 5, 8] and mm.dtype == "int32"
+        f = kir.quant_fusion(g)
+        lin = [n for n in f.nodes if n.op == "int8_linear"]
+        assert len(lin) == 1 and lin[0].shape == [2, 5, 8] and lin[0].attrs["bias"] and f.output == lin[0].id
+
+    # batched right operands trace with the reference's broadcast shapes
+    g = kir.trace(lambda a, b: a.matmul(b), np.zeros((3, 1, 4, 6), np.float32), np.zeros((5, 6, 7), np.float32))
+    assert g.nodes[-1].shape == [3, 5, 4, 7]
+    g = kir.trace(lambda x: x.layer_norm(np.ones(16, np.float32), np.zeros(16, np.float32)), x3)
+    assert g.nodes[-1].shape == [2, 5, 16]
+    with pytest.raises(ValueError):
+        kir.trace(lambda x: x.matmul(np.zeros((15, 8), np.float32)), x3)
+    with pytest.raises(ValueError):
+        kir.trace(lambda x: x.matmul(np.zeros((8,), np.float32)), x3)
+    with pytest.raises(ValueError):  # the int8 weight must be 2-D
+        kir.trace(lambda x, wq: x.quantize().int8_matmul(wq.quantize()), x3, np.zeros((2, 16, 8), np.float32))
+
+
 def test_plan_memory_chain_reuses_slots():
     """A 6-deep chain of computed nodes: each op's input dies at that op, so
     (as in the reference's planner, which releases inputs after the op runs)

@@ -217,6 +217,27 @@ def test_matmul_f32_equals_reference_build(shape):
     assert (np.abs(mine - ref64) <= tol + 1e-30).all()
 
 
+@pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built")
+def test_reference_batched_matmul_is_the_2d_matmul_of_its_rows():
+    """The reference's batched matmul with a shared 2-D right operand
+    (Tensor.cpp:364-393 -> Ops.cpp:427-437) and its general broadcast add of
+    a bias (Ops.cpp:121-125) equal, bit for bit, the 2-D matmul and bias add
+    of the flattened [batch * M, K] rows: what the HIP path computes for a
+    [batch, seq, d] activation."""
+    gen = np.random.Generator(np.random.PCG64(21))
+    a = gen.standard_normal((4, 16, 96)).astype(np.float32)
+    b = gen.standard_normal((96, 40)).astype(np.float32)
+    bias = gen.standard_normal(40).astype(np.float32)
+    batched = O.ref_batched_matmul(a, b)
+    flat = O.ref_matmul(a.reshape(-1, 96), b).reshape(4, 16, 40)
+    np.testing.assert_array_equal(batched.view(np.uint32), flat.view(np.uint32))
+    np.testing.assert_array_equal(O.ref_add_broadcast(batched, bias).view(np.uint32),
+                                  O.ref_add_bias(flat.reshape(-1, 40), bias).reshape(4, 16, 40).view(np.uint32))
+    # the shim passes the batch axis through: a batch of distinct matrices
+    # is not the first matrix repeated
+    assert not np.array_equal(batched[1], batched[0])
+
+
 # ---------------------------------------------------------------------------
 # Mutation checks: a plausible mistake planted in a copy of the oracle must
 # fail the fixtures above.
