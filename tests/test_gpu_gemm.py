@@ -198,6 +198,82 @@ def test_c5_linear_i8_special_rows(hip, M, K, N):
     np.testing.assert_array_equal(bits32(out), bits32(expect))
 
 
+def _linear_i8_raw(Nn, D, xd, qwd, swd, biasd, M, K, N):
+    """kh_linear_i8 through the C ABI into fresh outputs: (out, codes, scales)."""
+    q = D.empty([M, K], "int8")
+    sx = D.empty([M], "float64")
+    out = D.empty([M, N], "float32")
+    Nn.call("kh_linear_i8", xd.ptr, M, K, qwd.ptr, N, swd.ptr, 1, biasd.ptr, q.ptr, sx.ptr, out.ptr)
+    return out, q, sx
+
+
+def test_c5_decode_calls_back_to_back(hip):
+    """Consecutive kh_linear_i8 calls with new activations, different M and
+    both (K, N), queued before any is checked: each call's codes, scales and
+    outputs equal the oracle's (no call reads another's codes)."""
+    from kansaiml_amd import _native as Nn
+    H, D = hip
+    gen = np.random.Generator(np.random.PCG64(77))
+    plan = [(8, 4096, 4096), (8, 4096, 4096), (32, 4096, 4096), (4, 2048, 2048), (17, 4096, 11008),
+            (32, 4096, 11008), (8, 4096, 4096)]
+    calls = []
+    for M, K, N in plan:
+        w = gen.integers(-127, 128, (N, K), dtype=np.int8)
+        sw = gen.uniform(1e-4, 1e-3, N)
+        bias = gen.standard_normal(N).astype(np.float32)
+        x = _c5_activations(gen, M, K)
+        wd, swd, bd, xd = D.from_host(w), D.from_host(sw), D.from_host(bias), D.from_host(x)
+        calls.append((x, w, sw, bias, M, K, N) + _linear_i8_raw(Nn, D, xd, wd, swd, bd, M, K, N))
+    for x, w, sw, bias, M, K, N, out, q, sx in calls:
+        print(f"back-to-back M={M} K={K} N={N}", flush=True)
+        eq, es = O.ko_quantize_rows(x)
+        np.testing.assert_array_equal(q.numpy(), eq)
+        np.testing.assert_array_equal(sx.numpy().view(np.uint64), es.view(np.uint64))
+        np.testing.assert_array_equal(bits32(out.numpy()), bits32(O.ko_epilogue(O.ko_gemm_i8(eq, w), es, sw, bias)))
+
+
+def test_c5_decode_graph_replays(hip):
+    """kh_linear_i8 (per-row quantize + skinny GEMM at M = 8) recorded as a
+    HIP graph and replayed with new activations copied in between, and eager
+    calls between replays: every replay's codes and outputs equal the
+    oracle's for the activations it found."""
+    import ctypes
+    from kansaiml_amd import _native as Nn
+    H, D = hip
+    gen = np.random.Generator(np.random.PCG64(78))
+    M, K, N = 8, 4096, 4096
+    w = gen.integers(-127, 128, (N, K), dtype=np.int8)
+    sw = gen.uniform(1e-4, 1e-3, N)
+    bias = gen.standard_normal(N).astype(np.float32)
+    wd, swd, bd = D.from_host(w), D.from_host(sw), D.from_host(bias)
+    xd = D.empty([M, K], "float32")
+    q, sx, out = D.empty([M, K], "int8"), D.empty([M], "float64"), D.empty([M, N], "float32")
+    args = (xd.ptr, M, K, wd.ptr, N, swd.ptr, 1, bd.ptr, q.ptr, sx.ptr, out.ptr)
+    xd.copy_from(gen.standard_normal((M, K), dtype=np.float32))
+    Nn.call("kh_linear_i8", *args)
+    Nn.synchronize()
+    Nn.call("kh_graph_capture_begin")
+    try:
+        Nn.call("kh_linear_i8", *args)
+    except BaseException:
+        Nn.lib().kh_graph_capture_end(None)
+        raise
+    g = ctypes.c_void_p()
+    Nn.call("kh_graph_capture_end", ctypes.byref(g))
+    try:
+        for r in range(4):
+            x = _c5_activations(gen, M, K) * np.float32(r + 1)
+            xd.copy_from(x)
+            Nn.call("kh_graph_launch", g)
+            if r == 2:  # an eager call between replays
+                _linear_i8_raw(Nn, D, xd, wd, swd, bd, M, K, N)
+            eq, es = O.ko_quantize_rows(x)
+            np.testing.assert_array_equal(bits32(out.numpy()), bits32(O.ko_epilogue(O.ko_gemm_i8(eq, w), es, sw, bias)))
+            np.testing.assert_array_equal(q.numpy(), eq)
+    finally:
+        Nn.call("kh_graph_destroy", g)
+
+
 def test_linear_i8_per_token(hip):
     """kh_linear_i8: per-token quantize fused ahead of the GEMM (config C5)."""
     H, D = hip
