@@ -1090,6 +1090,152 @@ int launch_skinny(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, in
     return kh::launch_status("gemm_i8_skinny");
 }
 
+// ---------------------------------------------------------------------------
+// Narrow-N GEMM: many rows, at most 128 output columns (C4's vocabulary head,
+// M = 16384, N = 65, K = 384).  A 128 x 128 ping-pong tile there computes 128
+// columns for 65 and gives the chip one tile per 128 rows (128 workgroups on
+// 256 CUs).  Here a workgroup owns 64 rows and every column: the whole packed
+// weight (N rows of K bytes, zero rows up to 16 NT) goes into LDS once; each
+// 16-row group of A has two waves, each multiplying the group's
+// v_mfma_i32_16x16x64_i8 A fragments (loaded straight from memory, all of
+// them before the weight is staged) with half of the NT 16-column B
+// fragments read from LDS, then applying the epilogue of the other kernels
+// (epilogue_finish: the same binary64 dequantize, bias, activation and
+// residual).  Bound: the A and output bytes, M K + 4 M N (C4's head: 8.47 ->
+// 7.36 us against the 128 x 128 ping-pong tiles, graph-replayed).  LDS rows
+// are K + 16 bytes apart, so the 16 rows of a fragment read fall on distinct
+// banks.  Non-temporal output stores measured slower (7.93 us).
+// ---------------------------------------------------------------------------
+constexpr int kNarrowRows = 64;
+constexpr int kNarrowMaxK = 512;
+// Two waves per 16-row group, each with half of the column tiles: 8 waves
+// per workgroup (7.36 us for the C4 head against 7.93 with one wave per
+// group and all of its tiles).
+constexpr int kNarrowWN = 2;
+
+template <int NT, bool FUSED>
+__global__ __launch_bounds__(256 * kNarrowWN) void gemm_i8_narrow_kernel(const int8_t* __restrict__ A,
+                                                             const int8_t* __restrict__ B, int M, int N, int K,
+                                                             Epilogue ep) {
+    extern __shared__ __attribute__((aligned(16))) int8_t bs[];  // [16 NT][K + 16]
+    // Chunks of 16 bytes of the weight per thread: 16 NT rows x K / 16 <= 32
+    // chunks each, over the workgroup's threads.
+    constexpr int kMaxChunks = (16 * NT * (kNarrowMaxK / 16) + 256 * kNarrowWN - 1) / (256 * kNarrowWN);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ks = K >> 6;  // 64-k steps, 1..8
+    const int kc16 = K >> 4;
+    const int ldb = K + 16;
+    constexpr int NTW = (NT + kNarrowWN - 1) / kNarrowWN;  // column tiles per wave
+    const int m0 = blockIdx.x * kNarrowRows + (wave % 4) * 16;
+    const int t0 = (wave / 4) * NTW;
+    // Every load before any is used: the A fragments of all k-steps (rows >=
+    // M read zero: buffer bound), the thread's chunks of the weight (rows >= N
+    // read zero), the epilogue's column and row operands.
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, (uint32_t)M * (uint32_t)K);
+    const int a_off = (m0 + (lane & 15)) * K + (lane >> 4) * 16;
+    i32x4v a[kNarrowMaxK / 64];
+#pragma unroll
+    for (int s = 0; s < kNarrowMaxK / 64; ++s)
+        if (s < ks) a[s] = __builtin_amdgcn_raw_buffer_load_b128(ra, a_off, 64 * s, 0);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(B, (uint32_t)N * (uint32_t)K);
+    const int chunks = 16 * NT * kc16;
+    i32x4v bv[kMaxChunks];
+#pragma unroll
+    for (int u = 0; u < kMaxChunks; ++u) {
+        const int c = tid + 256 * kNarrowWN * u;
+        if (c < chunks) {
+            const int n = c / kc16;
+            bv[u] = __builtin_amdgcn_raw_buffer_load_b128(rb, n * K + (c - n * kc16) * 16, 0, 0);
+        }
+    }
+    double sbj[NT];
+    float bj[NT];
+#pragma unroll
+    for (int tt = 0; tt < NTW; ++tt) {
+        const int t = t0 + tt;
+        const int jc = min(16 * t + (lane & 15), N - 1);
+        sbj[tt] = ep.sb ? ep.sb[ep.sb_per_col ? jc : 0] : 0.0;
+        bj[tt] = ep.bias ? ep.bias[jc] : 0.0f;
+    }
+    double sai[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        sai[r] = ep.out ? ep.sa[ep.sa_per_row ? min(m0 + 4 * (lane >> 4) + r, M - 1) : 0] : 0.0;
+#pragma unroll
+    for (int u = 0; u < kMaxChunks; ++u) {
+        const int c = tid + 256 * kNarrowWN * u;
+        if (c < chunks) {
+            const int n = c / kc16;
+            *reinterpret_cast<i32x4v*>(bs + n * ldb + (c - n * kc16) * 16) = bv[u];
+        }
+    }
+    __syncthreads();
+    i32x4v acc[NTW];
+#pragma unroll
+    for (int t = 0; t < NTW; ++t) acc[t] = i32x4v{0, 0, 0, 0};
+    const int8_t* bl = bs + (lane & 15) * ldb + (lane >> 4) * 16;
+#pragma unroll
+    for (int s = 0; s < kNarrowMaxK / 64; ++s) {
+        if (s < ks) {
+#pragma unroll
+            for (int tt = 0; tt < NTW; ++tt)
+                if (t0 + tt < NT)
+                    acc[tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                        a[s], *reinterpret_cast<const i32x4v*>(bl + 16 * (t0 + tt) * ldb + 64 * s), acc[tt], 0, 0, 0);
+        }
+    }
+    // 16x16 result layout: register r of lane l is row 4 (l / 16) + r,
+    // column l % 16 of the tile.
+#pragma unroll
+    for (int tt = 0; tt < NTW; ++tt) {
+        const int t = t0 + tt;
+        const int64_t j = 16 * t + (lane & 15);
+        if (t >= NT || j >= N) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t i = m0 + 4 * (lane >> 4) + r;
+            if (i >= M) continue;
+            if (ep.acc) ep.acc[i * N + j] = acc[tt][r];
+            if (ep.out) {
+                const float resid = (FUSED && ep.residual) ? ep.residual[i * N + j] : 0.0f;
+                ep.out[i * N + j] = epilogue_finish<FUSED>(ep, acc[tt][r], sai[r] * sbj[tt], bj[tt], resid);
+            }
+        }
+    }
+}
+
+// The weight's LDS copy (16 NT rows of K + 16 bytes) within 64 KiB, 32-bit
+// offsets into A, and enough rows for the chip (2048 rows: 32 workgroups).
+bool narrow_fits(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K) {
+    const int64_t lds = ((N + 15) / 16) * 16 * (K + 16);
+    return N >= 1 && N <= 128 && M >= 2048 && K >= 64 && K <= kNarrowMaxK && K % 64 == 0 && lds <= 65536 &&
+           kh::aligned(A, 16) && kh::aligned(B, 16) && (M + kNarrowRows) * K <= 0x7FFFFFFFLL;
+}
+
+int launch_narrow(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
+                  const Epilogue& ep) {
+    const unsigned blocks = (unsigned)((M + kNarrowRows - 1) / kNarrowRows);
+    const bool fused = ep.act != kActNone || ep.residual;
+    auto go = [&](auto nt) {
+        constexpr int NT = decltype(nt)::value;
+        const size_t lds = (size_t)16 * NT * (K + 16);
+        if (fused)
+            gemm_i8_narrow_kernel<NT, true><<<blocks, 256 * kNarrowWN, lds, d->stream>>>(A, B, (int)M, (int)N, (int)K, ep);
+        else
+            gemm_i8_narrow_kernel<NT, false><<<blocks, 256 * kNarrowWN, lds, d->stream>>>(A, B, (int)M, (int)N, (int)K, ep);
+    };
+    if (N <= 16) go(std::integral_constant<int, 1>());
+    else if (N <= 32) go(std::integral_constant<int, 2>());
+    else if (N <= 48) go(std::integral_constant<int, 3>());
+    else if (N <= 64) go(std::integral_constant<int, 4>());
+    else if (N <= 80) go(std::integral_constant<int, 5>());
+    else if (N <= 96) go(std::integral_constant<int, 6>());
+    else if (N <= 112) go(std::integral_constant<int, 7>());
+    else go(std::integral_constant<int, 8>());
+    return kh::launch_status("gemm_i8_narrow");
+}
+
 template <int BM, int BN, int NS>
 int launch_pingpong_cfg(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
                         const Epilogue& ep, unsigned* parts, int* nparts, int mode) {
@@ -1643,6 +1789,8 @@ static int gemm_i8_impl(const int8_t* a, const int8_t* b_packed, int64_t M, int6
     bool parts_done = false;
     if (skinny_fits(a, b_packed, M, N, K)) {
         rc = launch_skinny(d, a, b_packed, M, N, K, ep);
+    } else if (!parts && narrow_fits(a, b_packed, M, N, K)) {
+        rc = launch_narrow(d, a, b_packed, M, N, K, ep);
     } else if (pingpong_fits(a, b_packed, M, N, K)) {
         // The ping-pong kernel writes one partial per workgroup when they fit.
         const int64_t worst = ((M + 127) / 128) * ((N + 127) / 128);

@@ -42,7 +42,8 @@ def test_gemm_i8_golden(hip, name):
 SHAPES = [
     (64, 512, 512),      # C1's int8 Linear
     (1, 1, 16), (1, 4096, 4096), (8, 4096, 4096), (32, 11008, 4096),  # C5 decode shapes
-    (16384, 65, 384),    # C4 vocab head: N=65 edge tile
+    (16384, 65, 384),    # C4 vocab head: the narrow-N kernel (N=65: a 1-column last tile)
+    (2048, 1, 64), (2049, 16, 128), (4000, 100, 448), (3000, 128, 448), (2100, 17, 512),  # narrow-N kernel
     (256, 1536, 384), (256, 384, 1536),
     (129, 257, 80), (300, 200, 48), (2048, 2048, 512), (2304, 2176, 1024),
     (33, 40, 130), (100, 50, 77), (5, 7, 3),  # K % 16 != 0: byte-gather path
@@ -477,7 +478,7 @@ def test_matmul_f32_c3b_full_size(hip):
 @pytest.mark.parametrize("M,N,K", [(512, 512, 256),      # ping-pong, full tiles
                                    (300, 1152, 384),     # ping-pong, partial tiles
                                    (130, 70, 80),        # general kernel (K % 64 != 0)
-                                   (16384, 65, 384),     # ping-pong, one partial column tile (a vocabulary head)
+                                   (16384, 65, 384),     # a vocabulary head: narrow-N kernel; with partials ping-pong
                                    (8, 512, 512)])       # skinny kernel
 @pytest.mark.parametrize("row_scales", [False, True])
 def test_gemm_i8_fused_epilogues(hip, M, N, K, row_scales):
@@ -515,6 +516,36 @@ def test_gemm_i8_fused_epilogues(hip, M, N, K, row_scales):
     q2, s2 = H.quantize_tensor(r_out)
     np.testing.assert_array_equal(q1.numpy(), q2.numpy())
     assert s1.numpy()[0] == s2.numpy()[0]
+
+
+@pytest.mark.parametrize("M,N,K", [(2055, 65, 384), (4096, 128, 448), (3000, 7, 64)])
+@pytest.mark.parametrize("row_scales", [False, True])
+def test_gemm_i8_narrow_fused_epilogues(hip, M, N, K, row_scales):
+    """The narrow-N kernel (N <= 128, M >= 2048) with the GELU and residual
+    epilogues and no partials: the same bits as the unfused graph, and its
+    int32 accumulators equal the oracle's."""
+    from kansaiml_amd import _native as Nn
+    H, D = hip
+    gen = np.random.Generator(np.random.PCG64(M + 5 * N + 3 * K))
+    a = gen.integers(-127, 128, (M, K), dtype=np.int8)
+    bt = gen.integers(-127, 128, (N, K), dtype=np.int8)
+    sa = gen.uniform(1e-4, 1e-3, M) if row_scales else np.array([3e-4])
+    sb = gen.uniform(1e-4, 1e-3, N)
+    bias = gen.standard_normal(N).astype(np.float32)
+    res = gen.standard_normal((M, N)).astype(np.float32)
+    ad, bd, sad, sbd, biasd = D.from_host(a), D.from_host(bt), D.from_host(sa), D.from_host(sb), D.from_host(bias)
+    plain, acc = H.gemm_i8(ad, bd, sad, sbd, biasd, want_acc=True)
+    eacc = O.ko_gemm_i8(a, bt)
+    np.testing.assert_array_equal(acc.numpy(), eacc)
+    expect = O.ko_epilogue(eacc, sa, sb, bias)
+    np.testing.assert_array_equal(bits32(plain.numpy()), bits32(expect))
+    g_out, _ = H.gemm_i8_fused(ad, bd, sad, sbd, biasd, act="gelu")
+    g_ref = D([M, N])
+    Nn.call("kh_gelu", plain.ptr, g_ref.ptr, M * N)
+    np.testing.assert_array_equal(bits32(g_out.numpy()), bits32(g_ref.numpy()))
+    r_out, _ = H.gemm_i8_fused(ad, bd, sad, sbd, None, residual=D.from_host(res))
+    np.testing.assert_array_equal(bits32(r_out.numpy()),
+                                  bits32((res + O.ko_epilogue(eacc, sa, sb, None)).astype(np.float32)))
 
 
 @pytest.mark.parametrize("M,N,K", [(16384, 1536, 384),   # C4 fc1: ping-pong, two passes
