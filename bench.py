@@ -522,10 +522,13 @@ def bench_c4(steps, warmup):
         ms = eager
     breakdown = c4_gemm_breakdown(model, ids, ms, steps)
     # the same forward with per-token activation scales (an option beside
-    # the reference's per-tensor configuration), replayed as a HIP graph
+    # the reference's per-tensor configuration), replayed as a HIP graph:
+    # LayerNorms emit per-row codes, the attention output is quantized per
+    # row inside the O GEMM (qload, from the attention's per-(row, head)
+    # partials), fc1's output by the per-row quantize
     ms_row = None  # a profiled run traces the configured (per-tensor) forward only
     if GRAPH_TIMING:
-        gr = CharLM(w, act_granularity="row").capture(64, 256)
+        gr = CharLM(w, act_granularity="row", qload=True).capture(64, 256)
         ms_row = time_kernel(lambda: gr(ids, to_host=False), steps, warmup, tag="c4_graph_per_token")
         gr.close()
     ops = int8_linear_ops(w, 64, 256)

@@ -240,6 +240,22 @@ int kh_gemm_i8_qload(const float* x, int64_t M, int64_t N, int64_t K, const unsi
                      const float* residual, float* out, double* x_scale, unsigned* absmax_parts, int max_parts,
                      int* nparts);
 
+/* kh_gemm_i8_qload with one scale per row of x (per token): row i is
+ * quantized with the scale of its own absmax (quantize.py:50-70 applied to
+ * the row), taken from the producer's partials row_parts [M, parts_per_row]
+ * (the max |x| bits of pieces of each row, e.g. kh_attention_rows' one word
+ * per head), inside the GEMM that consumes x, so the codes are never
+ * written; the epilogue then uses sa_i * sb_j.  x_scales (may be NULL)
+ * receives the M binary64 row scales.  The same outputs as
+ * kh_quantize_rows followed by kh_gemm_i8_ex with per-row scales (which run
+ * for shapes the fused kernel does not take: M a multiple of 64, N = 128,
+ * 256 or a multiple of 384, K of 64, parts_per_row <= 16).  A NaN/inf row
+ * reports KH_ERR_NONFINITE at the next synchronize.  No reference
+ * counterpart (the reference has no per-token quantize). */
+int kh_gemm_i8_qload_rows(const float* x, int64_t M, int64_t N, int64_t K, const unsigned* row_parts,
+                          int parts_per_row, const int8_t* b_packed, const double* sb, int sb_per_col,
+                          const float* bias, int act, const float* residual, float* out, double* x_scales);
+
 /* Per-token activation quantize fused into the GEMM's producer: x fp32
  * [M, K] is quantized per row into q_scratch (int8 [M, K]) and
  * sx_scratch (binary64 [M]), then kh_gemm_i8 runs with sa = sx_scratch
@@ -362,6 +378,11 @@ int kh_causal_attention_ex(const float* qkv, int B, int T, int H, int dk, float*
  * is shorter than its position table (train_shakespeare_large.py:86). */
 int kh_attention_ex(const float* qkv, int B, int T, int H, int dk, int causal, float* out, unsigned* absmax_parts,
                     int max_parts, int* nparts);
+/* kh_attention_ex(causal) writing, instead of per-tensor partials, the max
+ * |out| bits of every (row, head): row_parts [B*T, H] -- what a following
+ * per-row (per-token) quantize of out needs (the row's absmax is the max of
+ * its H words; kh_gemm_i8_qload_rows reads them). */
+int kh_attention_rows(const float* qkv, int B, int T, int H, int dk, int causal, float* out, unsigned* row_parts);
 
 /* ---- measurement utility (no reference counterpart) ------------------- */
 

@@ -77,6 +77,7 @@ _SIGNATURES = {
     "kh_gemm_i8_quant": [_vp, _vp, _i64, _i64, _i64, _vp, _int, _vp, _int, _vp, _int, _vp, _vp, _vp],
     "kh_gemm_i8_qload": [_vp, _i64, _i64, _i64, _vp, _int, _vp, _vp, _int, _vp, _int, _vp, _vp, _vp, _vp, _int,
                          ctypes.POINTER(ctypes.c_int)],
+    "kh_gemm_i8_qload_rows": [_vp, _i64, _i64, _i64, _vp, _int, _vp, _vp, _int, _vp, _int, _vp, _vp, _vp],
     "kh_absmax_parts": [_vp, _i64, _vp, _int, ctypes.POINTER(ctypes.c_int)],
     "kh_quantize_tensor_parts": [_vp, _i64, _vp, _int, _vp, _vp],
     "kh_layernorm_ex": [_vp, _i64, _int, _vp, _vp, ctypes.c_float, _vp, _vp, _int, ctypes.POINTER(ctypes.c_int)],
@@ -84,6 +85,7 @@ _SIGNATURES = {
     "kh_causal_attention_ex": [_vp, _int, _int, _int, _int, _vp, _vp, _int, ctypes.POINTER(ctypes.c_int)],
     "kh_layernorm_quant_rows": [_vp, _i64, _int, _vp, _vp, ctypes.c_float, _vp, _vp],
     "kh_attention_ex": [_vp, _int, _int, _int, _int, _int, _vp, _vp, _int, ctypes.POINTER(ctypes.c_int)],
+    "kh_attention_rows": [_vp, _int, _int, _int, _int, _int, _vp, _vp],
     "kh_linear_i8": [_vp, _i64, _i64, _vp, _i64, _vp, _int, _vp, _vp, _vp, _vp],
     "kh_linear_i8_noalloc": [_vp, _i64, _i64, _vp, _i64, _vp, _int, _vp, _vp],
     "kh_linear_i8_tensor": [_vp, _i64, _i64, _vp, _i64, _vp, _int, _vp, _vp, _vp, _vp],

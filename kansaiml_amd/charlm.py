@@ -122,7 +122,9 @@ class CharLM:
         qload (kir.quant_fusion's option): the remaining per-tensor
         quantizes (of the attention and fc1 outputs) run inside the GEMM
         that consumes them (kh_gemm_i8_qload), so their codes are never
-        written.
+        written; with act_granularity "row", the attention output's per-row
+        quantize runs inside the O GEMM (kh_gemm_i8_qload_rows, from the
+        attention's per-(row, head) partials).
         act_granularity: "tensor" (the reference's quantize_symmetric over the
         whole activation, the C4 configuration) or "row" (one scale per token;
         a LayerNorm then emits codes and scales in one pass)."""

@@ -199,7 +199,8 @@ __device__ __forceinline__ ColEpi col_epi(const Epilogue& ep, int64_t j) {
 template <bool FUSED, int MODE, bool ROWSA = false>
 __device__ __forceinline__ unsigned store_block32_full(const Epilogue& ep, int64_t rowblk, int64_t colblk, int N,
                                                        int lane, double sa, const i32x16& v,
-                                                       const kh::quant::Scale& sc, ColEpi ce) {
+                                                       const kh::quant::Scale& sc, ColEpi ce,
+                                                       const double* sa_rows = nullptr, int sa_row0 = 0) {
     const int fr = lane & 31, fh = lane >> 5;
     const double sbj = ce.sb;
     const double s = sa * sbj;
@@ -218,7 +219,8 @@ __device__ __forceinline__ unsigned store_block32_full(const Epilogue& ep, int64
         // Value r of this lane is row rowblk + 4*fh + 8*(r/4) + r%4: four
         // row scales at a time (sa[i] * sb[j], then the product), so only
         // four binary64 scales are live at once.
-        const double* sar = ep.sa + rowblk + 4 * fh;
+        // (sa_rows: the block's row scales elsewhere, first row at sa_row0.)
+        const double* sar = (sa_rows ? sa_rows + sa_row0 : ep.sa + rowblk) + 4 * fh;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             double s4[4];
@@ -713,7 +715,7 @@ __global__ __launch_bounds__(512, BN == 256 ? 2 : ((BM == 256 || NS >= 4 || (FUS
 // ---------------------------------------------------------------------------
 constexpr int kQlBM = 64;
 
-template <int NB, int NS, bool FUSED>
+template <int NB, int NS, bool FUSED, bool ROWS = false>
 __global__ __launch_bounds__(512, 2) void gemm_i8_qload_kernel(const float* __restrict__ X, int M, int N, int K,
                                                                const unsigned* __restrict__ xparts, int nxparts,
                                                                const int8_t* __restrict__ B, Epilogue ep,
@@ -727,13 +729,10 @@ __global__ __launch_bounds__(512, 2) void gemm_i8_qload_kernel(const float* __re
     static_assert(NS >= 2 && NS <= 5, "wait_loads_beyond covers up to 3 stages ahead");
     __shared__ __attribute__((aligned(1024))) int8_t lds[NS * kStage];
     __shared__ unsigned red[kWaves];
-
-    // The tensor's scale (quantize.py:67-68), the same in every workgroup.
-    const kh::quant::Scale sc = kh::quant::make_scale(kh::quant::block_reduce_partials(xparts, nxparts, red));
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
-        if (ep.qscale) *ep.qscale = sc.s;
-        if (sc.bad) kh::quant::flag_nonfinite(ep.fault);
-    }
+    // ROWS: the workgroup's 64 row scales (quantize.py:67-68 per row).
+    __shared__ double row_s[ROWS ? kQlBM : 1];
+    __shared__ float row_rf[ROWS ? kQlBM : 1];
+    __shared__ unsigned row_flags[ROWS ? kQlBM : 1];
 
     const int tiles_n = N / BN;
     const int tm = blockIdx.x / tiles_n, tn = blockIdx.x - tm * tiles_n;
@@ -741,10 +740,51 @@ __global__ __launch_bounds__(512, 2) void gemm_i8_qload_kernel(const float* __re
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;
     auto swz = [](int r) { return (r >> 2) & 3; };
-
     // A: 8 floats of row t / 8 at k = 8 (t % 8) of each step; their codes go
     // to bytes 8 (t % 2) of chunk (t % 8) / 2.
     const int arow = tid >> 3, aq = tid & 7;
+
+    kh::quant::Scale sc;
+    if constexpr (!ROWS) {
+        // The tensor's scale (quantize.py:67-68), the same in every workgroup.
+        sc = kh::quant::make_scale(kh::quant::block_reduce_partials(xparts, nxparts, red));
+        if (blockIdx.x == 0 && threadIdx.x == 0) {
+            if (ep.qscale) *ep.qscale = sc.s;
+            if (sc.bad) kh::quant::flag_nonfinite(ep.fault);
+        }
+    } else {
+        // Row r's scale from the producer's nxparts (<= 16) words of row r,
+        // all issued at once through one resource for the workgroup's rows
+        // (a resource per lane would be a loop over the lanes); indices past
+        // the row read its last word again, which leaves the maximum
+        // unchanged.  The tn == 0 workgroups report the scales.
+        if (tid < kQlBM) {
+            const int64_t gr = (int64_t)tm * kQlBM + tid;
+            const __amdgpu_buffer_rsrc_t rp =
+                make_rsrc(xparts + (int64_t)tm * kQlBM * nxparts, (uint32_t)(kQlBM * nxparts) * 4u);
+            unsigned w[16];
+#pragma unroll
+            for (int p = 0; p < 16; ++p)
+                w[p] = __builtin_amdgcn_raw_buffer_load_b32(rp, (tid * nxparts + min(p, nxparts - 1)) * 4, 0, 0);
+            unsigned mb = 0;
+#pragma unroll
+            for (int p = 0; p < 16; ++p) mb = max(mb, w[p]);
+            const kh::quant::Scale s = kh::quant::make_scale(mb);
+            row_s[tid] = s.s;
+            row_rf[tid] = s.rf;
+            row_flags[tid] = (s.fast ? 1u : 0u) | (s.bad ? 2u : 0u);
+            if (tn == 0) {
+                if (ep.qscale) ep.qscale[gr] = s.s;
+                if (s.bad) kh::quant::flag_nonfinite(ep.fault);
+            }
+        }
+        __syncthreads();
+        sc.s = row_s[arow];
+        sc.rf = row_rf[arow];
+        sc.fast = (row_flags[arow] & 1u) != 0;
+        sc.bad = (row_flags[arow] & 2u) != 0;
+    }
+
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(X + (int64_t)tm * kQlBM * K, (uint32_t)kQlBM * (uint32_t)K * 4u);
     const int a_voff = (arow * K + aq * 8) * 4;
     const int a_lds = arow * BK + (((aq >> 1) ^ swz(arow)) << 4) + 8 * (aq & 1);
@@ -817,9 +857,14 @@ __global__ __launch_bounds__(512, 2) void gemm_i8_qload_kernel(const float* __re
     unsigned mx = 0;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-        mx = max(mx, store_block32_full<FUSED, kh::quant::kOutStore>(ep, (int64_t)tm * kQlBM + wm * 32,
-                                                                      (int64_t)tn * BN + wn * 32 * NB + b * 32, N,
-                                                                      lane, sc.s, acc[b], sc, ce[b]));
+        if constexpr (ROWS)
+            mx = max(mx, store_block32_full<FUSED, kh::quant::kOutStore, true>(
+                             ep, (int64_t)tm * kQlBM + wm * 32, (int64_t)tn * BN + wn * 32 * NB + b * 32, N, lane,
+                             0.0, acc[b], sc, ce[b], row_s, wm * 32));
+        else
+            mx = max(mx, store_block32_full<FUSED, kh::quant::kOutStore>(ep, (int64_t)tm * kQlBM + wm * 32,
+                                                                          (int64_t)tn * BN + wn * 32 * NB + b * 32, N,
+                                                                          lane, sc.s, acc[b], sc, ce[b]));
         __builtin_amdgcn_sched_barrier(0);
     }
     if (parts) {
@@ -1751,16 +1796,16 @@ int qload_nb(const float* x, const int8_t* b, int64_t M, int64_t N, int64_t K) {
     return N % 384 == 0 ? 3 : 0;
 }
 
-template <int NB>
+template <int NB, bool ROWS = false>
 int launch_qload(kh::Device* d, const float* x, int64_t M, int64_t N, int64_t K, const unsigned* xparts,
                  int nxparts, const int8_t* b, const Epilogue& ep, unsigned* parts) {
     const unsigned grid = (unsigned)((M / kQlBM) * (N / (128 * NB)));
     if (ep.act != kActNone || ep.residual)
-        gemm_i8_qload_kernel<NB, 5, true><<<grid, 512, 0, d->stream>>>(x, (int)M, (int)N, (int)K, xparts, nxparts, b,
-                                                                       ep, parts);
+        gemm_i8_qload_kernel<NB, 5, true, ROWS><<<grid, 512, 0, d->stream>>>(x, (int)M, (int)N, (int)K, xparts,
+                                                                             nxparts, b, ep, parts);
     else
-        gemm_i8_qload_kernel<NB, 5, false><<<grid, 512, 0, d->stream>>>(x, (int)M, (int)N, (int)K, xparts, nxparts,
-                                                                        b, ep, parts);
+        gemm_i8_qload_kernel<NB, 5, false, ROWS><<<grid, 512, 0, d->stream>>>(x, (int)M, (int)N, (int)K, xparts,
+                                                                              nxparts, b, ep, parts);
     return kh::launch_status("gemm_i8_qload");
 }
 
@@ -1924,6 +1969,39 @@ int kh_gemm_i8_qload(const float* x, int64_t M, int64_t N, int64_t K, const unsi
     if (!rc)
         rc = kh_gemm_i8_ex(q, b_packed, M, N, K, sc, 0, sb, sb_per_col, bias, act, residual, out, absmax_parts,
                            max_parts, nparts);
+    const int frc = kh_free(tmp);  // stream-ordered reuse: later work is queued behind the GEMM
+    return rc ? rc : frc;
+}
+
+int kh_gemm_i8_qload_rows(const float* x, int64_t M, int64_t N, int64_t K, const unsigned* row_parts,
+                          int parts_per_row, const int8_t* b_packed, const double* sb, int sb_per_col,
+                          const float* bias, int act, const float* residual, float* out, double* x_scales) {
+    KH_REQUIRE(M >= 0 && N >= 0 && K >= 0, "kh_gemm_i8_qload_rows: negative shape");
+    KH_REQUIRE(K <= 133144, "kh_gemm_i8_qload_rows: K > 133144 could overflow the int32 accumulator");
+    KH_REQUIRE(M <= 0xFFFFLL * 128 && N <= 0x7FFFFFFFLL, "kh_gemm_i8_qload_rows: shape too large");
+    KH_REQUIRE(act == kActNone || act == kActGelu, "kh_gemm_i8_qload_rows: unknown activation");
+    KH_REQUIRE(parts_per_row >= 1, "kh_gemm_i8_qload_rows: parts_per_row must be >= 1");
+    if (M == 0) return KH_OK;
+    KH_REQUIRE(x && row_parts && b_packed && sb && (out || N == 0), "kh_gemm_i8_qload_rows: null pointer");
+    KH_DEVICE_OR_RETURN(d);
+    const int nb = parts_per_row <= 16 && K > 0 ? qload_nb(x, b_packed, M, N, K) : 0;
+    if (nb) {
+        Epilogue ep{nullptr, sb, bias, out, nullptr, 1, sb_per_col, act, residual, nullptr, nullptr, 0, x_scales,
+                    d->fault};
+        return nb == 1   ? launch_qload<1, true>(d, x, M, N, K, row_parts, parts_per_row, b_packed, ep, nullptr)
+               : nb == 2 ? launch_qload<2, true>(d, x, M, N, K, row_parts, parts_per_row, b_packed, ep, nullptr)
+                         : launch_qload<3, true>(d, x, M, N, K, row_parts, parts_per_row, b_packed, ep, nullptr);
+    }
+    // Other shapes: the per-row quantize (the same row scales: each is the
+    // row's absmax, which the partials only hold in pieces) and the GEMM.
+    void* tmp = nullptr;
+    int rc = kh_alloc((size_t)(M * K) + (size_t)M * 8, &tmp);
+    if (rc) return rc;
+    double* sc = x_scales ? x_scales : static_cast<double*>(tmp);
+    int8_t* q = static_cast<int8_t*>(tmp) + (size_t)M * 8;
+    rc = kh_quantize_rows(x, M, K, q, sc);
+    if (!rc && N)
+        rc = kh_gemm_i8_ex(q, b_packed, M, N, K, sc, 1, sb, sb_per_col, bias, act, residual, out, nullptr, 0, nullptr);
     const int frc = kh_free(tmp);  // stream-ordered reuse: later work is queued behind the GEMM
     return rc ? rc : frc;
 }

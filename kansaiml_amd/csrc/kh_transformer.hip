@@ -613,7 +613,8 @@ __device__ __forceinline__ void attention_pv(const float* vs, const f32x4v (&st)
 
 template <bool CAUSAL>
 __global__ __launch_bounds__(256, 3) void attention_mfma_kernel(const float* __restrict__ qkv, int B, int T, int H,
-                                                             float* __restrict__ out, unsigned* __restrict__ parts) {
+                                                             float* __restrict__ out, unsigned* __restrict__ parts,
+                                                             unsigned* __restrict__ rparts) {
     __shared__ __attribute__((aligned(1024))) float ks[kAttK * kDk];
     __shared__ __attribute__((aligned(1024))) float vs[kAttK * kDk];
     using kh::pipe::wait_imm;
@@ -738,6 +739,14 @@ __global__ __launch_bounds__(256, 3) void attention_mfma_kernel(const float* __r
 #pragma unroll
             for (int e = 0; e < 4; ++e) mxo = max(mxo, kh::abs_bits32(y[e]));
         }
+    }
+    if (rparts) {
+        // Per-(row, head) max |out| bits, for a following per-row quantize:
+        // the lanes li, li + 16, li + 32, li + 48 hold query q's 64 outputs.
+        unsigned mr = mxo;
+        mr = max(mr, (unsigned)__shfl_xor((int)mr, 16));
+        mr = max(mr, (unsigned)__shfl_xor((int)mr, 32));
+        if (g == 0 && q < T) rparts[((int64_t)b * T + q) * H + h] = mr;
     }
     if (parts) {
         // Per-workgroup max |out| bits, for a following per-tensor quantize.
@@ -909,8 +918,8 @@ int kh_gelu(const float* x, float* out, int64_t n) {
     return kh::launch_status("gelu");
 }
 
-int kh_attention_ex(const float* qkv, int B, int T, int H, int dk, int causal, float* out, unsigned* absmax_parts,
-                    int max_parts, int* nparts) {
+static int attention_impl(const float* qkv, int B, int T, int H, int dk, int causal, float* out,
+                          unsigned* absmax_parts, int max_parts, int* nparts, unsigned* row_parts) {
     KH_REQUIRE(B > 0 && T > 0 && H > 0, "kh_attention: bad shape");
     KH_REQUIRE(dk == kDk, "kh_attention: only head dimension 64 is supported");
     KH_REQUIRE(causal == 0 || causal == 1, "kh_attention: causal must be 0 or 1");
@@ -932,10 +941,10 @@ int kh_attention_ex(const float* qkv, int B, int T, int H, int dk, int causal, f
     // to Q together with log2(e), keeping the scores in base-2 units.
     if (causal)
         attention_mfma_kernel<true><<<(unsigned)blocks, 256, 0, d->stream>>>(qkv, B, T, H, out,
-                                                                          fused ? absmax_parts : nullptr);
+                                                                          fused ? absmax_parts : nullptr, row_parts);
     else
         attention_mfma_kernel<false><<<(unsigned)blocks, 256, 0, d->stream>>>(qkv, B, T, H, out,
-                                                                           fused ? absmax_parts : nullptr);
+                                                                           fused ? absmax_parts : nullptr, row_parts);
     int rc = kh::launch_status("attention");
     if (rc || !absmax_parts) return rc;
     if (fused) {
@@ -943,6 +952,16 @@ int kh_attention_ex(const float* qkv, int B, int T, int H, int dk, int causal, f
         return KH_OK;
     }
     return kh_absmax_parts(out, (int64_t)B * T * H * kDk, absmax_parts, max_parts, nparts);
+}
+
+int kh_attention_ex(const float* qkv, int B, int T, int H, int dk, int causal, float* out, unsigned* absmax_parts,
+                    int max_parts, int* nparts) {
+    return attention_impl(qkv, B, T, H, dk, causal, out, absmax_parts, max_parts, nparts, nullptr);
+}
+
+int kh_attention_rows(const float* qkv, int B, int T, int H, int dk, int causal, float* out, unsigned* row_parts) {
+    KH_REQUIRE(row_parts, "kh_attention_rows: null row_parts");
+    return attention_impl(qkv, B, T, H, dk, causal, out, nullptr, 0, nullptr, row_parts);
 }
 
 int kh_causal_attention_ex(const float* qkv, int B, int T, int H, int dk, float* out, unsigned* absmax_parts,

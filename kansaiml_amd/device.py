@@ -33,10 +33,11 @@ def _dtype_name(dt) -> str:
 class DeviceTensor:
     """A contiguous device buffer with a shape and a KIR dtype string."""
 
-    # absmax_parts: the per-tensor absmax partials the producing kernel wrote
-    # alongside this tensor, when a fused graph asked for them (kir.py).
+    # absmax_parts / row_parts: the per-tensor or per-row absmax partials the
+    # producing kernel wrote alongside this tensor, when a fused graph asked
+    # for them (kir.py).
     # _base: the tensor a view was cut from (kept alive as long as the view).
-    __slots__ = ("ptr", "shape", "dtype", "nbytes", "_owned", "absmax_parts", "_base", "__weakref__")
+    __slots__ = ("ptr", "shape", "dtype", "nbytes", "_owned", "absmax_parts", "row_parts", "_base", "__weakref__")
 
     def __init__(self, shape, dtype: str = "float32"):
         if dtype not in DTYPES:
@@ -47,6 +48,7 @@ class DeviceTensor:
         self.dtype = dtype
         self.nbytes = math.prod(self.shape) * np.dtype(DTYPES[dtype]).itemsize
         self.ptr, self._owned, self.absmax_parts, self._base = None, False, None, None  # until kh_alloc succeeds
+        self.row_parts = None
         p = ctypes.c_void_p()
         N.call("kh_alloc", max(self.nbytes, 1), ctypes.byref(p))
         self.ptr = p
@@ -105,7 +107,7 @@ class DeviceTensor:
             raise ValueError(f"reshape: cannot view {self.shape} as {shape}")
         v = object.__new__(DeviceTensor)
         v.ptr, v.shape, v.dtype, v.nbytes, v._owned = self.ptr, shape, self.dtype, self.nbytes, False
-        v.absmax_parts, v._base = None, self
+        v.absmax_parts, v.row_parts, v._base = None, None, self
         return v
 
     def view(self, offset: int, shape) -> "DeviceTensor":
@@ -120,7 +122,7 @@ class DeviceTensor:
         v = object.__new__(DeviceTensor)
         v.ptr = ctypes.c_void_p(self.addr + offset * item)
         v.shape, v.dtype, v.nbytes, v._owned = shape, self.dtype, n * item, False
-        v.absmax_parts, v._base = None, self
+        v.absmax_parts, v.row_parts, v._base = None, None, self
         return v
 
     def copy_from(self, src) -> None:

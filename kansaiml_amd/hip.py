@@ -458,6 +458,66 @@ def attention(qkv: DeviceTensor, batch: int, seq: int, heads: int, d_model: int,
     return out, parts
 
 
+class RowParts:
+    """Max |x| bits of pieces of every row of x (int32 [rows, per_row]) that a
+    producer kernel wrote alongside x, for a per-row quantize of x inside
+    the GEMM that consumes it (gemm_i8_qload_rows)."""
+
+    def __init__(self, rows: int, per_row: int):
+        self.buf = DeviceTensor([rows, per_row], "int32")
+        self.per_row = per_row
+
+    def release(self):
+        self.buf.release()
+
+
+def attention_rows(qkv: DeviceTensor, batch: int, seq: int, heads: int, d_model: int, *, causal: bool = True):
+    """attention() also writing the max |out| bits of every (row, head).
+    Returns (out, RowParts)."""
+    _need(qkv, "float32", 2, "attention(qkv)")
+    if heads <= 0 or d_model != heads * 64:
+        raise RuntimeError(f"attention: d_model must be heads * 64 (the kernel's head size), got {d_model} "
+                           f"for {heads} heads")
+    if batch < 0 or seq < 0 or list(qkv.shape) != [batch * seq, 3 * d_model]:
+        raise RuntimeError(f"attention: qkv must be [batch * seq, 3 * d_model] = [{batch * seq}, {3 * d_model}], "
+                           f"got {qkv.shape}")
+    out = DeviceTensor([batch * seq, d_model], "float32")
+    rp = RowParts(batch * seq, heads)
+    N.call("kh_attention_rows", qkv.ptr, batch, seq, heads, d_model // heads, int(bool(causal)), out.ptr, rp.buf.ptr)
+    return out, rp
+
+
+def gemm_i8_qload_rows(x: DeviceTensor, rp: RowParts, b_packed: DeviceTensor, sb: DeviceTensor,
+                       bias: DeviceTensor | None = None, *, act: str | None = None,
+                       residual: DeviceTensor | None = None, want_scales: bool = False):
+    """The per-row (per-token) quantize of x [..., M, K] fp32 inside the int8
+    GEMM that consumes it, each row's scale from its producer's partials:
+    the same output as quantize_rows(x) then gemm_i8_fused with per-row
+    scales, without writing the codes.  Returns out, or (out, row scales
+    float64 [M]) when want_scales."""
+    M, K, lead = _rows(x, "float32", "gemm_i8_qload_rows(x)")
+    _need(b_packed, "int8", 2, "gemm_i8_qload_rows(b)")
+    Nn, K2 = b_packed.shape
+    if K != K2:
+        raise RuntimeError(f"gemm_i8_qload_rows: incompatible shapes {x.shape} x {b_packed.shape}^T")
+    if list(rp.buf.shape) != [M, rp.per_row]:
+        raise RuntimeError(f"gemm_i8_qload_rows: partials {rp.buf.shape} do not cover the {M} rows of x")
+    if act not in ACTS:
+        raise ValueError(f"gemm_i8_qload_rows: unknown activation {act!r}")
+    sb_mode = _scale_mode(sb, Nn, "gemm_i8_qload_rows(sb)")
+    if bias is not None:
+        _need(bias, "float32", 1, "gemm_i8_qload_rows(bias)")
+        if bias.shape[0] != Nn:
+            raise RuntimeError("gemm_i8_qload_rows: bias must have N entries")
+    if residual is not None:
+        _need_residual(residual, lead, Nn, "gemm_i8_qload_rows")
+    out = DeviceTensor(lead + [Nn], "float32")
+    scales = DeviceTensor([M], "float64") if want_scales else None
+    N.call("kh_gemm_i8_qload_rows", x.ptr, M, Nn, K, rp.buf.ptr, rp.per_row, b_packed.ptr, sb.ptr, sb_mode,
+           _opt(bias), ACTS[act], _opt(residual), out.ptr, _opt(scales))
+    return (out, scales) if want_scales else out
+
+
 def causal_attention(qkv: DeviceTensor, batch: int, seq: int, heads: int, d_model: int, *, absmax: bool = False):
     """attention() under the causal mask."""
     return attention(qkv, batch, seq, heads, d_model, causal=True, absmax=absmax)

@@ -244,6 +244,8 @@ def quant_fusion(graph, producer_quant: bool | str = False, qload: bool = False)
                                                  =>  int8_linear
       with qload=True, also the per-tensor quantize of its activation:
       quantize -> int8_matmul -> ...             =>  int8_linear (qload)
+      and the per-row quantize of an attention output:
+      attention -> quantize(row) -> int8_matmul  =>  attention (row_absmax) -> int8_linear (qload, rows)
       matmul -> add(bias)                        =>  matmul_bias
       add(bias) -> relu                          =>  fused_bias_relu
     and, with producer_quant=True (both) or "layer_norm" (the second only),
@@ -313,6 +315,16 @@ def quant_fusion(graph, producer_quant: bool | str = False, qload: bool = False)
                     chain.insert(0, qa.id)
                     ins[0] = qa.inputs[0]
                     attrs["qload"] = True
+                elif (qload and qa.op == "quantize" and qa.attrs.get("granularity") == "row"
+                        and only_user(qa.id) == n.id and qa.id not in fused
+                        and by_id[qa.inputs[0]].op in _ROW_ABSMAX_PRODUCERS
+                        and only_user(qa.inputs[0]) == qa.id):
+                    # The per-row quantize of a producer that writes per-row
+                    # partials, inside the GEMM (kh_gemm_i8_qload_rows).
+                    chain.insert(0, qa.id)
+                    ins[0] = qa.inputs[0]
+                    attrs["qload"] = True
+                    attrs["rows"] = True
                 nxt = next_free(dq)
                 if nxt is not None and by_id[nxt].op == "add":
                     a_in = by_id[nxt].inputs
@@ -384,9 +396,12 @@ def quant_fusion(graph, producer_quant: bool | str = False, qload: bool = False)
     out.output = remap[graph.output]
 
     # Phase 3: producers of a per-tensor quantize (or of a quantize fused
-    # into its int8_linear) write its absmax partials.
+    # into its int8_linear) write its absmax partials; producers of a per-row
+    # quantize fused into its int8_linear write per-row partials.
     for n in out.nodes:
-        if ((n.op == "quantize" and n.attrs.get("granularity", "tensor") == "tensor")
+        if n.op == "int8_linear" and n.attrs.get("rows"):
+            out.nodes[n.inputs[0]].attrs["row_absmax"] = True
+        elif ((n.op == "quantize" and n.attrs.get("granularity", "tensor") == "tensor")
                 or (n.op == "int8_linear" and n.attrs.get("qload"))):
             src = out.nodes[n.inputs[0]]
             if src.op in _ABSMAX_PRODUCERS:
@@ -395,6 +410,8 @@ def quant_fusion(graph, producer_quant: bool | str = False, qload: bool = False)
 
 
 _ABSMAX_PRODUCERS = ("int8_linear", "layer_norm", "attention")
+# Producers that can write per-row partials (kh_attention_rows).
+_ROW_ABSMAX_PRODUCERS = ("attention",)
 
 # quant_fusion(qload=True) fuses a quantize into its GEMM only for activations
 # of at most this many columns: on MI355X the fused kernel (one workgroup
@@ -556,6 +573,16 @@ def _exec(node, vals):
         at = node.attrs
         bias = ins[2] if at.get("bias") else None
         residual = ins[-1] if at.get("residual") else None
+        if at.get("rows"):
+            rp = getattr(x, "row_parts", None)
+            if rp is not None:
+                return H.gemm_i8_qload_rows(x, rp, w.codes, w.scales, bias, act=at.get("act"), residual=residual)
+            # No producer partials: the per-row quantize, then the GEMM.
+            q, s = H.quantize_rows(x)
+            out, _ = H.gemm_i8_fused(q, w.codes, s, w.scales, bias, act=at.get("act"), residual=residual)
+            q.release()
+            s.release()
+            return out
         parts = getattr(x, "absmax_parts", None)
         if parts is None and not at.get("act") and residual is None and not at.get("absmax"):
             # No producer partials and a plain epilogue: kh_linear_i8_tensor
@@ -616,6 +643,11 @@ def _exec(node, vals):
         N.call("kh_gelu", ins[0].ptr, out.ptr, ins[0].numel())
         return out
     if op == "attention":
+        if node.attrs.get("row_absmax"):
+            out, rp = H.attention_rows(ins[0], node.attrs["batch"], node.attrs["seq"], node.attrs["heads"],
+                                       node.shape[1], causal=node.attrs["causal"])
+            out.row_parts = rp
+            return out
         out, parts = H.attention(ins[0], node.attrs["batch"], node.attrs["seq"], node.attrs["heads"], node.shape[1],
                                  causal=node.attrs["causal"], absmax=bool(node.attrs.get("absmax")))
         return _with_parts(out, parts)
@@ -627,9 +659,9 @@ def _exec(node, vals):
 def _release(v):
     from .quantize import QTensor
     if isinstance(v, DeviceTensor):
-        parts = getattr(v, "absmax_parts", None)
-        if parts is not None:
-            parts.release()
+        for parts in (getattr(v, "absmax_parts", None), getattr(v, "row_parts", None)):
+            if parts is not None:
+                parts.release()
         v.release()
     elif isinstance(v, _Acc):
         v.acc.release()

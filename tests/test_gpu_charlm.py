@@ -391,7 +391,13 @@ def _check_node_sampled(node, got, ins, gen, nrows=64, nbatches=3):
     if op == "int8_linear":
         from oracle import oracle as O
         rows = np.sort(gen.choice(got.shape[0], nrows, replace=False))
-        if node.attrs.get("qload"):
+        if node.attrs.get("qload") and node.attrs.get("rows"):
+            # per-row scales: each row's own absmax (the oracle's per-row quantize)
+            q, s = O.ko_quantize_rows(ins[0])
+            ins = [(q, s)] + list(ins[1:])
+            node = type("N", (), {"op": "int8_linear",
+                                  "attrs": {k: v for k, v in node.attrs.items() if k not in ("qload", "rows")}})()
+        elif node.attrs.get("qload"):
             # the per-tensor scale depends on the whole input: quantize it all
             q, s = O.ko_quantize_tensor(ins[0])
             ins = [(q.reshape(ins[0].shape), np.array([s]))] + list(ins[1:])
@@ -413,7 +419,7 @@ def _check_node_sampled(node, got, ins, gen, nrows=64, nbatches=3):
         _check_node(node, got, ins)
 
 
-@pytest.mark.parametrize("act_granularity,qload", [("tensor", False), ("tensor", True), ("row", False)])
+@pytest.mark.parametrize("act_granularity,qload", [("tensor", False), ("tensor", True), ("row", False), ("row", True)])
 def test_full_c4_forward(G, act_granularity, qload):
     """Config C4 at full size (vocab 65, d 384, 6 heads, 6 layers, FFN 1536,
     seq 256, batch 64), node by node on the GPU's own inputs: every
@@ -446,7 +452,8 @@ def test_full_c4_forward(G, act_granularity, qload):
     # 6 blocks: 2 LayerNorms, 4 Linears, attention; then the final LayerNorm
     # and the head.  The LayerNorms emit their own codes; the attention and
     # fc1 outputs are quantized by a quantize node, or with qload the
-    # attention output inside the O GEMM.
+    # attention output inside the O GEMM (per tensor from the attention's
+    # partials, or per row from its per-(row, head) partials).
     if not qload:
         assert counts == {"embedding": 1, ln: 13, "int8_linear": 25, "attention": 6, "quantize": 12}, counts
     else:

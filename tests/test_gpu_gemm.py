@@ -815,3 +815,91 @@ def test_layernorm_and_attention_absmax_parts(hip):
     Nn.call("kh_quantize_tensor_parts", out2.ptr, 1000 * 384, small.ptr, n.value, q3.ptr, s3.ptr)
     np.testing.assert_array_equal(q3.numpy(), q_ln.numpy())
     assert s3.numpy()[0] == s_ln.numpy()[0]
+
+
+def _row_parts_host(x, per_row):
+    """Max |x| bits of per_row equal pieces of every row (a producer's row
+    partials, computed on the host)."""
+    bits = np.ascontiguousarray(x, np.float32).view(np.uint32) & np.uint32(0x7FFFFFFF)
+    rows, k = bits.shape
+    return bits.reshape(rows, per_row, k // per_row).max(axis=2).astype(np.uint32).view(np.int32)
+
+
+@pytest.mark.parametrize("batch,seq,heads,causal", [(2, 100, 2, True), (3, 256, 6, True), (2, 64, 3, False)])
+def test_attention_row_partials(hip, batch, seq, heads, causal):
+    """kh_attention_rows writes the max |out| bits of every (row, head) of the
+    output it stores, and the output is kh_attention_ex's bit for bit."""
+    H, D = hip
+    gen = np.random.Generator(np.random.PCG64(batch * 1000 + seq + heads))
+    d = 64 * heads
+    qkv = D.from_host((gen.standard_normal((batch * seq, 3 * d)) * 1.5).astype(np.float32))
+    out, rp = H.attention_rows(qkv, batch, seq, heads, d, causal=causal)
+    ref, _ = H.attention(qkv, batch, seq, heads, d, causal=causal)
+    o = out.numpy()
+    np.testing.assert_array_equal(bits32(o), bits32(ref.numpy()))
+    np.testing.assert_array_equal(rp.buf.numpy(), _row_parts_host(o, heads))
+
+
+@pytest.mark.parametrize("M,N,K,P", [(1024, 384, 384, 6),    # C4's O: the fused kernel, 6 parts per row
+                                     (2048, 384, 1536, 12),  # fc2's shape, 12 parts per row
+                                     (512, 256, 512, 1),     # N = 256 tile, one part per row
+                                     (128, 128, 64, 16),     # N = 128 tile, 16 parts
+                                     (100, 200, 384, 6),     # unfused: per-row quantize + GEMM
+                                     (1024, 384, 384, 32)])  # more than 16 parts: unfused
+def test_gemm_i8_qload_rows_matches_two_steps(hip, M, N, K, P):
+    """kh_gemm_i8_qload_rows equals the oracle's per-row quantize, int32 GEMM
+    and binary64 epilogue, bit for bit, for the plain, GELU and residual
+    epilogues; its row scales are the oracle's; rows of zeros, exact ties
+    and outliers included."""
+    H, D = hip
+    gen = np.random.Generator(np.random.PCG64(M + 7 * N + 3 * K + P))
+    x = (gen.standard_normal((M, K)) * 2).astype(np.float32)
+    x[3] = 0.0
+    x[5] = gen.integers(-126, 126, K).astype(np.float32) + np.float32(0.5)
+    x[5, 0] = 127.0
+    x[7, K // 2] = 300.0
+    bt = gen.integers(-127, 128, (N, K), dtype=np.int8)
+    sb = gen.uniform(1e-4, 1e-3, N)
+    bias = gen.standard_normal(N).astype(np.float32)
+    res = gen.standard_normal((M, N)).astype(np.float32)
+    rp = H.RowParts(M, P)
+    rp.buf.copy_from(_row_parts_host(x, P))
+    xd, bd, sbd, biasd = D.from_host(x), D.from_host(bt), D.from_host(sb), D.from_host(bias)
+    qx, sx = O.ko_quantize_rows(x)
+    eacc = O.ko_gemm_i8(qx, bt)
+    expect = O.ko_epilogue(eacc, sx, sb, bias)
+    out, scales = H.gemm_i8_qload_rows(xd, rp, bd, sbd, biasd, want_scales=True)
+    np.testing.assert_array_equal(scales.numpy().view(np.uint64), sx.view(np.uint64))
+    np.testing.assert_array_equal(bits32(out.numpy()), bits32(expect))
+    plain, _ = H.gemm_i8(D.from_host(qx), bd, D.from_host(sx), sbd, biasd)
+    g_ref = D([M, N])
+    from kansaiml_amd import _native as Nn
+    Nn.call("kh_gelu", plain.ptr, g_ref.ptr, M * N)
+    g = H.gemm_i8_qload_rows(xd, rp, bd, sbd, biasd, act="gelu")
+    np.testing.assert_array_equal(bits32(g.numpy()), bits32(g_ref.numpy()))
+    r = H.gemm_i8_qload_rows(xd, rp, bd, sbd, None, residual=D.from_host(res))
+    np.testing.assert_array_equal(bits32(r.numpy()), bits32((res + O.ko_epilogue(eacc, sx, sb, None)).astype(np.float32)))
+
+
+def test_gemm_i8_qload_rows_reports_nonfinite(hip):
+    """A NaN in a row reaches the per-row scale: ValueError at the next
+    synchronize, as kh_quantize_rows reports it; a clean call afterwards is
+    exact."""
+    from kansaiml_amd import _native as Nn
+    H, D = hip
+    gen = np.random.Generator(np.random.PCG64(5))
+    M, N, K = 256, 384, 384
+    x = gen.standard_normal((M, K)).astype(np.float32)
+    bt = gen.integers(-127, 128, (N, K), dtype=np.int8)
+    sb = gen.uniform(1e-4, 1e-3, N)
+    xb = x.copy()
+    xb[17, 100] = np.nan
+    rp = H.RowParts(M, 6)
+    rp.buf.copy_from(_row_parts_host(xb, 6))
+    H.gemm_i8_qload_rows(D.from_host(xb), rp, D.from_host(bt), D.from_host(sb))
+    with pytest.raises(ValueError):
+        Nn.synchronize()
+    rp.buf.copy_from(_row_parts_host(x, 6))
+    out = H.gemm_i8_qload_rows(D.from_host(x), rp, D.from_host(bt), D.from_host(sb)).numpy()
+    qx, sx = O.ko_quantize_rows(x)
+    np.testing.assert_array_equal(bits32(out), bits32(O.ko_epilogue(O.ko_gemm_i8(qx, bt), sx, sb, None)))
