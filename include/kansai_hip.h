@@ -383,6 +383,17 @@ int kh_attention_ex(const float* qkv, int B, int T, int H, int dk, int causal, f
  * per-row (per-token) quantize of out needs (the row's absmax is the max of
  * its H words; kh_gemm_i8_qload_rows reads them). */
 int kh_attention_rows(const float* qkv, int B, int T, int H, int dk, int causal, float* out, unsigned* row_parts);
+/* Attention with the caller's additive mask, the reference's contract
+ * (nn.py:421-422: scores = q k^T / sqrt(dk) + mask, then softmax), with or
+ * without the causal mask on top.  mask: fp32, element (b, h, i, j) at
+ * b*stride_b + h*stride_h + i*stride_q + j (a stride 0 broadcasts that axis,
+ * e.g. the reference's [1, 1, T, T] causal mask: 0, 0, T; keys contiguous),
+ * mask_elems elements in all.  -inf entries give probability 0; a row masked
+ * everywhere gives NaN, as the reference's softmax does.  row_parts (may be
+ * NULL): kh_attention_rows' per-(row, head) partials. */
+int kh_attention_masked(const float* qkv, int B, int T, int H, int dk, int causal, const float* mask,
+                        int64_t mask_elems, int64_t stride_b, int64_t stride_h, int64_t stride_q, float* out,
+                        unsigned* row_parts);
 
 /* ---- measurement utility (no reference counterpart) ------------------- */
 

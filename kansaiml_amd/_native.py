@@ -86,6 +86,7 @@ _SIGNATURES = {
     "kh_layernorm_quant_rows": [_vp, _i64, _int, _vp, _vp, ctypes.c_float, _vp, _vp],
     "kh_attention_ex": [_vp, _int, _int, _int, _int, _int, _vp, _vp, _int, ctypes.POINTER(ctypes.c_int)],
     "kh_attention_rows": [_vp, _int, _int, _int, _int, _int, _vp, _vp],
+    "kh_attention_masked": [_vp, _int, _int, _int, _int, _int, _vp, _i64, _i64, _i64, _i64, _vp, _vp],
     "kh_linear_i8": [_vp, _i64, _i64, _vp, _i64, _vp, _int, _vp, _vp, _vp, _vp],
     "kh_linear_i8_noalloc": [_vp, _i64, _i64, _vp, _i64, _vp, _int, _vp, _vp],
     "kh_linear_i8_tensor": [_vp, _i64, _i64, _vp, _i64, _vp, _int, _vp, _vp, _vp, _vp],

@@ -537,6 +537,17 @@ constexpr int kDk = 64;
 constexpr int kAttQ = 64;  // queries per workgroup (16 per wave)
 constexpr int kAttK = 64;  // keys per LDS tile
 constexpr float kLog2eOver8 = 0.18033688011112042f;  // log2(e) / sqrt(64)
+constexpr float kLog2e = 1.4426950408889634f;
+
+// A caller's additive mask (nn.py:421-422: scores + mask, broadcast to
+// [batch, heads, query, key]): element strides of the batch, head and query
+// axes (0 where the axis broadcasts; keys contiguous), read through a buffer
+// resource of `bytes` (reads past it, for keys or queries past T, give 0).
+struct AttMask {
+    const float* m;
+    uint32_t bytes;
+    int sb, sh, sq;
+};
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
@@ -611,10 +622,10 @@ __device__ __forceinline__ void attention_pv(const float* vs, const f32x4v (&st)
     }
 }
 
-template <bool CAUSAL>
+template <bool CAUSAL, bool MASK = false>
 __global__ __launch_bounds__(256, 3) void attention_mfma_kernel(const float* __restrict__ qkv, int B, int T, int H,
                                                              float* __restrict__ out, unsigned* __restrict__ parts,
-                                                             unsigned* __restrict__ rparts) {
+                                                             unsigned* __restrict__ rparts, AttMask am) {
     __shared__ __attribute__((aligned(1024))) float ks[kAttK * kDk];
     __shared__ __attribute__((aligned(1024))) float vs[kAttK * kDk];
     using kh::pipe::wait_imm;
@@ -638,6 +649,9 @@ __global__ __launch_bounds__(256, 3) void attention_mfma_kernel(const float* __r
     const int row_bytes = 3 * D * 4;
     const __amdgpu_buffer_rsrc_t rsrc = kh::pipe::make_rsrc(bq, (uint32_t)(T * row_bytes));
     const int kcol = (D + h * kDk) * 4, vcol = kcol + D * 4;
+    // MASK: this lane's query row of the mask (in elements).
+    const __amdgpu_buffer_rsrc_t rmask = kh::pipe::make_rsrc(am.m, am.bytes);
+    const int mrow = b * am.sb + h * am.sh + q * am.sq;
 
     // Q operand: query q, d = 16g .. 16g+15, scaled by log2(e) / 8.
     float qf[16];
@@ -681,15 +695,32 @@ __global__ __launch_bounds__(256, 3) void attention_mfma_kernel(const float* __r
         else if (nt == 3) attention_scores<3>(ks, qf, li, g, st);
         else if (nt == 2) attention_scores<2>(ks, qf, li, g, st);
         else attention_scores<1>(ks, qf, li, g, st);
+        if constexpr (MASK) {
+            // The caller's mask, in the scores' base-2 units: keys
+            // 16t + 4g + e of the tile (register e ^ (g & 1), att_key's order).
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float mv = __uint_as_float(
+                        __builtin_amdgcn_raw_buffer_load_b32(rmask, (mrow + k0 + 16 * t + 4 * g + e) * 4, 0, 0));
+                    st[t][e ^ (g & 1)] += mv * kLog2e;
+                }
+        }
         // Causal mask (key > query) and keys past T -- only where the tile
-        // reaches this wave's diagonal or the sequence end.
+        // reaches this wave's diagonal or the sequence end.  Under a caller's
+        // mask these scores are -inf: a row whose every visible key the
+        // caller masked with -inf then has no real score, m stays at its
+        // -3e38 start, and -inf keeps their probabilities 0 (l = 0, a NaN
+        // row, as the reference's softmax of an all -inf row gives).
+        constexpr float kOff = MASK ? -__builtin_inff() : -3.0e38f;
         if (!((!CAUSAL || k0 + kAttK - 1 <= q0) && k0 + kAttK <= T)) {
 #pragma unroll
             for (int t = 0; t < 4; ++t)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int key = k0 + 16 * t + att_key(4 * g + r);
-                    st[t][r] = ((CAUSAL && key > q) || key >= T) ? -3.0e38f : st[t][r];
+                    st[t][r] = ((CAUSAL && key > q) || key >= T) ? kOff : st[t][r];
                 }
         }
         float mx = -3.0e38f;
@@ -919,7 +950,8 @@ int kh_gelu(const float* x, float* out, int64_t n) {
 }
 
 static int attention_impl(const float* qkv, int B, int T, int H, int dk, int causal, float* out,
-                          unsigned* absmax_parts, int max_parts, int* nparts, unsigned* row_parts) {
+                          unsigned* absmax_parts, int max_parts, int* nparts, unsigned* row_parts,
+                          const AttMask* mask = nullptr) {
     KH_REQUIRE(B > 0 && T > 0 && H > 0, "kh_attention: bad shape");
     KH_REQUIRE(dk == kDk, "kh_attention: only head dimension 64 is supported");
     KH_REQUIRE(causal == 0 || causal == 1, "kh_attention: causal must be 0 or 1");
@@ -939,12 +971,16 @@ static int attention_impl(const float* qkv, int B, int T, int H, int dk, int cau
     // 1/sqrt(d_k) = 1/8 for dk = 64 (the reference's binary64 Python float,
     // nn.py:413, is exactly representable in binary32); the kernel applies it
     // to Q together with log2(e), keeping the scores in base-2 units.
-    if (causal)
-        attention_mfma_kernel<true><<<(unsigned)blocks, 256, 0, d->stream>>>(qkv, B, T, H, out,
-                                                                          fused ? absmax_parts : nullptr, row_parts);
+    unsigned* pp = fused ? absmax_parts : nullptr;
+    const AttMask am = mask ? *mask : AttMask{nullptr, 0, 0, 0, 0};
+    if (mask && causal)
+        attention_mfma_kernel<true, true><<<(unsigned)blocks, 256, 0, d->stream>>>(qkv, B, T, H, out, pp, row_parts, am);
+    else if (mask)
+        attention_mfma_kernel<false, true><<<(unsigned)blocks, 256, 0, d->stream>>>(qkv, B, T, H, out, pp, row_parts, am);
+    else if (causal)
+        attention_mfma_kernel<true><<<(unsigned)blocks, 256, 0, d->stream>>>(qkv, B, T, H, out, pp, row_parts, am);
     else
-        attention_mfma_kernel<false><<<(unsigned)blocks, 256, 0, d->stream>>>(qkv, B, T, H, out,
-                                                                           fused ? absmax_parts : nullptr, row_parts);
+        attention_mfma_kernel<false><<<(unsigned)blocks, 256, 0, d->stream>>>(qkv, B, T, H, out, pp, row_parts, am);
     int rc = kh::launch_status("attention");
     if (rc || !absmax_parts) return rc;
     if (fused) {
@@ -962,6 +998,26 @@ int kh_attention_ex(const float* qkv, int B, int T, int H, int dk, int causal, f
 int kh_attention_rows(const float* qkv, int B, int T, int H, int dk, int causal, float* out, unsigned* row_parts) {
     KH_REQUIRE(row_parts, "kh_attention_rows: null row_parts");
     return attention_impl(qkv, B, T, H, dk, causal, out, nullptr, 0, nullptr, row_parts);
+}
+
+int kh_attention_masked(const float* qkv, int B, int T, int H, int dk, int causal, const float* mask,
+                        int64_t mask_elems, int64_t stride_b, int64_t stride_h, int64_t stride_q, float* out,
+                        unsigned* row_parts) {
+    KH_REQUIRE(mask && mask_elems > 0, "kh_attention_masked: null or empty mask");
+    KH_REQUIRE(kh::aligned(mask, 4), "kh_attention_masked: the mask must be 4-byte aligned");
+    KH_REQUIRE(stride_b >= 0 && stride_h >= 0 && stride_q >= 0, "kh_attention_masked: negative stride");
+    KH_REQUIRE(B > 0 && T > 0 && H > 0, "kh_attention: bad shape");
+    // The last element any (batch, head, query, key) reads must be inside
+    // the mask; every offset (up to a padded query's last key) a 32-bit
+    // byte offset.
+    const int64_t last = (B - 1) * stride_b + (H - 1) * stride_h + (T - 1) * stride_q + (T - 1);
+    KH_REQUIRE(last < mask_elems, "kh_attention_masked: the mask's strides reach past its elements");
+    const int64_t nq = (T + kAttQ - 1) / kAttQ;
+    const int64_t reach = (B - 1) * stride_b + (H - 1) * stride_h + (nq * kAttQ) * stride_q + nq * kAttQ + kAttK;
+    KH_REQUIRE(mask_elems * 4 <= 0x7FFFFFFFLL && reach * 4 <= 0x7FFFFFFFLL,
+               "kh_attention_masked: the mask must stay under 2 GiB of offsets");
+    const AttMask am{mask, (uint32_t)(mask_elems * 4), (int)stride_b, (int)stride_h, (int)stride_q};
+    return attention_impl(qkv, B, T, H, dk, causal, out, nullptr, 0, nullptr, row_parts, &am);
 }
 
 int kh_causal_attention_ex(const float* qkv, int B, int T, int H, int dk, float* out, unsigned* absmax_parts,

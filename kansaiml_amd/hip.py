@@ -440,10 +440,32 @@ def layer_norm(x: DeviceTensor, w: DeviceTensor, b: DeviceTensor, eps: float = 1
     return out, parts
 
 
+def mask_strides(mask: DeviceTensor, batch: int, heads: int, seq: int) -> tuple:
+    """Element strides (batch, head, query) of an additive attention mask
+    whose shape broadcasts to [batch, heads, seq, seq] (nn.py:421-422's
+    scores.add(mask)): right-aligned, each axis of size 1 or the full size,
+    the key axis full and contiguous.  A size-1 axis gets stride 0."""
+    _need(mask, "float32", None, "attention(mask)")
+    shape = list(mask.shape)
+    if not 1 <= len(shape) <= 4 or shape[-1] != seq:
+        raise RuntimeError(f"attention: mask {shape} does not broadcast to [{batch}, {heads}, {seq}, {seq}] with "
+                           f"its last axis the {seq} keys")
+    full = [batch, heads, seq, seq]
+    shape4 = [1] * (4 - len(shape)) + shape
+    strides, step = [0, 0, 0, 0], 1
+    for ax in (3, 2, 1, 0):
+        if shape4[ax] not in (1, full[ax]):
+            raise RuntimeError(f"attention: mask {shape} does not broadcast to {full}")
+        strides[ax] = step if shape4[ax] != 1 else 0
+        step *= shape4[ax]
+    return strides[0], strides[1], strides[2]
+
+
 def attention(qkv: DeviceTensor, batch: int, seq: int, heads: int, d_model: int, *, causal: bool = True,
-              absmax: bool = False):
-    """Multi-head attention core (nn.py:381-427), with the causal mask or none.
-    Returns (out, AbsmaxParts | None)."""
+              absmax: bool = False, mask: DeviceTensor | None = None):
+    """Multi-head attention core (nn.py:381-427), with the causal mask or none,
+    and optionally the caller's additive mask (broadcast to [batch, heads,
+    seq, seq]).  Returns (out, AbsmaxParts | None)."""
     _need(qkv, "float32", 2, "attention(qkv)")
     if heads <= 0 or d_model != heads * 64:
         raise RuntimeError(f"attention: d_model must be heads * 64 (the kernel's head size), got {d_model} "
@@ -452,6 +474,15 @@ def attention(qkv: DeviceTensor, batch: int, seq: int, heads: int, d_model: int,
         raise RuntimeError(f"attention: qkv must be [batch * seq, 3 * d_model] = [{batch * seq}, {3 * d_model}], "
                            f"got {qkv.shape}")
     out = DeviceTensor([batch * seq, d_model], "float32")
+    if mask is not None:
+        sb, sh, sq = mask_strides(mask, batch, heads, seq)
+        N.call("kh_attention_masked", qkv.ptr, batch, seq, heads, d_model // heads, int(bool(causal)), mask.ptr,
+               mask.numel(), sb, sh, sq, out.ptr, None)
+        parts = None
+        if absmax:
+            parts = AbsmaxParts()
+            N.call("kh_absmax_parts", out.ptr, out.numel(), parts.buf.ptr, ABSMAX_PARTS, ctypes.byref(parts._n))
+        return out, parts
     parts = AbsmaxParts() if absmax else None
     N.call("kh_attention_ex", qkv.ptr, batch, seq, heads, d_model // heads, int(bool(causal)), out.ptr,
            parts.buf.ptr if parts else None, ABSMAX_PARTS if parts else 0, ctypes.byref(parts._n) if parts else None)
@@ -471,7 +502,8 @@ class RowParts:
         self.buf.release()
 
 
-def attention_rows(qkv: DeviceTensor, batch: int, seq: int, heads: int, d_model: int, *, causal: bool = True):
+def attention_rows(qkv: DeviceTensor, batch: int, seq: int, heads: int, d_model: int, *, causal: bool = True,
+                   mask: DeviceTensor | None = None):
     """attention() also writing the max |out| bits of every (row, head).
     Returns (out, RowParts)."""
     _need(qkv, "float32", 2, "attention(qkv)")
@@ -483,6 +515,11 @@ def attention_rows(qkv: DeviceTensor, batch: int, seq: int, heads: int, d_model:
                            f"got {qkv.shape}")
     out = DeviceTensor([batch * seq, d_model], "float32")
     rp = RowParts(batch * seq, heads)
+    if mask is not None:
+        sb, sh, sq = mask_strides(mask, batch, heads, seq)
+        N.call("kh_attention_masked", qkv.ptr, batch, seq, heads, d_model // heads, int(bool(causal)), mask.ptr,
+               mask.numel(), sb, sh, sq, out.ptr, rp.buf.ptr)
+        return out, rp
     N.call("kh_attention_rows", qkv.ptr, batch, seq, heads, d_model // heads, int(bool(causal)), out.ptr, rp.buf.ptr)
     return out, rp
 

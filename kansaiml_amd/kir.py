@@ -185,13 +185,26 @@ class TraceValue:
     def gelu(self):
         return self._emit("gelu", [self], self.shape)
 
-    def attention(self, batch: int, seq: int, heads: int, causal: bool = True):
+    def attention(self, batch: int, seq: int, heads: int, causal: bool = True, mask=None):
         """self: fused Q|K|V projection [batch*seq, 3*D] -> [batch*seq, D];
         causal adds the mask that hides later keys, otherwise every query
-        attends over all seq keys of its sequence."""
+        attends over all seq keys of its sequence; `mask` (optional) is an
+        additive mask added to the scaled scores, broadcast to [batch, heads,
+        seq, seq] (nn.py:421-422)."""
         if len(self.shape) != 2 or self.shape[0] != batch * seq or self.shape[1] % (3 * heads):
             raise ValueError(f"attention: {self.shape} is not [batch*seq, 3*D] for {heads} heads")
-        return self._emit("attention", [self], [self.shape[0], self.shape[1] // 3], batch=batch, seq=seq,
+        ins = [self]
+        if mask is not None:
+            mask = self._coerce(mask)
+            try:
+                if mask.shape[-1] != seq:
+                    raise ValueError
+                _broadcast(mask.shape, [batch, heads, seq, seq], "attention(mask)")
+            except (ValueError, IndexError):
+                raise ValueError(f"attention: mask {mask.shape} does not broadcast to "
+                                 f"[{batch}, {heads}, {seq}, {seq}]") from None
+            ins.append(mask)
+        return self._emit("attention", ins, [self.shape[0], self.shape[1] // 3], batch=batch, seq=seq,
                           heads=heads, causal=bool(causal))
 
     def causal_attention(self, batch: int, seq: int, heads: int):
@@ -643,13 +656,14 @@ def _exec(node, vals):
         N.call("kh_gelu", ins[0].ptr, out.ptr, ins[0].numel())
         return out
     if op == "attention":
+        mask = ins[1] if len(ins) > 1 else None
         if node.attrs.get("row_absmax"):
             out, rp = H.attention_rows(ins[0], node.attrs["batch"], node.attrs["seq"], node.attrs["heads"],
-                                       node.shape[1], causal=node.attrs["causal"])
+                                       node.shape[1], causal=node.attrs["causal"], mask=mask)
             out.row_parts = rp
             return out
         out, parts = H.attention(ins[0], node.attrs["batch"], node.attrs["seq"], node.attrs["heads"], node.shape[1],
-                                 causal=node.attrs["causal"], absmax=bool(node.attrs.get("absmax")))
+                                 causal=node.attrs["causal"], absmax=bool(node.attrs.get("absmax")), mask=mask)
         return _with_parts(out, parts)
     if op == "tuple":
         return tuple(ins)

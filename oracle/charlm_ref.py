@@ -43,7 +43,9 @@ def gelu(x):
     return (x * (f32(0.5) * (f32(1.0) + erf(x * f32(0.70710678118654752440)).astype(f32)))).astype(f32)
 
 
-def attention(qkv, batch, seq, heads, causal=True):
+def attention(qkv, batch, seq, heads, causal=True, mask=None):
+    """mask (optional): additive, broadcast to [batch, heads, seq, seq] and
+    added to the scaled scores (nn.py:421-422), on top of the causal mask."""
     D = qkv.shape[1] // 3
     dk = D // heads
     q = qkv[:, :D].reshape(batch, seq, heads, dk).transpose(0, 2, 1, 3)
@@ -51,9 +53,11 @@ def attention(qkv, batch, seq, heads, causal=True):
     v = qkv[:, 2 * D:].reshape(batch, seq, heads, dk).transpose(0, 2, 1, 3)
     scale = f32(1.0 / math.sqrt(dk))
     s = (q @ k.transpose(0, 1, 3, 2)).astype(f32) * scale
+    if mask is not None:
+        s = (s + np.asarray(mask, s.dtype)).astype(s.dtype)
     if causal:
-        mask = np.where(np.arange(seq)[None, :] <= np.arange(seq)[:, None], f32(0.0), f32(-1e9))
-        s = (s + mask).astype(f32)
+        cm = np.where(np.arange(seq)[None, :] <= np.arange(seq)[:, None], f32(0.0), f32(-1e9))
+        s = (s + cm).astype(f32)
     s = s - s.max(axis=-1, keepdims=True)
     e = np.exp(s).astype(f32)
     p = (e / e.sum(axis=-1, keepdims=True, dtype=f32)).astype(f32)

@@ -60,13 +60,15 @@ def _gelu64(x):
     return np.vectorize(lambda v: v * 0.5 * (1.0 + math.erf(v / math.sqrt(2.0))))(np.asarray(x, f64))
 
 
-def _attn64(q, k, v, batch, seq, heads, causal=True):
+def _attn64(q, k, v, batch, seq, heads, causal=True, mask=None):
     """softmax(q k^T / sqrt(dk) + causal mask) v, one (batch, head, query) at a
     time; head h owns columns h*dk .. h*dk+dk-1 (a row-major reshape of
     d_model into (heads, dk), nn.py:393-402).  Unmasked: every query sees all
-    seq keys."""
+    seq keys.  mask: an additive mask broadcast to [batch, heads, seq, seq]
+    added to the scaled scores (nn.py:421-422)."""
     D = q.shape[1]
     dk = D // heads
+    mk = np.broadcast_to(np.asarray(mask, f64), (batch, heads, seq, seq)) if mask is not None else None
     out = np.zeros((batch * seq, D), f64)
     for b in range(batch):
         for h in range(heads):
@@ -75,6 +77,8 @@ def _attn64(q, k, v, batch, seq, heads, causal=True):
                 qi = q[b * seq + i, cols].astype(f64)
                 keys = i + 1 if causal else seq
                 s = [float(qi @ k[b * seq + j, cols].astype(f64)) / math.sqrt(dk) for j in range(keys)]
+                if mk is not None:
+                    s = [t + float(mk[b, h, i, j]) for j, t in enumerate(s)]
                 m = max(s)
                 e = [math.exp(t - m) for t in s]
                 tot = sum(e)
@@ -248,6 +252,53 @@ def test_unmasked_attention_vs_binary64_loops(batch, seq, heads, dk):
     # and the unmasked form is not the causal one
     if seq > 1:
         assert not np.allclose(got, R.causal_attention(qkv, batch, seq, heads), rtol=0, atol=2e-6)
+
+
+@pytest.mark.parametrize("mshape", [(7, 7), (2, 1, 7, 7), (1, 3, 7, 7), (2, 3, 7, 7), (2, 1, 1, 7)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_masked_attention_vs_binary64_loops(mshape, causal):
+    """The caller's additive mask (nn.py:421-422) in the restatement against
+    the binary64 loops, for every broadcast shape the kernel takes."""
+    batch, seq, heads, dk = 2, 7, 3, 8
+    D = heads * dk
+    qkv = _qkv(batch, seq, heads, dk, seed=77)
+    mask = (_gen(len(mshape) * 13 + sum(mshape)).standard_normal(mshape) * 2).astype(f32)
+    got = R.attention(qkv, batch, seq, heads, causal=causal, mask=mask)
+    want = _attn64(qkv[:, :D], qkv[:, D:2 * D], qkv[:, 2 * D:], batch, seq, heads, causal=causal, mask=mask)
+    np.testing.assert_allclose(got, want, rtol=0, atol=2e-6)
+    # a mask matters: the unmasked result differs
+    assert not np.allclose(got, R.attention(qkv, batch, seq, heads, causal=causal), rtol=0, atol=1e-4)
+
+
+def test_masked_attention_closed_forms():
+    """Zero mask = no mask; BigGPT's own [1, 1, T, T] -1e9 mask
+    (train_shakespeare_large.py:74-75) = the causal form; a -inf mask on key
+    j for every query = attention without key j; a constant added to a
+    query's whole mask row changes nothing (softmax shift invariance)."""
+    batch, seq, heads, dk = 2, 9, 3, 8
+    D = heads * dk
+    qkv = _qkv(batch, seq, heads, dk, seed=91)
+    plain = R.attention(qkv, batch, seq, heads, causal=False)
+    np.testing.assert_array_equal(R.attention(qkv, batch, seq, heads, causal=False,
+                                              mask=np.zeros((seq, seq), f32)), plain)
+    big = np.array([[0.0 if j <= i else -1e9 for j in range(seq)] for i in range(seq)], f32).reshape(1, 1, seq, seq)
+    np.testing.assert_array_equal(R.attention(qkv, batch, seq, heads, causal=False, mask=big),
+                                  R.causal_attention(qkv, batch, seq, heads))
+    j = 4
+    drop = np.zeros((1, 1, 1, seq), f32)
+    drop[..., j] = -np.inf
+    keep = [t for t in range(seq) if t != j]
+    q, k, v = qkv[:, :D], qkv[:, D:2 * D], qkv[:, 2 * D:]
+    got = R.attention(qkv, batch, seq, heads, causal=False, mask=drop)
+    for b in range(batch):
+        rows = [b * seq + t for t in keep]
+        sub = np.concatenate([q[rows], k[rows], v[rows]], axis=1)
+        want = _attn64(sub[:, :D], sub[:, D:2 * D], sub[:, 2 * D:], 1, seq - 1, heads, causal=False)
+        # queries other than j see the same keys; compare their rows
+        np.testing.assert_allclose(got[rows], want, rtol=0, atol=2e-6)
+    shift = (_gen(3).standard_normal((1, 1, seq, 1)) * 5).astype(f64)
+    np.testing.assert_allclose(R.attention(qkv, batch, seq, heads, causal=False, mask=shift),
+                               plain, rtol=0, atol=2e-6)
 
 
 def test_attention_closed_forms():

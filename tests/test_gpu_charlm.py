@@ -142,6 +142,153 @@ def test_attention(G, batch, seq, heads, causal):
     assert np.abs(out.numpy() - ref).max() < 2e-5
 
 
+MASK_SHAPES = {"TT": lambda b, h, t: (t, t), "B1TT": lambda b, h, t: (b, 1, t, t),
+               "1HTT": lambda b, h, t: (1, h, t, t), "BHTT": lambda b, h, t: (b, h, t, t),
+               "B11T": lambda b, h, t: (b, 1, 1, t)}
+
+
+def _mask(gen, kind, batch, heads, seq):
+    """A random additive mask of the named broadcast shape; the [B,1,1,T]
+    kind is a key-padding mask (0, or -inf on each sequence's last keys,
+    never key 0)."""
+    shape = MASK_SHAPES[kind](batch, heads, seq)
+    if kind == "B11T":
+        m = np.zeros(shape, np.float32)
+        for b in range(batch):
+            pad = int(gen.integers(0, seq))  # 0 .. seq-1 padded keys
+            m[b, 0, 0, seq - pad:] = -np.inf
+        return m
+    return (gen.standard_normal(shape) * 2).astype(np.float32)
+
+
+@pytest.mark.parametrize("batch,seq,heads", [(2, 5, 3), (2, 100, 2), (1, 130, 2), (3, 64, 2)])
+@pytest.mark.parametrize("kind", list(MASK_SHAPES))
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_additive_mask(G, batch, seq, heads, kind, causal):
+    """scores.add(mask) before the softmax (nn.py:421-422) for every way a
+    mask broadcasts to [batch, heads, seq, seq], with the causal mask on top
+    or not, against the restatement; the per-(row, head) output maxima the
+    masked kernel writes for a following per-token quantize are exact."""
+    from kansaiml_amd import hip as H
+    N, D = G
+    gen = np.random.Generator(np.random.PCG64(batch * 7919 + seq * 31 + heads))
+    dm = heads * 64
+    qkv = (gen.standard_normal((batch * seq, 3 * dm)) * 1.5).astype(np.float32)
+    m = _mask(gen, kind, batch, heads, seq)
+    print(f"masked attention {kind} {m.shape} batch={batch} seq={seq} heads={heads} causal={causal}", flush=True)
+    qd, md = D.from_host(qkv), D.from_host(m)
+    out, _ = H.attention(qd, batch, seq, heads, dm, causal=causal, mask=md)
+    got = out.numpy()
+    ref = R.attention(qkv.astype(np.float64), batch, seq, heads, causal=causal, mask=m.astype(np.float64))
+    assert np.isfinite(ref).all()
+    assert np.abs(got - ref).max() < 3e-5
+    out2, rp = H.attention_rows(qd, batch, seq, heads, dm, causal=causal, mask=md)
+    N.synchronize()
+    np.testing.assert_array_equal(out2.numpy().view(np.uint32), got.view(np.uint32))
+    want = np.abs(got).reshape(batch * seq, heads, 64).max(axis=2).view(np.uint32)
+    np.testing.assert_array_equal(rp.buf.numpy().view(np.uint32).reshape(-1)[:batch * seq * heads],
+                                  want.reshape(-1))
+
+
+@pytest.mark.parametrize("batch,seq,heads", [(2, 100, 2), (1, 256, 6)])
+def test_attention_zero_mask_and_reference_causal_mask(G, batch, seq, heads):
+    """A zero mask changes nothing (bit-exact against the unmasked kernel,
+    causal or not), and the reference model's own causal mask (a [1, 1, T, T]
+    tensor, 0 on and below the diagonal, -1e9 above) without the causal flag
+    gives the causal kernel's output bit for bit: every masked probability
+    is exactly 0 either way."""
+    from kansaiml_amd import hip as H
+    N, D = G
+    gen = np.random.Generator(np.random.PCG64(seq + heads))
+    dm = heads * 64
+    qd = D.from_host((gen.standard_normal((batch * seq, 3 * dm)) * 1.5).astype(np.float32))
+    zero = D.from_host(np.zeros((seq, seq), np.float32))
+    for causal in (True, False):
+        plain, _ = H.attention(qd, batch, seq, heads, dm, causal=causal)
+        masked, _ = H.attention(qd, batch, seq, heads, dm, causal=causal, mask=zero)
+        np.testing.assert_array_equal(masked.numpy().view(np.uint32), plain.numpy().view(np.uint32))
+    tri = np.where(np.arange(seq)[None, :] <= np.arange(seq)[:, None], 0.0, -1e9).astype(np.float32)
+    causal_out, _ = H.attention(qd, batch, seq, heads, dm, causal=True)
+    ref_mask, _ = H.attention(qd, batch, seq, heads, dm, causal=False, mask=D.from_host(tri[None, None]))
+    np.testing.assert_array_equal(ref_mask.numpy().view(np.uint32), causal_out.numpy().view(np.uint32))
+
+
+def test_attention_fully_masked_row_is_nan(G):
+    """A query whose every visible key the mask sets to -inf has no score
+    left: NaN, as the reference states for a literal -inf mask that masks a
+    whole row (nn.py:355-360; its softmax, Tensor.cpp:906-913, takes -inf -
+    -inf).  The causal flag excludes later keys exactly, so under it a row
+    whose keys up to the query are all -inf is NaN too (the restatement's
+    additive -1e9 there leaves scores s - 1e9, which keep nothing of s in
+    binary32: an artifact of rounding, not compared).  Every other row
+    matches the restatement."""
+    from kansaiml_amd import hip as H
+    N, D = G
+    batch, seq, heads = 1, 70, 2
+    gen = np.random.Generator(np.random.PCG64(70))
+    qkv = (gen.standard_normal((seq, 3 * 128))).astype(np.float32)
+    m = np.zeros((seq, seq), np.float32)
+    m[3, :] = -np.inf     # query 3 sees nothing
+    m[66, :67] = -np.inf  # query 66: keys 0..66 masked; only keys 67..69 (later ones) left
+    for causal in (True, False):
+        out, _ = H.attention(D.from_host(qkv), batch, seq, heads, 128, causal=causal, mask=D.from_host(m))
+        got = out.numpy()
+        with np.errstate(invalid="ignore"):
+            ref = R.attention(qkv.astype(np.float64), batch, seq, heads, causal=causal, mask=m.astype(np.float64))
+        nan_rows = [3, 66] if causal else [3]
+        assert np.isnan(got[nan_rows]).all() and np.isnan(ref[3]).all()
+        ok = np.ones(seq, bool)
+        ok[nan_rows] = False
+        assert not np.isnan(got[ok]).any()
+        assert np.abs(got[ok] - ref[ok]).max() < 2e-5
+
+
+def test_attention_mask_shapes_rejected(G):
+    from kansaiml_amd import hip as H
+    N, D = G
+    qd = D.from_host(np.zeros((2 * 8, 3 * 128), np.float32))
+    for bad in [(8, 7), (3, 1, 8, 8), (1, 3, 8, 8), (2, 2, 2, 8, 8), (8, 8, 8)]:
+        with pytest.raises(RuntimeError, match="broadcast"):
+            H.attention(qd, 2, 8, 2, 128, mask=D.from_host(np.zeros(bad, np.float32)))
+    with pytest.raises(TypeError, match="float32"):
+        H.attention(qd, 2, 8, 2, 128, mask=D.from_host(np.zeros((8, 8), np.float64)))
+
+
+def test_attention_mask_traced_and_fused(G):
+    """A traced model with a mask constant: attention(mask) -> per-token
+    QLinear.  run_hip's unfused graph matches the eager masked kernel and
+    the oracle's int8 Linear of its output bit for bit; quant_fusion's
+    (masked attention writing row maxima -> quantize-on-load GEMM) gives the
+    same bits."""
+    from kansaiml_amd import hip as H
+    from kansaiml_amd import kir
+    from kansaiml_amd import quantize as Q
+    from oracle import oracle as O
+    N, D = G
+    batch, seq, heads = 2, 96, 3
+    dm = heads * 64
+    gen = np.random.Generator(np.random.PCG64(96))
+    qkv = (gen.standard_normal((batch * seq, 3 * dm)) * 1.5).astype(np.float32)
+    m = _mask(gen, "B11T", batch, heads, seq)
+    w = (gen.standard_normal((dm, 256)) * 0.05).astype(np.float32)
+    b = gen.standard_normal(256).astype(np.float32)
+
+    class Lin:
+        weight, bias = w, b
+
+    proj = Q.QLinear(Lin(), mode="int8", act_granularity="row", weight_granularity="col")
+    g = kir.trace(lambda x: proj(x.attention(batch, seq, heads, causal=True, mask=m)), qkv)
+    f = kir.quant_fusion(g, qload=True)
+    att = [n for n in f.nodes if n.op == "attention"]
+    assert len(att) == 1 and att[0].attrs.get("row_absmax"), "the masked attention did not take the row partials"
+    unfused = kir.run_hip(g, qkv)
+    fused = kir.run_hip(f, qkv)
+    eager, _ = H.attention(D.from_host(qkv), batch, seq, heads, dm, causal=True, mask=D.from_host(m))
+    want = O.int8_linear(eager.numpy(), w, b, x_gran="row", w_gran="col")[0]
+    np.testing.assert_array_equal(np.asarray(unfused, np.float32).view(np.uint32), want.view(np.uint32))
+    np.testing.assert_array_equal(np.asarray(fused, np.float32).view(np.uint32), want.view(np.uint32))
+
+
 def _host(v):
     """Host copy of a node value: arrays, or (codes, scales) for a QTensor
     (packed codes in their [out, in] storage order)."""
