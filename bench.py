@@ -731,18 +731,32 @@ def _summarize_trace(root):
     trace = _find(os.path.join(root, "trace"), "kernel_trace.csv")
     durs = {}
     for r in (_read_csv(trace) if trace else []):
-        durs.setdefault(r["Kernel_Name"], []).append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+        durs.setdefault(r["Kernel_Name"], []).append((int(r["Start_Timestamp"]),
+                                                      int(r["End_Timestamp"]) - int(r["Start_Timestamp"])))
+    # The trace run times each leg over the bench's default 50 steps after
+    # its warm-up: for a kernel that only its leg launches (the C3a GEMM),
+    # its last 50 dispatches are the timed ones.
+    steps = 50
+
+    def timed(name):
+        d = [t for _, t in sorted(durs[name])][-steps:]
+        return f"{float(np.mean(d)) / 1e3:.2f}"
+
     rows = [(f"`{_short(r['Name'])[:90]}`", r["Calls"], f"{float(r['AverageNs']) / 1e3:.2f}",
-             f"{float(np.median(durs[r['Name']])) / 1e3:.2f}" if r["Name"] in durs else "",
+             f"{float(np.median([t for _, t in durs[r['Name']]])) / 1e3:.2f}" if r["Name"] in durs else "",
+             timed(r["Name"]) if r["Name"] in durs else "",
              f"{float(r['MinNs']) / 1e3:.2f}", f"{float(r['MaxNs']) / 1e3:.2f}", f"{float(r['Percentage']):.1f}")
             for r in _read_csv(stats)]
     _write_profile("bench_kernels_mi355x.md", "Kernel trace of `bench.py` on one MI355X (gfx950)",
                    [profile_command("trace")],
                    "Every bench leg (`run_kernel_stats.csv`, medians from `run_kernel_trace.csv`); durations include "
                    "the profiler's per-dispatch timestamps. The average counts each leg's warm-up launches (this "
-                   "run warms each leg for 10 ms, while the shader clock is still ramping), so the median is the "
-                   "figure to set beside the bench line's timed steps.\n\n"
-                   + _md_table(["kernel", "calls", "avg us", "median us", "min us", "max us", "% time"], rows))
+                   "run warms each leg for at least 50 ms, the first of them while the shader clock is still "
+                   f"ramping); the median, and the average of a kernel's last {steps} dispatches (the leg's timed "
+                   "steps, for a kernel only one leg launches, such as the C3a GEMM), are the figures to set "
+                   "beside the bench line.\n\n"
+                   + _md_table(["kernel", "calls", "avg us", "median us", f"avg of last {steps} us", "min us",
+                                "max us", "% time"], rows))
 
 
 def _summarize_traffic(root, traffic):
