@@ -528,7 +528,7 @@ def bench_c4(steps, warmup):
     # partials), fc1's output by the per-row quantize
     ms_row = None  # a profiled run traces the configured (per-tensor) forward only
     if GRAPH_TIMING:
-        gr = CharLM(w, act_granularity="row", qload=True).capture(64, 256)
+        gr = CharLM(w, act_granularity="row").capture(64, 256)
         ms_row = time_kernel(lambda: gr(ids, to_host=False), steps, warmup, tag="c4_graph_per_token")
         gr.close()
     ops = int8_linear_ops(w, 64, 256)

@@ -323,7 +323,11 @@ def _check_node(node, got, ins):
         np.testing.assert_array_equal(got[0], q.reshape(got[0].shape))
         assert got[1][0] == s
     elif op == "int8_linear":
-        if node.attrs.get("qload"):
+        if node.attrs.get("qload") and node.attrs.get("rows"):
+            # the activation's per-row quantize ran inside the GEMM
+            q, s = O.ko_quantize_rows(ins[0])
+            ins = [(q, s)] + list(ins[1:])
+        elif node.attrs.get("qload"):
             # the activation's per-tensor quantize ran inside the GEMM: the
             # oracle's quantize of the same fp32 input
             q, s = O.ko_quantize_tensor(ins[0])
