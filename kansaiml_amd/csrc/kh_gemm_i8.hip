@@ -1157,7 +1157,8 @@ int launch_skinny(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, in
 // fragments read from LDS, then applying the epilogue of the other kernels
 // (epilogue_finish: the same binary64 dequantize, bias, activation and
 // residual).  Bound: the A and output bytes, M K + 4 M N (C4's head: 8.47 ->
-// 7.36 us against the 128 x 128 ping-pong tiles, graph-replayed).  LDS rows
+// 7.36 us against the 128 x 128 ping-pong tiles, graph-replayed; 6.44 us with
+// every load unconditional and the weight's requested first).  LDS rows
 // are K + 16 bytes apart, so the 16 rows of a fragment read fall on distinct
 // banks.  Non-temporal output stores measured slower (7.93 us).
 // ---------------------------------------------------------------------------
@@ -1184,25 +1185,25 @@ __global__ __launch_bounds__(256 * kNarrowWN) void gemm_i8_narrow_kernel(const i
     constexpr int NTW = (NT + kNarrowWN - 1) / kNarrowWN;  // column tiles per wave
     const int m0 = blockIdx.x * kNarrowRows + (wave % 4) * 16;
     const int t0 = (wave / 4) * NTW;
-    // Every load before any is used: the A fragments of all k-steps (rows >=
-    // M read zero: buffer bound), the thread's chunks of the weight (rows >= N
-    // read zero), the epilogue's column and row operands.
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, (uint32_t)M * (uint32_t)K);
-    const int a_off = (m0 + (lane & 15)) * K + (lane >> 4) * 16;
-    i32x4v a[kNarrowMaxK / 64];
-#pragma unroll
-    for (int s = 0; s < kNarrowMaxK / 64; ++s)
-        if (s < ks) a[s] = __builtin_amdgcn_raw_buffer_load_b128(ra, a_off, 64 * s, 0);
+    // Every load before any is used, in the order they are needed (loads
+    // return in issue order): the thread's chunks of the weight (rows >= N
+    // read zero: buffer bound; L2-resident and staged into LDS first), the
+    // epilogue's column and row operands, then the A fragments of all
+    // k-steps (rows >= M read zero).  Every load is unconditional -- a chunk
+    // or k-step past the end re-reads the last one (a cache hit, never used,
+    // or stored again to the same LDS slot with the same bytes): loads under
+    // a condition made the compiler wait for each one where the branches
+    // join, one memory round trip per k-step.
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(B, (uint32_t)N * (uint32_t)K);
     const int chunks = 16 * NT * kc16;
     i32x4v bv[kMaxChunks];
+    int bdst[kMaxChunks];
 #pragma unroll
     for (int u = 0; u < kMaxChunks; ++u) {
-        const int c = tid + 256 * kNarrowWN * u;
-        if (c < chunks) {
-            const int n = c / kc16;
-            bv[u] = __builtin_amdgcn_raw_buffer_load_b128(rb, n * K + (c - n * kc16) * 16, 0, 0);
-        }
+        const int c = min(tid + 256 * kNarrowWN * u, chunks - 1);
+        const int n = c / kc16, kc = c - n * kc16;
+        bv[u] = __builtin_amdgcn_raw_buffer_load_b128(rb, n * K + kc * 16, 0, 0);
+        bdst[u] = n * ldb + kc * 16;
     }
     double sbj[NT];
     float bj[NT];
@@ -1217,14 +1218,15 @@ __global__ __launch_bounds__(256 * kNarrowWN) void gemm_i8_narrow_kernel(const i
 #pragma unroll
     for (int r = 0; r < 4; ++r)
         sai[r] = ep.out ? ep.sa[ep.sa_per_row ? min(m0 + 4 * (lane >> 4) + r, M - 1) : 0] : 0.0;
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, (uint32_t)M * (uint32_t)K);
+    const int a_off = (m0 + (lane & 15)) * K + (lane >> 4) * 16;
+    i32x4v a[kNarrowMaxK / 64];
 #pragma unroll
-    for (int u = 0; u < kMaxChunks; ++u) {
-        const int c = tid + 256 * kNarrowWN * u;
-        if (c < chunks) {
-            const int n = c / kc16;
-            *reinterpret_cast<i32x4v*>(bs + n * ldb + (c - n * kc16) * 16) = bv[u];
-        }
-    }
+    for (int s = 0; s < kNarrowMaxK / 64; ++s)
+        a[s] = __builtin_amdgcn_raw_buffer_load_b128(ra, a_off, 64 * min(s, ks - 1), 0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < kMaxChunks; ++u) *reinterpret_cast<i32x4v*>(bs + bdst[u]) = bv[u];
     __syncthreads();
     i32x4v acc[NTW];
 #pragma unroll
