@@ -60,7 +60,11 @@ __global__ __launch_bounds__(256) void quant_rows_reg_kernel(const float* __rest
     constexpr int ROWS_PER_BLOCK = 256 / ROW_THREADS;
     __shared__ unsigned red[4];
     const int lt = threadIdx.x % ROW_THREADS;
-    const int sub = threadIdx.x / ROW_THREADS;
+    // A wave lies within one row's threads: the row, and so each row's
+    // buffer resource, is wave-uniform.  Said explicitly, the resources live
+    // in scalar registers; derived from threadIdx.x they were vector values,
+    // and every store became a loop over the lanes' distinct resources.
+    const int sub = __builtin_amdgcn_readfirstlane((int)threadIdx.x / ROW_THREADS);
     const int64_t row = (int64_t)blockIdx.x * ROWS_PER_BLOCK + sub;
     const bool active = row < rows;
     // An inactive slot (past the last row) gets an empty resource: loads read 0.
