@@ -384,23 +384,35 @@ __device__ __forceinline__ f32x4 deq4(unsigned w, double s) {
 // Codes load through the cache normally; the fp32 output is written with
 // nontemporal stores (measured fastest of the four load/store policy pairs).
 // Requires cols % 4 == 0, q 4-byte and out 16-byte aligned.
+// STEPS of 1024 codes per block: 4 for rows of more than 3072 codes, fewer
+// for shorter rows, so that a block issues no steps past its row's end.
 constexpr int kDeqSteps = 4;
+typedef int i32x4raw __attribute__((ext_vector_type(4)));  // a 16-byte buffer store's data
 constexpr int kDeqPerBlock = 256 * 4 * kDeqSteps;
 
+template <int STEPS>
 __global__ __launch_bounds__(256) void dequant_vec_kernel(const int8_t* __restrict__ q, int64_t cols,
                                                           const double* __restrict__ scales, int per_row,
                                                           float* __restrict__ out) {
     const int64_t row = blockIdx.y;
     const double s = scales[per_row ? row : 0];
-    const int64_t c4 = cols >> 2;
-    const unsigned* qr = reinterpret_cast<const unsigned*>(q + row * cols);
-    f32x4* orow = reinterpret_cast<f32x4*>(out + row * cols);
-    const int64_t base = (int64_t)blockIdx.x * (kDeqPerBlock / 4) + threadIdx.x;
+    // The block's span of the row, as buffer resources: every step's load is
+    // issued before the first conversion (loads past the row's end read 0,
+    // stores past it are dropped).  With a bounds test around each step the
+    // compiler waited for each load before issuing the next.
+    constexpr int kPerBlock = 1024 * STEPS;
+    const int64_t c0 = (int64_t)blockIdx.x * kPerBlock;
+    const int span = (int)min((int64_t)kPerBlock, cols - c0);
+    const __amdgpu_buffer_rsrc_t rq = row_rsrc(q + row * cols + c0, span);
+    const __amdgpu_buffer_rsrc_t ro = row_rsrc(out + row * cols + c0, (int64_t)span * 4);
+    unsigned w[STEPS];
 #pragma unroll
-    for (int step = 0; step < kDeqSteps; ++step) {
-        const int64_t i = base + step * 256;
-        if (i < c4) __builtin_nontemporal_store(deq4(qr[i], s), orow + i);
-    }
+    for (int step = 0; step < STEPS; ++step)
+        w[step] = __builtin_amdgcn_raw_buffer_load_b32(rq, threadIdx.x * 4, step * 1024, 0);
+#pragma unroll
+    for (int step = 0; step < STEPS; ++step)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4raw, deq4(w[step], s)), ro, threadIdx.x * 16,
+                                               step * 4096, kCacheNontemporal);
 }
 
 // Any shape / alignment.
@@ -616,18 +628,19 @@ static int dequant(const int8_t* q, int64_t rows, int64_t cols, const double* sc
     KH_DEVICE_OR_RETURN(d);
     const bool vec = (cols % 4 == 0) && kh::aligned(q, 4) && kh::aligned(out, 16);
     if (vec && rows <= 0x7FFFFFFFLL && (cols + kDeqPerBlock - 1) / kDeqPerBlock <= 0x7FFFFFFFLL) {
-        dim3 g((unsigned)((cols + kDeqPerBlock - 1) / kDeqPerBlock), (unsigned)rows);
-        if (rows > 65535) {
-            // grid.y is limited to 65535: walk the rows in slabs.
-            for (int64_t r0 = 0; r0 < rows; r0 += 65535) {
-                const int64_t nr = min((int64_t)65535, rows - r0);
-                dim3 gs(g.x, (unsigned)nr);
-                dequant_vec_kernel<<<gs, 256, 0, d->stream>>>(q + r0 * cols, cols, scales + (per_row ? r0 : 0),
-                                                            per_row ? 1 : 0, out + r0 * cols);
-            }
-        } else {
-            dequant_vec_kernel<<<g, 256, 0, d->stream>>>(q, cols, scales, per_row ? 1 : 0, out);
-        }
+        const int steps = cols > 3072 ? 4 : (int)((cols + 1023) / 1024);
+        const unsigned gx = (unsigned)((cols + 1024 * steps - 1) / (1024 * steps));
+        auto go = [&](const int8_t* qq, const double* ss, float* oo, unsigned nr) {
+            const dim3 g(gx, nr);
+            const int pr = per_row ? 1 : 0;
+            if (steps == 4) dequant_vec_kernel<4><<<g, 256, 0, d->stream>>>(qq, cols, ss, pr, oo);
+            else if (steps == 3) dequant_vec_kernel<3><<<g, 256, 0, d->stream>>>(qq, cols, ss, pr, oo);
+            else if (steps == 2) dequant_vec_kernel<2><<<g, 256, 0, d->stream>>>(qq, cols, ss, pr, oo);
+            else dequant_vec_kernel<1><<<g, 256, 0, d->stream>>>(qq, cols, ss, pr, oo);
+        };
+        // grid.y is limited to 65535: walk the rows in slabs.
+        for (int64_t r0 = 0; r0 < rows; r0 += 65535)
+            go(q + r0 * cols, scales + (per_row ? r0 : 0), out + r0 * cols, (unsigned)min((int64_t)65535, rows - r0));
     } else {
         const int64_t n = rows * cols;
         const int g = grid_for(n, 16, 16384);
