@@ -563,10 +563,19 @@ int kh_quantize_rows(const float* x, int64_t rows, int64_t cols, int8_t* q, doub
     const bool vec = (cols % 4 == 0) && kh::aligned(x, 16) && kh::aligned(q, 4);
     const unsigned per_row = (unsigned)rows;
     const unsigned four_rows = (unsigned)((rows + 3) / 4);
+    const unsigned two_rows = (unsigned)((rows + 1) / 2);
+    // The smallest row slot (threads x float4 per thread) that holds the row:
+    // slots past the row's end still cost their loads' issue.
     if (vec && cols <= 256)
         quant_rows_reg_kernel<1, 1><<<four_rows, 256, 0, d->stream>>>(x, q, scales, rows, cols, d->fault);
+    else if (vec && cols <= 512)
+        quant_rows_reg_kernel<1, 2><<<four_rows, 256, 0, d->stream>>>(x, q, scales, rows, cols, d->fault);
     else if (vec && cols <= 1024)
         quant_rows_reg_kernel<1, 4><<<four_rows, 256, 0, d->stream>>>(x, q, scales, rows, cols, d->fault);
+    else if (vec && cols <= 1536)
+        quant_rows_reg_kernel<2, 3><<<two_rows, 256, 0, d->stream>>>(x, q, scales, rows, cols, d->fault);
+    else if (vec && cols <= 2048)
+        quant_rows_reg_kernel<2, 4><<<two_rows, 256, 0, d->stream>>>(x, q, scales, rows, cols, d->fault);
     else if (vec && cols <= 4096)
         quant_rows_reg_kernel<4, 4><<<per_row, 256, 0, d->stream>>>(x, q, scales, rows, cols, d->fault);
     else if (vec && cols <= 16384)

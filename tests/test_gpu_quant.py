@@ -74,7 +74,8 @@ def _outlier_matrix(rows, cols, seed, frac=0.001):
 # cols <= 256, 1024, 4096, 16384, 32768 (multiples of 4) and the two-pass
 # kernel for cols % 4 != 0 and cols > 32768.
 @pytest.mark.parametrize("rows,cols", [(7, 8), (33, 256), (9, 1000), (64, 1024), (5, 3000), (16, 4096),
-                                       (3, 16384), (2, 32768), (2, 40000), (11, 33), (4, 4099)])
+                                       (3, 16384), (2, 32768), (2, 40000), (11, 33), (4, 4099),
+                                       (5, 384), (6, 512), (7, 1536), (3, 1028), (9, 2048), (1, 1200)])
 def test_quantize_rows_vs_oracle(hip, rows, cols):
     H, D = hip
     x = _outlier_matrix(rows, cols, seed=rows * 7919 + cols)
