@@ -197,9 +197,9 @@ class TraceValue:
         if mask is not None:
             mask = self._coerce(mask)
             try:
-                if mask.shape[-1] != seq:
+                if mask.shape[-1] != seq or _broadcast(mask.shape, [batch, heads, seq, seq],
+                                                       "attention(mask)") != [batch, heads, seq, seq]:
                     raise ValueError
-                _broadcast(mask.shape, [batch, heads, seq, seq], "attention(mask)")
             except (ValueError, IndexError):
                 raise ValueError(f"attention: mask {mask.shape} does not broadcast to "
                                  f"[{batch}, {heads}, {seq}, {seq}]") from None

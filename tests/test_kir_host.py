@@ -239,6 +239,36 @@ def test_quantize_fuses_into_its_int8_linear_with_qload():
     assert sum(n.op == "quantize" for n in f2.nodes if n.attrs.get("granularity") == "row") == 1
 
 
+def test_masked_attention_trace_and_row_qload_fusion():
+    """attention(mask=...) records the additive mask as its second input for
+    every shape that broadcasts to [batch, heads, seq, seq] (nn.py:421-422),
+    rejects the rest, and a per-row quantize of its output fused into the
+    next int8 Linear (qload) makes the masked attention write row maxima."""
+    batch, seq, heads, d = 2, 8, 2, 128
+    qkv = np.zeros((batch * seq, 3 * d), np.float32)
+    w = np.zeros((d, 16), np.float32)
+
+    def model(mask):
+        def fn(x):
+            a = x.attention(batch, seq, heads, causal=True, mask=mask)
+            return a.quantize("row").int8_matmul(x._coerce(w).quantize()).dequantize()
+        return fn
+
+    for shape in [(seq,), (seq, seq), (batch, 1, seq, seq), (1, heads, seq, seq), (batch, heads, seq, seq),
+                  (batch, 1, 1, seq)]:
+        g = kir.trace(model(np.zeros(shape, np.float32)), qkv)
+        att = next(n for n in g.nodes if n.op == "attention")
+        assert len(att.inputs) == 2 and g.nodes[att.inputs[1]].op == "constant"
+        assert list(g.nodes[att.inputs[1]].shape) == list(shape)
+        f = kir.quant_fusion(g, qload=True)
+        assert next(n for n in f.nodes if n.op == "attention").attrs.get("row_absmax")
+        lin = [n for n in f.nodes if n.op == "int8_linear"]
+        assert len(lin) == 1 and lin[0].attrs.get("qload") and lin[0].attrs.get("rows")
+    for bad in [(seq, seq + 1), (3, 1, seq, seq), (1, 3, seq, seq), (2, batch, heads, seq, seq), (seq + 1,)]:
+        with pytest.raises(ValueError, match="broadcast"):
+            kir.trace(model(np.zeros(bad, np.float32)), qkv)
+
+
 @pytest.mark.parametrize("values,shape", [([1.0, 2.0, 3.0], [2, 2]), ([], [1]), ([1.0], [-1]), ([1.0, 2.0], [1])])
 def test_from_flat_length_mismatch_raises(values, shape):
     """kansai.from_flat throws runtime_error("from_flat: data length does not
