@@ -1006,13 +1006,21 @@ int kh_attention_masked(const float* qkv, int B, int T, int H, int dk, int causa
     KH_REQUIRE(mask && mask_elems > 0, "kh_attention_masked: null or empty mask");
     KH_REQUIRE(kh::aligned(mask, 4), "kh_attention_masked: the mask must be 4-byte aligned");
     KH_REQUIRE(stride_b >= 0 && stride_h >= 0 && stride_q >= 0, "kh_attention_masked: negative stride");
+    KH_REQUIRE(mask_elems <= 0x7FFFFFFFLL / 4 && stride_b <= 0x7FFFFFFFLL && stride_h <= 0x7FFFFFFFLL &&
+                   stride_q <= 0x7FFFFFFFLL,
+               "kh_attention_masked: the mask must stay under 2 GiB of offsets");
     KH_REQUIRE(B > 0 && T > 0 && H > 0, "kh_attention: bad shape");
     // The last element any (batch, head, query, key) reads must be inside
     // the mask; every offset (up to a padded query's last key) a 32-bit
     // byte offset.
+    // (Bounded in binary64 first: the int64 sums below cannot overflow once
+    // it is under the mask's size.)
+    const int64_t nq = (T + kAttQ - 1) / kAttQ;
+    KH_REQUIRE((double)(B - 1) * stride_b + (double)(H - 1) * stride_h + (double)(nq * kAttQ) * stride_q +
+                       (double)(nq * kAttQ + kAttK) <= (double)(0x7FFFFFFFLL / 4),
+               "kh_attention_masked: the mask must stay under 2 GiB of offsets");
     const int64_t last = (B - 1) * stride_b + (H - 1) * stride_h + (T - 1) * stride_q + (T - 1);
     KH_REQUIRE(last < mask_elems, "kh_attention_masked: the mask's strides reach past its elements");
-    const int64_t nq = (T + kAttQ - 1) / kAttQ;
     const int64_t reach = (B - 1) * stride_b + (H - 1) * stride_h + (nq * kAttQ) * stride_q + nq * kAttQ + kAttK;
     KH_REQUIRE(mask_elems * 4 <= 0x7FFFFFFFLL && reach * 4 <= 0x7FFFFFFFLL,
                "kh_attention_masked: the mask must stay under 2 GiB of offsets");

@@ -473,9 +473,10 @@ def attention(qkv: DeviceTensor, batch: int, seq: int, heads: int, d_model: int,
     if batch < 0 or seq < 0 or list(qkv.shape) != [batch * seq, 3 * d_model]:
         raise RuntimeError(f"attention: qkv must be [batch * seq, 3 * d_model] = [{batch * seq}, {3 * d_model}], "
                            f"got {qkv.shape}")
+    strides = mask_strides(mask, batch, heads, seq) if mask is not None else None  # checked before allocating
     out = DeviceTensor([batch * seq, d_model], "float32")
     if mask is not None:
-        sb, sh, sq = mask_strides(mask, batch, heads, seq)
+        sb, sh, sq = strides
         N.call("kh_attention_masked", qkv.ptr, batch, seq, heads, d_model // heads, int(bool(causal)), mask.ptr,
                mask.numel(), sb, sh, sq, out.ptr, None)
         parts = None
@@ -513,10 +514,11 @@ def attention_rows(qkv: DeviceTensor, batch: int, seq: int, heads: int, d_model:
     if batch < 0 or seq < 0 or list(qkv.shape) != [batch * seq, 3 * d_model]:
         raise RuntimeError(f"attention: qkv must be [batch * seq, 3 * d_model] = [{batch * seq}, {3 * d_model}], "
                            f"got {qkv.shape}")
+    strides = mask_strides(mask, batch, heads, seq) if mask is not None else None  # checked before allocating
     out = DeviceTensor([batch * seq, d_model], "float32")
     rp = RowParts(batch * seq, heads)
     if mask is not None:
-        sb, sh, sq = mask_strides(mask, batch, heads, seq)
+        sb, sh, sq = strides
         N.call("kh_attention_masked", qkv.ptr, batch, seq, heads, d_model // heads, int(bool(causal)), mask.ptr,
                mask.numel(), sb, sh, sq, out.ptr, rp.buf.ptr)
         return out, rp

@@ -128,6 +128,36 @@ def test_attention_shape_checked(qkv_shape, batch, seq, heads, d_model):
         H.attention(qkv, batch, seq, heads, d_model)
 
 
+@pytest.mark.parametrize("mshape", [[8, 7], [3, 1, 8, 8], [1, 3, 8, 8], [2, 2, 2, 8, 8], [9]])
+def test_attention_mask_shape_checked(mshape):
+    """A mask that does not broadcast to [batch, heads, seq, seq] (key axis
+    last and full) is refused before any device call."""
+    from kansaiml_amd import hip as H
+    with pytest.raises(RuntimeError, match="broadcast"):
+        H.attention(_fake([16, 384]), 2, 8, 2, 128, mask=_fake(mshape))
+    with pytest.raises(TypeError, match="float32"):
+        H.attention(_fake([16, 384]), 2, 8, 2, 128, mask=_fake([8, 8], "float64"))
+
+
+@needs_lib
+@pytest.mark.parametrize("elems,strides,msg", [
+    (0, (0, 0, 64), "null or empty"),               # empty mask
+    (64, (-1, 0, 8), "negative stride"),
+    (1 << 40, (0, 0, 8), "2 GiB"),                  # size past 32-bit offsets
+    (64, (1 << 33, 0, 8), "2 GiB"),                 # stride past 32-bit offsets
+    (64, (0, 1 << 30, 1 << 30), "2 GiB"),           # strides whose reach passes 32-bit offsets
+    (63, (0, 0, 8), "reach past"),                  # [8, 8] mask one element short
+])
+def test_attention_mask_abi_checks(elems, strides, msg):
+    """kh_attention_masked's own checks of the mask's size and strides
+    (called through the C ABI with fake pointers: every check comes before
+    the first device access)."""
+    from kansaiml_amd import _native as N
+    fake = ctypes.c_void_p(256)
+    with pytest.raises(Exception, match=msg):
+        N.call("kh_attention_masked", fake, 1, 8, 2, 64, 1, fake, elems, *strides, fake, None)
+
+
 @pytest.mark.parametrize("kw", [{"act_granularity": "col"}, {"act_granularity": "token"}, {"mode": "fp8"}])
 def test_qlinear_rejects_unknown_options(kw):
     from kansaiml_amd.quantize import QLinear
