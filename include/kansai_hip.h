@@ -224,8 +224,23 @@ int kh_gemm_i8_quant(const int8_t* a, const int8_t* b_packed, int64_t M, int64_t
                      const double* sa, int sa_per_row, const double* sb, int sb_per_col,
                      const float* bias, int act, const float* residual, int8_t* q, double* scale);
 
+/* kh_gemm_i8_ex's fp32 result quantized per row (per token), as
+ * kh_quantize_rows would quantize it (quantize.py:50-70 applied to each row
+ * of qlinear's output, quantize.py:115-122, and its GELU, nn.py:466-478),
+ * without the fp32 result ever being written: codes int8 [M, N] into q, the
+ * M binary64 row scales into scales.  A workgroup owns 32 whole rows and
+ * keeps their results in registers between the row absmax and the codes; it
+ * takes N = 512, 1024 or 1536 and K = 256 or 384 (the per-token fc1 of a
+ * small model, 16-byte aligned operands); other shapes run
+ * kh_gemm_i8_ex into a pooled temporary and kh_quantize_rows.  A NaN/inf row
+ * reports KH_ERR_NONFINITE at the next synchronize.  No reference
+ * counterpart (the reference has no per-token quantize). */
+int kh_gemm_i8_quant_rows(const int8_t* a, const int8_t* b_packed, int64_t M, int64_t N, int64_t K,
+                          const double* sa, int sa_per_row, const double* sb, int sb_per_col,
+                          const float* bias, int act, int8_t* q, double* scales);
+
 /* The per-tensor quantize of an fp32 activation fused into the GEMM that
- * consumes it: kh_quantize_tensor_parts(x, x_parts) (quantize.py:50-70 on
+ * consumes it:kh_quantize_tensor_parts(x, x_parts) (quantize.py:50-70 on
  * the activation, with the absmax partials its producer wrote) followed by
  * kh_gemm_i8_ex(codes, b_packed, sa = that scale, ...) (qlinear's int8
  * matmul and dequantize, quantize.py:115-144, with the fused bias / GELU /

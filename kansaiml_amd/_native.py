@@ -75,6 +75,7 @@ _SIGNATURES = {
     "kh_gemm_i8_ex": [_vp, _vp, _i64, _i64, _i64, _vp, _int, _vp, _int, _vp, _int, _vp, _vp, _vp, _int,
                       ctypes.POINTER(ctypes.c_int)],
     "kh_gemm_i8_quant": [_vp, _vp, _i64, _i64, _i64, _vp, _int, _vp, _int, _vp, _int, _vp, _vp, _vp],
+    "kh_gemm_i8_quant_rows": [_vp, _vp, _i64, _i64, _i64, _vp, _int, _vp, _int, _vp, _int, _vp, _vp],
     "kh_gemm_i8_qload": [_vp, _i64, _i64, _i64, _vp, _int, _vp, _vp, _int, _vp, _int, _vp, _vp, _vp, _vp, _int,
                          ctypes.POINTER(ctypes.c_int)],
     "kh_gemm_i8_qload_rows": [_vp, _i64, _i64, _i64, _vp, _int, _vp, _vp, _int, _vp, _int, _vp, _vp, _vp],

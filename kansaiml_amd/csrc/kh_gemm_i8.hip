@@ -196,6 +196,29 @@ __device__ __forceinline__ ColEpi col_epi(const Epilogue& ep, int64_t j) {
     return ColEpi{ep.sb ? ep.sb[ep.sb_per_col ? j : 0] : 0.0, ep.bias ? ep.bias[j] : 0.0f};
 }
 
+// The int8 codes of a 32x32 block (lane l's 16 values: column l % 32, rows
+// 4 (l / 32) + 8 (r / 4) + r % 4, the low byte of c[r] each) through `rq`,
+// a resource over the block's 32 rows of N codes (from column -col0).  Codes of rows 8g + t
+// (t = 0..3) of this lane's column, packed (byte t = row t), then transposed
+// across each quad of lanes so that lane 4p + t holds row 8g + t of columns
+// 4p .. 4p + 3: one dword store per group instead of four byte stores (N and
+// the codes' base 4-byte aligned).
+__device__ __forceinline__ void store_codes_block32(__amdgpu_buffer_rsrc_t rq, int N, int lane,
+                                                    const unsigned (&c)[16], int col0 = 0) {
+    const int fr = lane & 31, fh = lane >> 5;
+    const unsigned sel_a = (fr & 1) ? 0x03070105u : 0x06020400u;  // with lane ^ 1: bytes (0,2) or (1,3)
+    const unsigned sel_b = (fr & 2) ? 0x03020706u : 0x05040100u;  // with lane ^ 2: halves 0 or 1
+    const int qoff = (4 * fh + (fr & 3)) * N + (fr & ~3) + col0;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const unsigned p = __builtin_amdgcn_perm(c[4 * g + 1], c[4 * g], 0x0c0c0400u) |
+                           __builtin_amdgcn_perm(c[4 * g + 3], c[4 * g + 2], 0x04000c0cu);
+        const unsigned a = __builtin_amdgcn_perm(kh::lanes::quad_perm<0xB1>(p), p, sel_a);
+        const unsigned t = __builtin_amdgcn_perm(kh::lanes::quad_perm<0x4E>(a), a, sel_b);
+        __builtin_amdgcn_raw_buffer_store_b32(t, rq, qoff, 8 * g * N, 0);
+    }
+}
+
 template <bool FUSED, int MODE, bool ROWSA = false>
 __device__ __forceinline__ unsigned store_block32_full(const Epilogue& ep, int64_t rowblk, int64_t colblk, int N,
                                                        int lane, double sa, const i32x16& v,
@@ -271,22 +294,7 @@ __device__ __forceinline__ unsigned store_block32_full(const Epilogue& ep, int64
 #pragma unroll
             for (int r = 0; r < 16; ++r) c[r] = sc.bad ? 0u : (unsigned)kh::quant::quant_exact(y[r], sc.s);
         }
-        // Codes of rows 8g + t (t = 0..3) of this lane's column, packed (byte
-        // t = row t), then transposed across each quad of lanes so that lane
-        // 4p + t holds row 8g + t of columns 4p .. 4p + 3: one dword store per
-        // group instead of four byte stores.
-        const unsigned sel_a = (fr & 1) ? 0x03070105u : 0x06020400u;  // with lane ^ 1: bytes (0,2) or (1,3)
-        const unsigned sel_b = (fr & 2) ? 0x03020706u : 0x05040100u;  // with lane ^ 2: halves 0 or 1
-        const __amdgpu_buffer_rsrc_t rq = kh::pipe::make_rsrc(ep.q + base, span / 4u);
-        const int qoff = (4 * fh + (fr & 3)) * N + (fr & ~3);
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const unsigned p = __builtin_amdgcn_perm(c[4 * g + 1], c[4 * g], 0x0c0c0400u) |
-                               __builtin_amdgcn_perm(c[4 * g + 3], c[4 * g + 2], 0x04000c0cu);
-            const unsigned a = __builtin_amdgcn_perm(kh::lanes::quad_perm<0xB1>(p), p, sel_a);
-            const unsigned t = __builtin_amdgcn_perm(kh::lanes::quad_perm<0x4E>(a), a, sel_b);
-            __builtin_amdgcn_raw_buffer_store_b32(t, rq, qoff, 8 * g * N, 0);
-        }
+        store_codes_block32(kh::pipe::make_rsrc(ep.q + base, span / 4u), N, lane, c);
     }
     return mx;
 }
@@ -880,6 +888,258 @@ __global__ __launch_bounds__(512, 2) void gemm_i8_qload_kernel(const float* __re
             parts[blockIdx.x] = m;
         }
     }
+}
+
+// ---------------------------------------------------------------------------
+// Per-row (per-token) producer quantize: an int8 Linear's epilogue (bias,
+// GELU) quantized per row inside the GEMM, the fp32 result never written
+// (kh_gemm_i8_quant_rows: quantize.py:50-70 applied to each row of qlinear's
+// output, quantize.py:115-144).  A row's scale needs all N of its values, so
+// a workgroup owns 32 whole rows and keeps their results in registers: the
+// weight streams through LDS in units of 256 columns x 128 bytes of K
+// (LDS-DMA, 128 contiguous bytes per row, a ring of four units), each of the
+// 8 waves multiplies its 32 columns of the unit (v_mfma_i32_32x32x32_i8,
+// activation fragments held in registers), and after a chunk's last unit
+// turns its 32 x 32 accumulators into the epilogue's values (the fp32
+// epilogue of store_block32_full with per-row scales, then GELU), kept in
+// registers.  The rows' absmax is then reduced across the lanes and waves
+// (LDS) and the same registers are quantized with each row's scale.
+// ---------------------------------------------------------------------------
+constexpr int kRqRows = 32, kRqWaves = 8, kRqCols = 256, kRqSlab = 128, kRqRing = 4;
+
+template <bool GELU, int NC, int KS>
+__global__ __launch_bounds__(kRqWaves * 64, 2) void gemm_i8_quant_rows_kernel(const int8_t* __restrict__ A,
+                                                                              const int8_t* __restrict__ B, int M,
+                                                                              int N, int K, Epilogue ep) {
+    constexpr int kSlabs = KS / 4;  // 128-byte k-slabs per chunk of 256 columns
+    constexpr int kUnits = NC * kSlabs;
+    constexpr int kAhead = kRqRing - 1;
+    static_assert(KS % 4 == 0, "K must be a multiple of 128");
+    __shared__ __attribute__((aligned(1024))) int8_t b_lds[kRqRing][kRqCols * kRqSlab];
+    __shared__ unsigned red[kRqWaves][kRqRows];
+    __shared__ double row_sa[kRqWaves][kRqRows];  // each wave's own copy
+    __shared__ double row_s[kRqRows];
+    __shared__ float row_rf[kRqRows];
+    __shared__ unsigned row_fl[kRqRows];  // bit 0: fast path allowed, bit 1: non-finite
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int fr = lane & 31, fh = lane >> 5;
+    const int m0 = blockIdx.x * kRqRows;
+    const int rows_valid = min(kRqRows, M - m0);
+    // Rows past M read zeros (buffer bound); their codes are dropped below.
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(A + (int64_t)m0 * K, (uint32_t)rows_valid * (uint32_t)K);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(B, (uint32_t)N * (uint32_t)K);
+    // Row r of a unit holds its 8 granules of 16 bytes with granule g in slot
+    // g ^ swz(r): a fragment read (16 consecutive rows, one granule) then
+    // hits 16 distinct 16-byte slots of 256 bytes.
+    auto swz = [](int r) { return (r >> 1) & 7; };
+
+    // Unit u = (chunk u / kSlabs, slab u % kSlabs): this wave's 32 rows of
+    // it, 8 rows (of 128 bytes) per LDS-DMA instruction.
+    const int dr = lane >> 3, dg = lane & 7;
+    auto issue = [&](int u) {
+        const int c = u / kSlabs, sl = u % kSlabs;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = 32 * wave + 8 * i + dr;
+            lds_dma16(rb, b_lds[u % kRqRing] + (32 * wave + 8 * i) * kRqSlab,
+                      (kRqCols * c + r) * K + ((dg ^ swz(r)) << 4), kRqSlab * sl);
+        }
+    };
+    // The loads in the order they are needed: row fr's activation scale
+    // (written to LDS once unit 0 has landed), the first units, the
+    // activation fragments (substep t: lane l supplies k = 32 t + 16 (l / 32)
+    // .. + 15 of activation row l % 32, as of weight column l % 32 of its
+    // block) and the epilogue's column operands (chunk c: column 256 c + 32
+    // wave + fr).
+    const double my_sa = ep.sa[ep.sa_per_row ? min(m0 + fr, M - 1) : 0];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < kAhead && u < kUnits; ++u) issue(u);
+    __builtin_amdgcn_sched_barrier(0);
+    i32x4 af[KS];
+#pragma unroll
+    for (int t = 0; t < KS; ++t)
+        af[t] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, fr * K + 16 * fh, 32 * t, 0));
+    double sbj[NC];
+    float bj[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int j = kRqCols * c + 32 * wave + fr;
+        sbj[c] = ep.sb[ep.sb_per_col ? j : 0];
+        bj[c] = ep.bias ? ep.bias[j] : 0.0f;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // The LDS this wave touches while its LDS-DMAs are in flight -- its units'
+    // rows and its copy of the row scales -- is accessed by inline ds_read /
+    // ds_write with explicit waits: as plain LDS accesses the compiler would
+    // wait for every LDS-DMA in flight (the next units') before each.
+    const unsigned sa_lds = (unsigned)(uintptr_t)(__attribute__((address_space(3))) double*)row_sa[wave];
+
+    const int br = 32 * wave + fr;
+    const int b_off = br * kRqSlab;
+    float g[NC][16];
+    unsigned mx[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx[r] = 0;
+    // Chunk c's values (value r of the block is row 4 fh + 8 (r / 4) + r % 4)
+    // in four groups of four rows, each with its four rows' scales.
+    i32x16 acc[2];  // chunk c accumulates in acc[c % 2]
+    auto finish = [&](int c, int g4) {
+        double s4[4];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+            asm volatile("ds_read_b64 %0, %1" : "=v"(s4[rr]) : "v"(sa_lds + 8 * (4 * fh + 8 * g4 + rr)) : "memory");
+        __builtin_amdgcn_s_waitcnt(wait_imm(63, 0));
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) s4[rr] = s4[rr] * sbj[c];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const int r = 4 * g4 + rr;
+            float y = (float)((double)acc[c & 1][r] * s4[rr]);
+            if (ep.bias) y = y + bj[c];
+            if (GELU) y = kh::gelu(y);
+            g[c][r] = y;
+            mx[r] = max(mx[r], kh::abs_bits32(y));
+        }
+    };
+#pragma unroll
+    for (int u = 0; u < kUnits; ++u) {
+        // This wave's loads of unit u have landed (those of the units after
+        // it, 4 instructions each, may be in flight).  A wave reads only the
+        // rows of a unit it loaded itself, so the waves need no barrier
+        // here and drift apart (one's MFMAs overlap another's epilogue).
+        if (u + 2 < kUnits) __builtin_amdgcn_s_waitcnt(wait_imm(8, 15));
+        else if (u + 1 < kUnits) __builtin_amdgcn_s_waitcnt(wait_imm(4, 15));
+        else __builtin_amdgcn_s_waitcnt(wait_imm(0, 15));
+        asm volatile("" ::: "memory");  // the unit's LDS reads stay after the wait
+        if (u == 0 && fh == 0) asm volatile("ds_write_b64 %0, %1" : : "v"(sa_lds + 8 * fr), "v"(my_sa) : "memory");
+        // The unit's fragments, then (the reads issued) slot (u + 3) % 4 --
+        // read by this wave in step u - 1 -- takes unit u + 3.
+        const int8_t* base = b_lds[u % kRqRing] + b_off;
+        const int c = u / kSlabs, sl = u % kSlabs;
+        // (Inline ds_read_b128: read as plain LDS loads, the compiler would
+        // wait for every LDS-DMA in flight -- the next units' -- before them;
+        // the explicit wait below covers these four.)
+        i32x4 bfr[4];
+        const unsigned lds_row = (unsigned)(uintptr_t)(const __attribute__((address_space(3))) int8_t*)base;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            asm volatile("ds_read_b128 %0, %1"
+                         : "=v"(bfr[q])
+                         : "v"(lds_row + (((2 * q + fh) ^ swz(br)) << 4))
+                         : "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        if (u + kAhead < kUnits) issue(u + kAhead);
+        __builtin_amdgcn_s_waitcnt(wait_imm(63, 0));  // the four fragments in registers
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            acc[c & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[4 * sl + q], bfr[q],
+                                                               sl == 0 && q == 0 ? i32x16{0} : acc[c & 1], 0, 0, 0);
+        // The previous chunk's values, spread over this chunk's units (group
+        // g4 in unit g4 kSlabs / 4) so that the epilogue's arithmetic runs
+        // while the next units' weights are in flight.
+        if (c > 0) {
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4)
+                if (g4 * kSlabs / 4 == sl) finish(c - 1, g4);
+        }
+    }
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) finish(NC - 1, g4);
+
+    // Each row's largest |value| bits (NaN and +-inf above every finite
+    // value): over the lane's chunks, the 32 lanes of its half, the waves.
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx[r] = kh::lanes::half_max(mx[r]);
+    if (fr == 0) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red[wave][4 * fh + 8 * (r >> 2) + (r & 3)] = mx[r];
+    }
+    __syncthreads();
+    if (tid < kRqRows) {
+        unsigned m = red[0][tid];
+#pragma unroll
+        for (int w = 1; w < kRqWaves; ++w) m = max(m, red[w][tid]);
+        const kh::quant::Scale sc = kh::quant::make_scale(m);
+        row_s[tid] = sc.s;
+        row_rf[tid] = sc.rf;
+        row_fl[tid] = (sc.fast ? 1u : 0u) | (sc.bad ? 2u : 0u);
+        if (tid < rows_valid) {
+            ep.qscale[m0 + tid] = sc.s;
+            if (sc.bad) kh::quant::flag_nonfinite(ep.fault);
+        }
+    }
+    __syncthreads();
+    double rs[16];
+    float rrf[16];
+    bool all_fast = true;
+    unsigned rbad = 0;  // bit r: row of value r non-finite
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int row = 4 * fh + 8 * (r >> 2) + (r & 3);
+        rs[r] = row_s[row];
+        rrf[r] = row_rf[row];
+        const unsigned f = row_fl[row];
+        all_fast = all_fast && (f & 1u);
+        rbad |= ((f >> 1) & 1u) << r;
+    }
+    // quant_one with each row's scale: the fast path where every row of the
+    // lane allows it and each value is decisive, the exact one otherwise.
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(ep.q + (int64_t)m0 * N, (uint32_t)rows_valid * (uint32_t)N);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        unsigned cq[16];
+        bool ok = all_fast;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) cq[r] = kh::quant::quant_fast(g[c][r], rrf[r], ok);
+        if (!ok) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                cq[r] = ((rbad >> r) & 1u) ? 0u : (unsigned)kh::quant::quant_exact(g[c][r], rs[r]);
+        }
+        store_codes_block32(rq, N, lane, cq, kRqCols * c + 32 * wave);
+    }
+}
+
+// N = 256 NC (NC = 2, 4, 6) and K = 32 KS (KS = 8, 12): the C4 model's
+// per-token fc1 (K = 384, N = 1536) and the shapes around it.
+bool quant_rows_fits(const int8_t* A, const int8_t* B, const int8_t* q, int64_t M, int64_t N, int64_t K) {
+    return M >= 1 && (N == 512 || N == 1024 || N == 1536) && (K == 256 || K == 384) && kh::aligned(A, 16) &&
+           kh::aligned(B, 16) && kh::aligned(q, 4) && (M + kRqRows) * K <= 0x7FFFFFFFLL &&
+           (M + kRqRows) * N <= 0x7FFFFFFFLL;
+}
+
+template <bool GELU, int NC>
+void launch_quant_rows_nc(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
+                          const Epilogue& ep) {
+    const unsigned grid = (unsigned)((M + kRqRows - 1) / kRqRows);
+    if (K == 256)
+        gemm_i8_quant_rows_kernel<GELU, NC, 8><<<grid, kRqWaves * 64, 0, d->stream>>>(A, B, (int)M, (int)N, (int)K, ep);
+    else
+        gemm_i8_quant_rows_kernel<GELU, NC, 12><<<grid, kRqWaves * 64, 0, d->stream>>>(A, B, (int)M, (int)N, (int)K, ep);
+}
+
+template <bool GELU>
+void launch_quant_rows_act(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
+                           const Epilogue& ep) {
+    if (N == 512)
+        launch_quant_rows_nc<GELU, 2>(d, A, B, M, N, K, ep);
+    else if (N == 1024)
+        launch_quant_rows_nc<GELU, 4>(d, A, B, M, N, K, ep);
+    else
+        launch_quant_rows_nc<GELU, 6>(d, A, B, M, N, K, ep);
+}
+
+int launch_quant_rows(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
+                      const Epilogue& ep) {
+    if (ep.act == kActGelu)
+        launch_quant_rows_act<true>(d, A, B, M, N, K, ep);
+    else
+        launch_quant_rows_act<false>(d, A, B, M, N, K, ep);
+    return kh::launch_status("gemm_i8_quant_rows");
 }
 
 // ---------------------------------------------------------------------------
@@ -1917,6 +2177,36 @@ int kh_gemm_i8_quant(const int8_t* a, const int8_t* b_packed, int64_t M, int64_t
     rc = gemm_i8_impl(a, b_packed, M, N, K, sa, sa_per_row, sb, sb_per_col, bias, out, nullptr, act, residual,
                       nullptr, 0, nullptr);
     if (!rc) rc = kh_quantize_tensor(out, M * N, q, scale);
+    kh_free(tmp);  // stream-ordered reuse: later work is queued behind the quantize
+    return rc;
+}
+
+int kh_gemm_i8_quant_rows(const int8_t* a, const int8_t* b_packed, int64_t M, int64_t N, int64_t K, const double* sa,
+                          int sa_per_row, const double* sb, int sb_per_col, const float* bias, int act, int8_t* q,
+                          double* scales) {
+    KH_REQUIRE(M >= 0 && N >= 0 && K >= 0, "kh_gemm_i8_quant_rows: negative shape");
+    KH_REQUIRE(K <= 133144, "kh_gemm_i8_quant_rows: K > 133144 could overflow the int32 accumulator");
+    KH_REQUIRE(M <= 0xFFFFLL * 128 && N <= 0x7FFFFFFFLL, "kh_gemm_i8_quant_rows: shape too large");
+    KH_REQUIRE(act == kActNone || act == kActGelu, "kh_gemm_i8_quant_rows: unknown activation");
+    if (M == 0) return KH_OK;
+    KH_REQUIRE(scales, "kh_gemm_i8_quant_rows: null scales");
+    if (N == 0) return kh_quantize_rows(nullptr, M, 0, q, scales);  // every row's scale 1.0
+    KH_REQUIRE(q && sa && sb && (K == 0 || (a && b_packed)), "kh_gemm_i8_quant_rows: null pointer");
+    KH_DEVICE_OR_RETURN(d);
+    if (quant_rows_fits(a, b_packed, q, M, N, K)) {
+        Epilogue ep{sa, sb, bias, nullptr, nullptr, sa_per_row, sb_per_col, act, nullptr,
+                    q, nullptr, 0, scales, d->fault};
+        return launch_quant_rows(d, a, b_packed, M, N, K, ep);
+    }
+    // Other shapes: the fp32 result through a pooled temporary, then the
+    // per-row quantize.
+    void* tmp = nullptr;
+    int rc = kh_alloc((size_t)(M * N) * sizeof(float), &tmp);
+    if (rc) return rc;
+    float* out = static_cast<float*>(tmp);
+    rc = gemm_i8_impl(a, b_packed, M, N, K, sa, sa_per_row, sb, sb_per_col, bias, out, nullptr, act, nullptr,
+                      nullptr, 0, nullptr);
+    if (!rc) rc = kh_quantize_rows(out, M, N, q, scales);
     kh_free(tmp);  // stream-ordered reuse: later work is queued behind the quantize
     return rc;
 }

@@ -375,6 +375,31 @@ def gemm_i8_quant(a: DeviceTensor, b_packed: DeviceTensor, sa: DeviceTensor, sb:
     return q, s
 
 
+def gemm_i8_quant_rows(a: DeviceTensor, b_packed: DeviceTensor, sa: DeviceTensor, sb: DeviceTensor,
+                       bias: DeviceTensor | None = None, *, act: str | None = None):
+    """quantize_rows(gemm_i8_fused(...)) without writing the fp32 result:
+    returns (codes int8 [..., M, N], row scales float64 [M]).  sa holds one
+    scale per row of a (a per-token activation)."""
+    M, K, lead = _rows(a, "int8", "gemm_i8(a)")
+    _need(b_packed, "int8", 2, "gemm_i8(b)")
+    Nn, K2 = b_packed.shape
+    if K != K2:
+        raise RuntimeError(f"gemm_i8: incompatible shapes {a.shape} x {b_packed.shape}^T")
+    if act not in ACTS:
+        raise ValueError(f"gemm_i8_quant_rows: unknown activation {act!r}")
+    sa_mode = _scale_mode(sa, M, "gemm_i8(sa)")
+    sb_mode = _scale_mode(sb, Nn, "gemm_i8(sb)")
+    if bias is not None:
+        _need(bias, "float32", 1, "gemm_i8(bias)")
+        if bias.shape[0] != Nn:
+            raise RuntimeError("gemm_i8: bias must have N entries")
+    q = DeviceTensor(lead + [Nn], "int8")
+    s = DeviceTensor([M], "float64")
+    N.call("kh_gemm_i8_quant_rows", a.ptr, b_packed.ptr, M, Nn, K, sa.ptr, sa_mode, sb.ptr, sb_mode, _opt(bias),
+           ACTS[act], q.ptr, s.ptr)
+    return q, s
+
+
 def gemm_i8_qload(x: DeviceTensor, parts: AbsmaxParts, b_packed: DeviceTensor, sb: DeviceTensor,
                   bias: DeviceTensor | None = None, *, act: str | None = None,
                   residual: DeviceTensor | None = None, absmax: bool = False, want_scale: bool = False):

@@ -601,6 +601,79 @@ def test_gemm_i8_quant_edge_cases(hip):
     Nn.synchronize()
 
 
+@pytest.mark.parametrize("M,N,K", [(16384, 1536, 384),  # C4 fc1, per token: the fused kernel
+                                   (300, 1536, 384),    # a partial last workgroup (12 rows)
+                                   (64, 512, 256),      # two blocks per wave, 8 k-substeps
+                                   (1, 1024, 384),      # one row (a per-tensor scale), four blocks per wave
+                                   (130, 1024, 256),
+                                   (200, 1000, 384),    # other N: fp32 temporary + quantize_rows
+                                   (100, 512, 448)])    # other K: the same
+def test_gemm_i8_quant_rows_matches_unfused(hip, M, N, K):
+    """kh_gemm_i8_quant_rows' codes and row scales equal the per-row
+    quantize (kh_quantize_rows, and the oracle's) of the unfused GEMM's fp32
+    output, plain and with GELU, bit for bit.  Rows of zero codes under an
+    all-negative bias hold only negative values (their largest |GELU| is not
+    GELU(max): the fused kernel's extra sweep), a row with a huge activation
+    scale saturates, and a zero row scale gives a zero row."""
+    H, D = hip
+    gen = np.random.Generator(np.random.PCG64(3 * M + 7 * N + K))
+    a = gen.integers(-127, 128, (M, K), dtype=np.int8)
+    bt = gen.integers(-127, 128, (N, K), dtype=np.int8)
+    sa = gen.uniform(1e-4, 5e-4, M)
+    a[M // 2] = 0
+    sa[M - 1] = 0.0
+    if M > 2:
+        sa[1] = 1e30
+    sb = gen.uniform(1e-4, 1e-3, N)
+    ad, bd, sad, sbd = D.from_host(a), D.from_host(bt), D.from_host(sa), D.from_host(sb)
+    for bias in (gen.standard_normal(N).astype(np.float32), -np.abs(gen.standard_normal(N)).astype(np.float32) - 0.01,
+                 None):
+        biasd = D.from_host(bias) if bias is not None else None
+        for act in (None, "gelu"):
+            y, _ = H.gemm_i8_fused(ad, bd, sad, sbd, biasd, act=act)
+            q2, s2 = H.quantize_rows(y)
+            q, s = H.gemm_i8_quant_rows(ad, bd, sad, sbd, biasd, act=act)
+            np.testing.assert_array_equal(q.numpy(), q2.numpy())
+            np.testing.assert_array_equal(s.numpy().view(np.uint64), s2.numpy().view(np.uint64))
+            rows = np.unique(np.r_[0, 1, M // 2, M - 1, gen.integers(0, M, 64)]) % M
+            oq, os_ = O.ko_quantize_rows(y.numpy()[rows])
+            np.testing.assert_array_equal(q.numpy()[rows], oq)
+            np.testing.assert_array_equal(s.numpy()[rows], os_)
+
+
+def test_gemm_i8_quant_rows_edge_cases(hip):
+    """An empty result: nothing for M = 0, every row scale 1.0 for N = 0
+    (quantize.py:68 per row); a NaN row scale makes that row's values NaN:
+    its codes are zero, its scale NaN, the others untouched, and the next
+    synchronize raises ValueError as the unfused per-row quantize does."""
+    from kansaiml_amd import _native as Nn
+    H, D = hip
+    gen = np.random.Generator(np.random.PCG64(5))
+    a = gen.integers(-127, 128, (192, 256), dtype=np.int8)
+    bt = gen.integers(-127, 128, (384, 256), dtype=np.int8)
+    sb = D.from_host(np.full(384, 1e-3))
+    q, s = H.gemm_i8_quant_rows(D([0, 256], "int8"), D.from_host(bt), D([0], "float64"), sb)
+    assert q.shape == [0, 384] and s.shape == [0]
+    q, s = H.gemm_i8_quant_rows(D.from_host(a), D([0, 256], "int8"), D.from_host(np.full(192, 1e-3)),
+                                D([0], "float64"))
+    assert (s.numpy() == 1.0).all()
+    sa = np.full(192, 1e-3)
+    sa[70] = np.nan
+    ad, bd, sad = D.from_host(a), D.from_host(bt), D.from_host(sa)
+    for act in (None, "gelu"):
+        q, s = H.gemm_i8_quant_rows(ad, bd, sad, sb, act=act)
+        with pytest.raises(ValueError):
+            Nn.synchronize()
+        Nn.synchronize()
+        y, _ = H.gemm_i8_fused(ad, bd, sad, sb, act=act)
+        qh, sh = q.numpy(), s.numpy()
+        assert not qh[70].any() and np.isnan(sh[70])
+        keep = np.r_[0:70, 71:192]
+        oq, os_ = O.ko_quantize_rows(y.numpy()[keep])
+        np.testing.assert_array_equal(qh[keep], oq)
+        np.testing.assert_array_equal(sh[keep], os_)
+
+
 def _producer_parts(x):
     """Absmax partials of x as a producer would write them (kh_absmax_parts)."""
     import ctypes
