@@ -529,7 +529,8 @@ def bench_c4(steps, warmup):
     # the reference's per-tensor configuration), replayed as a HIP graph:
     # LayerNorms emit per-row codes, the attention output is quantized per
     # row inside the O GEMM (qload, from the attention's per-(row, head)
-    # partials), fc1's output by the per-row quantize
+    # partials), fc1's (-> GELU) rows inside the fc1 GEMM
+    # (kh_gemm_i8_quant_rows)
     ms_row = None  # a profiled run traces the configured (per-tensor) forward only
     if GRAPH_TIMING:
         gr = CharLM(w, act_granularity="row").capture(64, 256)

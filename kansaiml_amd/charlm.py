@@ -117,15 +117,18 @@ class CharLM:
                  qload: bool = True):
         """producer_quant (kir.quant_fusion's option): "layer_norm" (the
         default) -- each LayerNorm emits its int8 codes directly instead of
-        fp32 (two passes over its input; the fastest on MI355X); True -- fc1
-        (-> GELU) as well (less memory, slower); False -- neither.
+        fp32 (two passes over its input; the fastest on MI355X), and with
+        per-token scales fc1 (-> GELU) quantizes its own rows inside the GEMM
+        (kh_gemm_i8_quant_rows, one pass); True -- fc1's per-tensor quantize
+        as well (two passes over the GEMM: less memory, slower); False --
+        none.
         qload (kir.quant_fusion's option; on by default, bit-identical
         either way): the attention output's quantize runs inside the O GEMM
         that consumes it, so its codes are never written -- per tensor from
         the attention's absmax partials (kh_gemm_i8_qload), per row from its
-        per-(row, head) partials (kh_gemm_i8_qload_rows).  fc1's output
-        (1536 columns) keeps its separate quantize: quantizing on load in
-        fc2 measured no faster.  Replayed C4 forwards on one box: per tensor
+        per-(row, head) partials (kh_gemm_i8_qload_rows).  fc1's per-tensor
+        quantize stays a separate launch: quantizing on load in fc2 (K =
+        1536) measured no faster.  Replayed C4 forwards on one box: per tensor
         1.1075 -> 1.1055 ms, per row 1.092 -> 1.063 ms.
         act_granularity: "tensor" (the reference's quantize_symmetric over the
         whole activation, the C4 configuration) or "row" (one scale per token;

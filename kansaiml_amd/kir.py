@@ -264,7 +264,10 @@ def quant_fusion(graph, producer_quant: bool | str = False, qload: bool = False)
     and, with producer_quant=True (both) or "layer_norm" (the second only),
       ... the int8_linear chain -> quantize (per tensor) => int8_linear_quant
       layer_norm -> quantize (per tensor)        =>  layer_norm_quant
+    and, with producer_quant=True or "layer_norm",
       layer_norm -> quantize (per row)           =>  layer_norm_quant_rows
+      ... the int8_linear chain (no residual) -> quantize (per row)
+                                                 =>  int8_linear_quant_rows
     int8_linear's attrs record what it absorbed: bias (bool), act ("gelu" or
     None), residual (bool; the residual operand comes last) and qload (bool:
     operand 0 is the fp32 activation, quantized per tensor inside the GEMM,
@@ -276,7 +279,10 @@ def quant_fusion(graph, producer_quant: bool | str = False, qload: bool = False)
     values and reading them back) but not for the GEMM, whose VALU-bound
     epilogue (binary64 dequantize, GELU) the second pass repeats.
     layer_norm_quant_rows needs no second pass: each row's scale depends on
-    that row only, so one pass stores codes and scales.
+    that row only, so one pass stores codes and scales; int8_linear_quant_rows
+    neither: a workgroup owns whole rows and keeps their values in registers
+    (kh_gemm_i8_quant_rows), so it is faster than the two launches it
+    replaces and fuses under "layer_norm" too.
     Then every int8_linear, layer_norm or attention whose
     output feeds a per-tensor quantize is marked absmax=True: its kernel
     writes the absmax partials that quantize needs, so the quantize reads
@@ -312,6 +318,16 @@ def quant_fusion(graph, producer_quant: bool | str = False, qload: bool = False)
             return None
         q = only_user(nid)
         if q is not None and by_id[q].op == "quantize" and by_id[q].attrs.get("granularity", "tensor") == "tensor":
+            return q
+        return None
+
+    def row_quantize(nid):
+        """The per-row quantize that is the only user of nid, if any (and
+        producer fusion is on)."""
+        if producer_quant not in (True, "layer_norm"):
+            return None
+        q = only_user(nid)
+        if q is not None and by_id[q].op == "quantize" and by_id[q].attrs.get("granularity") == "row":
             return q
         return None
 
@@ -360,9 +376,13 @@ def quant_fusion(graph, producer_quant: bool | str = False, qload: bool = False)
                         attrs["residual"] = True
                 last = chain[-1]
                 q = tensor_quantize(last) if not attrs.get("qload") else None
+                qr = row_quantize(last) if not attrs.get("qload") and not attrs["residual"] else None
                 if q is not None:
                     absorbed.update(chain)
                     fused[q] = ("int8_linear_quant", ins, attrs)
+                elif qr is not None:
+                    absorbed.update(chain)
+                    fused[qr] = ("int8_linear_quant_rows", ins, attrs)
                 else:
                     absorbed.update(set(chain) - {last})
                     fused[last] = ("int8_linear", ins, attrs)
@@ -631,6 +651,12 @@ def _exec(node, vals):
         residual = ins[-1] if at.get("residual") else None
         q, s = H.gemm_i8_quant(a, b, sa, sb, bias, act=at.get("act"), residual=residual)
         return QTensor(q, s, list(node.shape), "tensor", packed=False)
+    if op == "int8_linear_quant_rows":
+        from .quantize import QTensor
+        a, b, sa, sb = _int8_operands(ins[0], ins[1], "int8_linear_quant_rows")
+        bias = ins[2] if node.attrs.get("bias") else None
+        q, s = H.gemm_i8_quant_rows(a, b, sa, sb, bias, act=node.attrs.get("act"))
+        return QTensor(q, s, list(node.shape), "row", packed=False)
     if op == "layer_norm_quant":
         from .quantize import QTensor
         x, w, b = ins

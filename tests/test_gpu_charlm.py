@@ -387,6 +387,22 @@ def _check_node(node, got, ins):
         q, s = O.ko_quantize_tensor(yh)
         np.testing.assert_array_equal(got[0], q.reshape(got[0].shape))
         assert got[1][0] == s
+    elif op == "int8_linear_quant_rows":
+        # the unfused int8_linear on the same inputs (checked against the
+        # oracle as the int8_linear node is), then the oracle's per-row
+        # quantize: codes and binary64 row scales bit for bit
+        from kansaiml_amd import hip as H
+        from kansaiml_amd.device import DeviceTensor as D
+        (qa, sa), (qw, sw) = ins[0], ins[1]
+        at = node.attrs
+        bias = ins[2] if at.get("bias") else None
+        y, _ = H.gemm_i8_fused(D.from_host(qa), D.from_host(qw), D.from_host(sa), D.from_host(sw),
+                               D.from_host(bias) if bias is not None else None, act=at.get("act"))
+        yh = y.numpy()
+        _check_node(type("N", (), {"op": "int8_linear", "attrs": at})(), yh, ins)
+        q, s = O.ko_quantize_rows(yh.reshape(-1, yh.shape[-1]))
+        np.testing.assert_array_equal(got[0].reshape(q.shape), q)
+        np.testing.assert_array_equal(got[1], s)
     elif op == "layer_norm":
         x, w, b = ins
         ref = R.layer_norm(x.astype(np.float64), w, b, node.attrs.get("eps", 1e-5))
@@ -517,8 +533,14 @@ def test_small_model_per_token(G, producer_quant):
         ins = [ids if by_id[i].op == "placeholder" else seen[i][1] for i in node.inputs]
         _check_node(node, got, ins)
         checked.add(node.op)
-    ln = "layer_norm_quant_rows" if producer_quant else "layer_norm"
-    assert checked == {"embedding", ln, "quantize", "int8_linear", "attention"}
+    # With producer fusion the LayerNorms emit codes and scales and fc1
+    # (-> GELU) quantizes its rows inside the GEMM; the attention output is
+    # quantized inside the O GEMM (qload): no quantize node is left.
+    if producer_quant:
+        assert checked == {"embedding", "layer_norm_quant_rows", "int8_linear", "int8_linear_quant_rows", "attention"}
+        assert [n.attrs.get("act") for n in g.nodes if n.op == "int8_linear_quant_rows"] == ["gelu"] * 2
+    else:
+        assert checked == {"embedding", "layer_norm", "quantize", "int8_linear", "attention"}
     assert all(n.attrs.get("granularity") == "row" for n in g.nodes if n.op == "quantize")
     fp = R.forward(w, ids, quantized=False)
     assert np.abs(y - fp).max() < 0.1 * np.abs(fp).max()
@@ -558,6 +580,28 @@ def _check_node_sampled(node, got, ins, gen, nrows=64, nbatches=3):
         sub = [(qa[rows], sa[rows] if sa.size > 1 else sa), w] + [
             (v[rows] if (k == len(ins) - 1 and node.attrs.get("residual")) else v) for k, v in enumerate(ins[2:], 2)]
         _check_node(node, got[rows], sub)
+    elif op == "int8_linear_quant_rows":
+        # the unfused GEMM (GPU) and per-row quantize in full, bit for bit;
+        # the GEMM's rows against the oracle, and their per-row quantize, on
+        # sampled rows
+        from oracle import oracle as O
+        from kansaiml_amd import hip as H
+        from kansaiml_amd.device import DeviceTensor as D
+        (qa, sa), (qw, sw) = ins[0], ins[1]
+        at = node.attrs
+        bias = ins[2] if at.get("bias") else None
+        y, _ = H.gemm_i8_fused(D.from_host(qa), D.from_host(qw), D.from_host(sa), D.from_host(sw),
+                               D.from_host(bias) if bias is not None else None, act=at.get("act"))
+        q2, s2 = H.quantize_rows(y)
+        np.testing.assert_array_equal(got[0].reshape(q2.shape), q2.numpy())
+        np.testing.assert_array_equal(got[1], s2.numpy())
+        rows = np.sort(gen.choice(got[0].shape[0], nrows, replace=False))
+        yh = y.numpy()[rows]
+        lin = type("N", (), {"op": "int8_linear", "attrs": at})()
+        _check_node(lin, yh, [(qa[rows], sa[rows] if sa.size > 1 else sa), ins[1]] + list(ins[2:]))
+        q, s = O.ko_quantize_rows(yh)
+        np.testing.assert_array_equal(got[0][rows], q)
+        np.testing.assert_array_equal(got[1][rows], s)
     elif op == "layer_norm":
         rows = np.sort(gen.choice(got.shape[0], nrows, replace=False))
         _check_node(node, got[rows], [ins[0][rows], ins[1], ins[2]])
@@ -605,10 +649,13 @@ def test_full_c4_forward(G, act_granularity, qload):
     # fc1 outputs are quantized by a quantize node, or with qload the
     # attention output inside the O GEMM (per tensor from the attention's
     # partials, or per row from its per-(row, head) partials).
+    # Per row, fc1 (-> GELU) quantizes its own rows (int8_linear_quant_rows).
+    lin = {"int8_linear": 25} if act_granularity == "tensor" else {"int8_linear": 19, "int8_linear_quant_rows": 6}
+    nq = 12 if act_granularity == "tensor" else 6
     if not qload:
-        assert counts == {"embedding": 1, ln: 13, "int8_linear": 25, "attention": 6, "quantize": 12}, counts
+        assert counts == {"embedding": 1, ln: 13, **lin, "attention": 6, "quantize": nq}, counts
     else:
-        assert counts == {"embedding": 1, ln: 13, "int8_linear": 25, "attention": 6, "quantize": 6}, counts
+        assert counts == {"embedding": 1, ln: 13, **lin, "attention": 6, **({"quantize": nq - 6} if nq > 6 else {})}, counts
         assert sum(bool(n.attrs.get("qload")) for n in g.nodes) == 6
     np.testing.assert_array_equal(seen[g.output][1].view(np.uint32), y.view(np.uint32))
     del seen

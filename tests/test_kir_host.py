@@ -143,8 +143,9 @@ def test_plan_memory_matches_liveness_brute_force():
 def test_quantize_producers_fuse_into_quant_nodes():
     """A per-tensor quantize whose input is only read by it absorbs its
     producer: layer_norm -> layer_norm_quant, an int8 Linear chain (here with
-    GELU) -> int8_linear_quant.  A producer with a second reader, or a
-    per-row quantize, keeps the fp32 tensor."""
+    GELU) -> int8_linear_quant; a per-row one too: layer_norm_quant_rows,
+    int8_linear_quant_rows.  A producer with a second reader keeps the fp32
+    tensor."""
     w1 = np.zeros((16, 32), np.float32)
     w2 = np.zeros((32, 16), np.float32)
     g1, b1 = np.ones(16, np.float32), np.zeros(16, np.float32)
@@ -195,6 +196,36 @@ def test_quantize_producers_fuse_into_quant_nodes():
         assert [n for n in fr.nodes if n.op == "layer_norm_quant_rows"][0].dtype == "int8"
     ops4 = [n.op for n in kir.quant_fusion(gr).nodes]
     assert "layer_norm" in ops4 and "layer_norm_quant_rows" not in ops4
+
+    # an int8 Linear (-> bias -> GELU) whose only user is a per-row quantize
+    # quantizes its own rows (int8_linear_quant_rows) under either producer
+    # option; not with a residual add in the chain, nor when fusion is off
+    def ffn_rows(x):
+        h = x.layer_norm(g1, b1).quantize("row")
+        f = h.int8_matmul(x._coerce(w1).quantize()).dequantize().add(bias).gelu()
+        return f.quantize("row").int8_matmul(x._coerce(w2).quantize()).dequantize()
+
+    gf = kir.trace(ffn_rows, np.zeros((4, 16), np.float32))
+    for opt in (True, "layer_norm"):
+        ff = kir.quant_fusion(gf, producer_quant=opt)
+        opsf = [n.op for n in ff.nodes if n.op not in ("placeholder", "constant")]
+        # (the two quantizes left are the weights')
+        assert [o for o in opsf if o != "quantize"] == ["layer_norm_quant_rows", "int8_linear_quant_rows",
+                                                        "int8_linear"], opsf
+        assert all(ff.nodes[n.inputs[0]].op == "constant" for n in ff.nodes if n.op == "quantize")
+        fq = [n for n in ff.nodes if n.op == "int8_linear_quant_rows"][0]
+        assert fq.dtype == "int8" and fq.attrs["act"] == "gelu" and fq.attrs["bias"] and not fq.attrs["residual"]
+        assert ff.nodes[fq.inputs[0]].op == "layer_norm_quant_rows"
+    assert "int8_linear_quant_rows" not in [n.op for n in kir.quant_fusion(gf).nodes]
+
+    def resid_rows(x):
+        h = x.layer_norm(g1, b1)
+        y = h.quantize("row").int8_matmul(x._coerce(np.zeros((16, 16), np.float32)).quantize()).dequantize()
+        return y.add(x).quantize("row").int8_matmul(x._coerce(np.zeros((16, 8), np.float32)).quantize())
+
+    fres = kir.quant_fusion(kir.trace(resid_rows, np.zeros((4, 16), np.float32)), producer_quant=True)
+    assert "int8_linear_quant_rows" not in [n.op for n in fres.nodes]
+    assert [n.attrs["residual"] for n in fres.nodes if n.op == "int8_linear"] == [True]
 
 
 def test_quantize_fuses_into_its_int8_linear_with_qload():
