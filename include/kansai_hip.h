@@ -87,6 +87,11 @@ int kh_pool_trim(void);
 /* bytes currently handed out, bytes cached in free lists, number of
  * hipMalloc calls made so far. */
 int kh_pool_stats(size_t* in_use, size_t* cached, size_t* driver_allocs);
+/* The number of kh_alloc calls served so far (from the free lists or the
+ * driver), including the library's own (e.g. kh_gemm_i8's split-K partials).
+ * No reference counterpart: it lets a caller check that a call drew nothing
+ * from the pool (kh_linear_i8_noalloc). */
+int kh_pool_requests(size_t* requests);
 /* The library's own scratch area (absmax partials and the like, outside the
  * pool): its size in bytes, the number of requests made of it so far and
  * the number of hipMalloc calls it made.  No reference counterpart: the
@@ -190,7 +195,10 @@ int kh_dequantize_packed(const int8_t* q_packed, int64_t k, int64_t n, const dou
  * them must be given.  The reference has no int8 GEMM (quantize.py:30-44):
  * this replaces its x.matmul(dequantize(W)).add(bias)
  * (quantize.py:115-122) on the int8 path.  K <= 133144 keeps the int32
- * accumulator exact. */
+ * accumulator exact.  Skinny shapes (M <= 64) whose 16-column tiles leave
+ * CUs idle (N < 16 x CUs / 2) with K >= 8192 split K across workgroups:
+ * int32 partials in pooled device memory, summed (exactly) by a second
+ * launch that applies the epilogue. */
 int kh_gemm_i8(const int8_t* a, const int8_t* b_packed, int64_t M, int64_t N, int64_t K,
                const double* sa, int sa_per_row, const double* sb, int sb_per_col,
                const float* bias, float* out, int32_t* acc_out);

@@ -51,6 +51,7 @@ _SIGNATURES = {
     "kh_free": [_vp],
     "kh_pool_trim": [],
     "kh_pool_stats": [ctypes.POINTER(_size), ctypes.POINTER(_size), ctypes.POINTER(_size)],
+    "kh_pool_requests": [ctypes.POINTER(_size)],
     "kh_scratch_stats": [ctypes.POINTER(_size), ctypes.POINTER(_size), ctypes.POINTER(_size)],
     "kh_memcpy_h2d": [_vp, _vp, _size],
     "kh_memcpy_d2h": [_vp, _vp, _size],
@@ -183,9 +184,10 @@ def device_info() -> dict:
 
 
 def pool_stats() -> dict:
-    a, b, c = _size(), _size(), _size()
+    a, b, c, r = _size(), _size(), _size(), _size()
     call("kh_pool_stats", ctypes.byref(a), ctypes.byref(b), ctypes.byref(c))
-    return {"in_use": a.value, "cached": b.value, "driver_allocs": c.value}
+    call("kh_pool_requests", ctypes.byref(r))
+    return {"in_use": a.value, "cached": b.value, "driver_allocs": c.value, "requests": r.value}
 
 
 def scratch_stats() -> dict:

@@ -1171,7 +1171,7 @@ constexpr int kSkinnyWaves = 8;
 template <int MT, int NT, int C, bool ONE, bool LEAN = false>
 __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_i8_skinny_kernel(const int8_t* __restrict__ A,
                                                                            const int8_t* __restrict__ B, int M,
-                                                                           int N, int K, Epilogue ep) {
+                                                                           int N, int K, int kslice, Epilogue ep) {
     static_assert(MT * NT <= kSkinnyWaves, "one epilogue wave per 16x16 tile");
     __shared__ i32x4v red[kSkinnyWaves][MT * NT][64];
     // TP: the wave's weight slice is read whole rows at a time (16 / C rows
@@ -1184,15 +1184,17 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_i8_skinny_kernel(const
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n0 = blockIdx.x * 16 * NT;
     const int kg = (lane >> 4) * 16;
-    // The launch guarantees K % (512 * C) == 0 and K > 0; saying so lets the
-    // compiler load every kernel argument before the first weight load
-    // instead of after a loop-skip branch.
-    __builtin_assume(K >= 64 * kSkinnyWaves * C);
+    // The launch guarantees kslice % (512 * C) == 0 and kslice > 0; saying so
+    // lets the compiler load every kernel argument before the first weight
+    // load instead of after a loop-skip branch.
+    __builtin_assume(kslice >= 64 * kSkinnyWaves * C);
     // Activation loads in batches of up to 4 steps, each batch issued whole
     // before its MFMAs (all C at once measured slower at N = 11008).
     constexpr int AC = C < 4 ? C : 4;
-    const int kper = K / kSkinnyWaves;  // a multiple of 64 * C; exactly 64 * C when ONE
-    const int k_begin = wave * kper;
+    // Split K: workgroup (x, y) sums k in [y kslice, (y + 1) kslice) (kslice
+    // = K without a split) and writes its int32 sums as partial y.
+    const int kper = kslice / kSkinnyWaves;  // a multiple of 64 * C; exactly 64 * C when ONE
+    const int k_begin = blockIdx.y * kslice + wave * kper;
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, (uint32_t)M * (uint32_t)K);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(B, (uint32_t)N * (uint32_t)K);
     int b_off[NT];
@@ -1355,9 +1357,22 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void gemm_i8_skinny_kernel(const
     for (int r = 0; r < 4; ++r) {
         const int64_t i = t * 16 + 4 * (lane >> 4) + r;
         if (i >= M) continue;
-        if (ep.acc) ep.acc[i * N + j] = sum[r];
+        if (ep.acc) ep.acc[((int64_t)blockIdx.y * M + i) * N + j] = sum[r];
         if (ep.out) ep.out[i * N + j] = epilogue_finish(ep, sum[r], sai[r] * sbj, bj, res[r]);
     }
+}
+
+// The split-K partials [S, M, N] (int32) summed -- exact in any order -- and
+// the epilogue applied, as the unsplit kernel does (epilogue_store: the same
+// sa_i * sb_j product, bias, activation and residual).
+__global__ __launch_bounds__(256) void skinny_splitk_epilogue_kernel(const int32_t* __restrict__ P, int S, int M,
+                                                                     int N, Epilogue ep) {
+    const int64_t mn = (int64_t)M * N;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= mn) return;
+    int32_t sum = 0;
+    for (int s = 0; s < S; ++s) sum += P[s * mn + idx];
+    epilogue_store(ep, idx / N, idx % N, N, sum);
 }
 
 bool skinny_fits(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K) {
@@ -1365,9 +1380,35 @@ bool skinny_fits(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t
            kh::aligned(B, 16) && M * K <= 0xFFFFFFFFLL && N * K <= 0xFFFFFFFFLL && N <= 0x7FFFFFFF;
 }
 
+// Split-K factor for a skinny launch: with one 16-column tile per workgroup a
+// narrow N leaves CUs idle (N = 1024: 64 workgroups on 256 CUs, each
+// streaming 16 K bytes of weight), so K is split over up to 8 workgroups per
+// tile until the grid covers the CUs, keeping each wave at least one 64-k
+// step, for K >= kSplitMinK (below it the weight is small enough that the
+// second launch costs more than the idle CUs).  1 where the caller cannot
+// allocate (the partials live in pooled device memory).
+constexpr int64_t kSplitMinK = 8192;
+int skinny_split(const kh::Device* d, int64_t N, int64_t K, bool may_alloc) {
+    const int64_t tiles = (N + 15) / 16, steps = K / (64 * kSkinnyWaves);
+    int S = 1;
+    if (!may_alloc || K < kSplitMinK) return 1;
+    while (S < 8 && tiles * S * 2 <= d->cus && steps % (2 * S) == 0) S *= 2;
+    return S;
+}
+
 int launch_skinny(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
-                  const Epilogue& ep) {
-    const int64_t steps = K / (64 * kSkinnyWaves);  // 64-k steps per wave
+                  const Epilogue& ep, bool may_alloc = true) {
+    const int S = skinny_split(d, N, K, may_alloc);
+    const int64_t kslice = K / S;
+    const int64_t steps = kslice / (64 * kSkinnyWaves);  // 64-k steps per wave
+    Epilogue eps = ep;
+    void* parts = nullptr;
+    if (S > 1) {
+        int rc = kh_alloc((size_t)S * (size_t)(M * N) * sizeof(int32_t), &parts);
+        if (rc) return rc;
+        eps.out = nullptr;
+        eps.acc = static_cast<int32_t*>(parts);
+    }
     // One 16-column tile per workgroup.  (32 columns, each activation
     // fragment feeding two weight tiles, measured faster for two row tiles
     // at N = 11008 before the whole-row weight reads; with them the
@@ -1375,10 +1416,10 @@ int launch_skinny(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, in
     const bool lean = M > 16 && (N + 15) / 16 > d->cus;
     auto go = [&](auto mt, auto nt, auto c, auto one, auto leanv) {
         constexpr int NT = decltype(nt)::value;
-        const unsigned blocks = (unsigned)((N + 16 * NT - 1) / (16 * NT));
+        const dim3 blocks((unsigned)((N + 16 * NT - 1) / (16 * NT)), (unsigned)S);
         gemm_i8_skinny_kernel<decltype(mt)::value, NT, decltype(c)::value, decltype(one)::value,
                               decltype(leanv)::value><<<blocks, kSkinnyWaves * 64, 0, d->stream>>>(
-            A, B, (int)M, (int)N, (int)K, ep);
+            A, B, (int)M, (int)N, (int)K, (int)kslice, eps);
     };
     auto pick = [&](auto mt) {
         using T = std::true_type;
@@ -1402,7 +1443,16 @@ int launch_skinny(kh::Device* d, const int8_t* A, const int8_t* B, int64_t M, in
     if (M <= 16) pick(std::integral_constant<int, 1>());
     else if (M <= 32) pick(std::integral_constant<int, 2>());
     else pick(std::integral_constant<int, 4>());
-    return kh::launch_status("gemm_i8_skinny");
+    int rc = kh::launch_status("gemm_i8_skinny");
+    if (S > 1) {
+        if (!rc) {
+            skinny_splitk_epilogue_kernel<<<(unsigned)((M * N + 255) / 256), 256, 0, d->stream>>>(
+                static_cast<const int32_t*>(parts), S, (int)M, (int)N, ep);
+            rc = kh::launch_status("skinny_splitk_epilogue");
+        }
+        kh_free(parts);  // stream-ordered: reused only by work queued after the epilogue
+    }
+    return rc;
 }
 
 // ---------------------------------------------------------------------------
@@ -2085,10 +2135,11 @@ int launch_qload(kh::Device* d, const float* x, int64_t M, int64_t N, int64_t K,
 
 extern "C" {
 
+// may_alloc = false: no pool allocation (the skinny kernel then never splits K).
 static int gemm_i8_impl(const int8_t* a, const int8_t* b_packed, int64_t M, int64_t N, int64_t K, const double* sa,
                         int sa_per_row, const double* sb, int sb_per_col, const float* bias, float* out,
                         int32_t* acc_out, int act, const float* residual, unsigned* parts, int max_parts,
-                        int* nparts) {
+                        int* nparts, bool may_alloc = true) {
     KH_REQUIRE(M >= 0 && N >= 0 && K >= 0, "kh_gemm_i8: negative shape");
     KH_REQUIRE(out || acc_out, "kh_gemm_i8: neither out nor acc_out given");
     KH_REQUIRE(K <= 133144, "kh_gemm_i8: K > 133144 could overflow the int32 accumulator");
@@ -2105,7 +2156,7 @@ static int gemm_i8_impl(const int8_t* a, const int8_t* b_packed, int64_t M, int6
     int rc;
     bool parts_done = false;
     if (skinny_fits(a, b_packed, M, N, K)) {
-        rc = launch_skinny(d, a, b_packed, M, N, K, ep);
+        rc = launch_skinny(d, a, b_packed, M, N, K, ep, may_alloc);
     } else if (!parts && narrow_fits(a, b_packed, M, N, K)) {
         rc = launch_narrow(d, a, b_packed, M, N, K, ep);
     } else if (pingpong_fits(a, b_packed, M, N, K)) {
@@ -2309,10 +2360,12 @@ int kh_gemm_i8_qload_rows(const float* x, int64_t M, int64_t N, int64_t K, const
 }
 
 // kh_linear_i8's work with the codes and scales in q_scratch / sx_scratch.
-// Allocates nothing: the decode kernel, kh_quantize_rows and kh_gemm_i8
-// without absmax partials use no library scratch.
+// With may_alloc = false it allocates nothing: the decode kernel,
+// kh_quantize_rows and the GEMM without absmax partials and without a K
+// split use no library scratch and no pooled memory.
 static int linear_i8_impl(const float* x, int64_t M, int64_t K, const int8_t* b_packed, int64_t N, const double* sb,
-                          int sb_per_col, const float* bias, int8_t* q_scratch, double* sx_scratch, float* out) {
+                          int sb_per_col, const float* bias, int8_t* q_scratch, double* sx_scratch, float* out,
+                          bool may_alloc = true) {
     if (M >= 1 && N >= 1 && x && b_packed && sb && q_scratch && sx_scratch &&
         decode_fits(x, M, K, b_packed, N, q_scratch)) {
         KH_DEVICE_OR_RETURN(d);
@@ -2324,7 +2377,8 @@ static int linear_i8_impl(const float* x, int64_t M, int64_t K, const int8_t* b_
     }
     int rc = kh_quantize_rows(x, M, K, q_scratch, sx_scratch);
     if (rc) return rc;
-    return kh_gemm_i8(q_scratch, b_packed, M, N, K, sx_scratch, 1, sb, sb_per_col, bias, out, nullptr);
+    return gemm_i8_impl(q_scratch, b_packed, M, N, K, sx_scratch, 1, sb, sb_per_col, bias, out, nullptr, kActNone,
+                        nullptr, nullptr, 0, nullptr, may_alloc);
 }
 
 int kh_linear_i8_tensor(const float* x, int64_t M, int64_t K, const int8_t* b_packed, int64_t N, const double* sb,
@@ -2363,7 +2417,7 @@ int kh_linear_i8_noalloc(const float* x, int64_t M, int64_t K, const int8_t* b_p
     if (!d) return KH_ERR_NO_DEVICE;
     int8_t* q = reinterpret_cast<int8_t*>(d->noalloc);
     double* sx = reinterpret_cast<double*>(d->noalloc + kh::kNoAllocCodeBytes);
-    return linear_i8_impl(x, M, K, b_packed, N, sb, sb_per_col, bias, q, sx, out);
+    return linear_i8_impl(x, M, K, b_packed, N, sb, sb_per_col, bias, q, sx, out, /*may_alloc=*/false);
 }
 
 }  // extern "C"

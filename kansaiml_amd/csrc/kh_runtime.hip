@@ -41,6 +41,7 @@ struct Pool {
     size_t in_use = 0;
     size_t cached = 0;
     size_t driver_allocs = 0;
+    size_t requests = 0;  // kh_alloc calls served
     // Graph capture (kh_graph_capture_begin .. _end).  Blocks freed while
     // capturing go to cap_free, not to free_lists: the captured nodes keep
     // using them at every launch, so no later work may be handed them.
@@ -311,6 +312,7 @@ int kh_alloc(size_t bytes, void** dptr) {
     bool capturing;
     {
         std::lock_guard<std::mutex> lk(pool.mu);
+        pool.requests += 1;
         capturing = pool.capturing;
         // While capturing, blocks freed by the capture come back first (the
         // same last-freed-first order as outside a capture).
@@ -393,6 +395,15 @@ int kh_pool_stats(size_t* in_use, size_t* cached, size_t* driver_allocs) {
     if (in_use) *in_use = pool.in_use;
     if (cached) *cached = pool.cached;
     if (driver_allocs) *driver_allocs = pool.driver_allocs;
+    return KH_OK;
+}
+
+int kh_pool_requests(size_t* requests) {
+    KH_REQUIRE(requests, "kh_pool_requests: null out pointer");
+    KH_DEVICE_OR_RETURN(d);
+    kh::Pool& pool = kh::g_slots[d->id].pool;
+    std::lock_guard<std::mutex> lk(pool.mu);
+    *requests = pool.requests;
     return KH_OK;
 }
 

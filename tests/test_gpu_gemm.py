@@ -53,6 +53,8 @@ SHAPES = [
     (512, 768, 64), (768, 512, 192), (1024, 256, 4160),  # full-tile kernel: K % 64 == 0, K % 128 != 0
     (1000, 1000, 128), (257, 129, 64), (33, 300, 640),    # ping-pong kernel, partial tiles in M and N
     (16384, 1152, 384), (16384, 384, 1536),               # C4 QKV and fc2 shapes
+    (8, 1024, 8192), (32, 512, 16384), (5, 100, 8192),    # skinny with K split over 4, 8, 8 workgroups
+    (64, 2048, 8192), (17, 40, 12288),                    # split over 2; over 8 with 3 steps per wave
 ]
 
 
@@ -479,7 +481,8 @@ def test_matmul_f32_c3b_full_size(hip):
                                    (300, 1152, 384),     # ping-pong, partial tiles
                                    (130, 70, 80),        # general kernel (K % 64 != 0)
                                    (16384, 65, 384),     # a vocabulary head: narrow-N kernel; with partials ping-pong
-                                   (8, 512, 512)])       # skinny kernel
+                                   (8, 512, 512),        # skinny kernel
+                                   (24, 1000, 8192)])    # skinny kernel, K split over 4 workgroups
 @pytest.mark.parametrize("row_scales", [False, True])
 def test_gemm_i8_fused_epilogues(hip, M, N, K, row_scales):
     """GELU and residual epilogues give the same bits as the unfused graph

@@ -47,6 +47,7 @@ def _with_alloc(N, D, c):
 # the one-launch decode kernel (M <= 2), and the tiled GEMM for larger M.
 PAIRS = [
     ((32, 4096, 4096, True), (8, 4096, 1024, True)),
+    ((16, 8192, 1024, True), (8, 16384, 512, False)),  # shapes kh_linear_i8 runs with a K split
     ((2, 4096, 11008, True), (1, 2048, 512, True)),
     ((512, 2048, 1024, True), (64, 512, 512, False)),
 ]
@@ -66,6 +67,8 @@ def test_noalloc_matches_linear_i8(lib, first, second):
         N.call("kh_linear_i8_noalloc", c["x"].ptr, c["M"], c["K"], c["w"].ptr, c["N"], c["sb"].ptr, c["per_col"],
                c["bias"].ptr, out.ptr)
     N.synchronize()
+    # (pool_stats counts kh_alloc requests too: a block taken from a free list
+    # and returned would leave the byte counts unchanged)
     assert N.pool_stats() == before, "the no-alloc entry point drew from the pool"
     # The library scratch (outside the pool) is neither requested nor grown:
     # a path through it would count a request even where it no longer grows.
