@@ -24,7 +24,7 @@ the reference runs for a quantized Linear after dequantizing the weight
 C restatement of quantize.py:66-76; C1 as the reference's whole call.
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 50] [--warm-ms 50] [--no-cpu]
-                    [--only gemm,probe,quant,f32,c1,skinny,c4,copy,pcie] [--c5-rows M:K:N,...]
+                    [--only gemm,probe,quant,f32,c1,skinny,c4,c4row,copy,pcie] [--c5-rows M:K:N,...]
 
 Profiling: `python bench.py --profile-commands OUT` prints the rocprofv3 runs
 (kernel traces, FETCH_SIZE / WRITE_SIZE traffic, counter groups for the C3a
@@ -550,6 +550,29 @@ def bench_c4(steps, warmup):
 COPY_BYTES = 1 << 30
 
 
+def bench_c4_per_token(steps, warmup):
+    """C4 with per-token activation scales (`CharLM(act_granularity="row")`,
+    the option beside the reference's per-tensor configuration): replayed as
+    a HIP graph, or run eagerly under --no-graph-timing so that a kernel
+    trace sees the same kernels (every per-row quantize inside its producer:
+    LayerNorm, the O GEMM, fc1's GEMM)."""
+    from kansaiml_amd.charlm import CharLM, CharLMWeights
+    from kansaiml_amd.device import DeviceTensor as D
+    w = CharLMWeights(seed=0)
+    model = CharLM(w, act_granularity="row")
+    ids = D.from_host(np.random.Generator(np.random.PCG64(9)).integers(0, 65, (64, 256)).astype(np.int32))
+    if GRAPH_TIMING:
+        g = model.capture(64, 256)
+        g(ids, to_host=False)
+        ms = time_kernel(lambda: g(g.inputs[0], to_host=False), steps, warmup, tag="c4_per_token_graph")
+        g.close()
+    else:
+        ms = time_kernel(lambda: model.forward(ids, to_host=False), steps, warmup, tag="c4_per_token_eager")
+    return {"workload": "C4 int8 char-LM forward with per-token activation scales, batch 64 x seq 256",
+            "timing": "HIP graph replay" if GRAPH_TIMING else "eager (profiled run: no graph launches)",
+            "ms_per_forward": round(ms, 4), "tokens_per_s": round(64 * 256 / (ms * 1e-3), 1)}
+
+
 def bench_mfma_probe():
     """The attainable int8 MFMA rate and the shader clock under that load
     (kh_probe_mfma_i8): random operand bytes, no memory traffic in the loop.
@@ -608,6 +631,7 @@ PROFILE_RUNS = {
                 "TCC_MISS_sum TA_BUFFER_READ_LDS_WAVEFRONTS_sum TD_TC_STALL_sum TD_TD_BUSY_sum", _GEMM_ARGS),
     "gemm_p3": ("--pmc GRBM_COUNT GRBM_GUI_ACTIVE SQ_CYCLES", _GEMM_ARGS),
     "c4_trace": ("--kernel-trace --stats", "--no-cpu --only c4 --steps 10 --warmup 20 --no-graph-timing"),
+    "c4row_trace": ("--kernel-trace --stats", "--no-cpu --only c4row --steps 40 --warmup 20 --no-graph-timing"),
     "c4_p1": ("--pmc SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_VALU_MFMA_BUSY_CYCLES SQ_ACTIVE_INST_VALU SQ_LDS_BANK_CONFLICT "
               "SQ_INSTS_VALU SQ_WAIT_ANY SQ_ACTIVE_INST_LDS", _C4_ARGS),
     "c4_p2": ("--pmc SQ_INSTS_MFMA SQ_INSTS_LDS SQ_WAVES SQ_INSTS_VMEM_WR SQ_INSTS_VMEM_RD GRBM_GUI_ACTIVE GRBM_COUNT",
@@ -889,12 +913,14 @@ def _summarize_counters(root, runs, fname, title, cal, select=None):
                    _COUNTER_NOTE + _counter_table(_by_kernel(disp), cal))
 
 
-def _summarize_c4_forward(root):
+def _summarize_c4_forward(root, run="c4_trace", fname="c4_forward_mi355x.md",
+                          title="C4 int8 char-LM forward: kernel time per forward on one MI355X (gfx950)",
+                          which="the default `CharLM` forward"):
     """The C4 forward's kernel time per forward: the trace split at each
     embedding launch, the segments with the modal number of launches (one
     forward each; the others include the bench's per-GEMM re-runs), and per
     kernel and grid the median of its launches' time per forward."""
-    tr = _find(os.path.join(root, "c4_trace"), "kernel_trace.csv")
+    tr = _find(os.path.join(root, run), "kernel_trace.csv")
     if not tr:
         return
     rows = sorted(_read_csv(tr), key=lambda r: int(r["Start_Timestamp"]))
@@ -928,14 +954,13 @@ def _summarize_c4_forward(root):
         total += per
     table.sort(key=lambda t: -t[0])
     body = (f"Workload: config C4 (vocab 65, d_model 384, 6 heads, 6 layers, FFN 1536, batch 64 x seq 256), the "
-            f"default `CharLM` forward run eagerly (the kernels a HIP-graph replay launches; rocprofv3's kernel "
+            f"{which} run eagerly (the kernels a HIP-graph replay launches; rocprofv3's kernel "
             f"trace has crashed inside hipGraphLaunch).  The trace is split into forwards at each embedding "
             f"launch; the {len(good)} segments holding exactly one forward's {mode} launches give the medians "
             f"below (durations include the profiler's per-dispatch timestamps).\n\n"
             + _md_table(["kernel", "WGs", "launches per forward", "us each", "us per forward"], [t[1] for t in table])
             + f"\n\nSum: {total:.1f} us of kernel time per forward.")
-    _write_profile("c4_forward_mi355x.md", "C4 int8 char-LM forward: kernel time per forward on one MI355X (gfx950)",
-                   [profile_command("c4_trace")], body)
+    _write_profile(fname, title, [profile_command(run)], body)
 
 
 def summarize(root):
@@ -963,6 +988,9 @@ def summarize(root):
                         "C5 decode rows (`kh_linear_i8`): hardware counters per kernel, one MI355X", cal,
                         select=lambda d: not d["kernel"].startswith("copy16"))
     _summarize_c4_forward(root)
+    _summarize_c4_forward(root, "c4row_trace", "c4_forward_per_token_mi355x.md",
+                          "C4 int8 char-LM forward with per-token activation scales: kernel time per forward on one "
+                          "MI355X (gfx950)", '`CharLM(act_granularity="row")` forward')
     return traffic
 
 
@@ -1246,6 +1274,12 @@ def main():
         log(f"C4 forward: {c4['ms_per_forward']:.3f} ms ({c4['timing']}; {c4['tokens_per_s']:.0f} tokens/s), "
             f"{c4['ms_per_forward_eager']:.3f} ms eager")
         Nn.call("kh_pool_trim")
+    c4row = None
+    if "c4row" in only:
+        log("C4 forward with per-token activation scales ...")
+        c4row = bench_c4_per_token(max(5, args.steps // 4), max(2, args.warmup // 10))
+        log(f"C4 per-token forward: {c4row['ms_per_forward']:.3f} ms ({c4row['timing']})")
+        Nn.call("kh_pool_trim")
     host_buffers = None
     if "pcie" in only:
         log("C2 and C3a from host buffers ...")
@@ -1322,6 +1356,7 @@ def main():
                           "bytes": "N*K + 8N + 4MK + 2MK + 4MN", "rows": skinny},
         "c1_linear": c1,
         "c4_forward": c4,
+        "c4_forward_per_token": c4row,
         "host_buffers": host_buffers,
         "cpu_baseline": cpu,
         "warmup_per_leg": {"min_ms": WARM_MS, **WARMUP_LOG},
