@@ -723,7 +723,7 @@ __global__ __launch_bounds__(512, BN == 256 ? 2 : ((BM == 256 || NS >= 4 || (FUS
 // ---------------------------------------------------------------------------
 constexpr int kQlBM = 64;
 
-template <int NB, int NS, bool FUSED, bool ROWS = false>
+template <int NB, int NS, bool FUSED, bool ROWS = false, int NK = 0>
 __global__ __launch_bounds__(512, 2) void gemm_i8_qload_kernel(const float* __restrict__ X, int M, int N, int K,
                                                                const unsigned* __restrict__ xparts, int nxparts,
                                                                const int8_t* __restrict__ B, Epilogue ep,
@@ -833,11 +833,12 @@ __global__ __launch_bounds__(512, 2) void gemm_i8_qload_kernel(const float* __re
 #pragma unroll
     for (int b = 0; b < NB; ++b) ce[b] = col_epi(ep, (int64_t)tn * BN + wn * 32 * NB + b * 32 + fr);
 
-    const int nk = K / BK;
+    const int nk = NK ? NK : K / BK;
     f32x4 xa[D][2];
 #pragma unroll
     for (int s = 0; s < D; ++s)
         if (s < nk) issue(s, xa[s]);
+#pragma unroll
     for (int k0 = 0; k0 < nk; k0 += D) {
 #pragma unroll
         for (int j = 0; j < D; ++j) {
@@ -846,18 +847,29 @@ __global__ __launch_bounds__(512, 2) void gemm_i8_qload_kernel(const float* __re
             int8_t* stage = lds + (k % NS) * kStage;
             wait_loads_beyond<kLoads>(min(D - 1, nk - 1 - k));  // this wave's A and B of step k landed
             const unsigned c0 = kh::quant::pack4(xa[j][0], sc), c1 = kh::quant::pack4(xa[j][1], sc);
-            *reinterpret_cast<u32x2*>(stage + a_lds) = u32x2{c0, c1};
+            const unsigned st_addr = (unsigned)(uintptr_t)(__attribute__((address_space(3))) int8_t*)stage;
+            // Inline LDS accesses: as plain ones the compiler would wait for
+            // every LDS-DMA in flight (the later steps' B) before each.
+            asm volatile("ds_write_b64 %0, %1" : : "v"(st_addr + a_lds), "v"(u32x2{c0, c1}) : "memory");
             __builtin_amdgcn_s_waitcnt(wait_imm(63, 0));
             __builtin_amdgcn_s_barrier();
-            if (k + D < nk) issue(k + D, xa[j]);
+            asm volatile("" ::: "memory");
+            i32x4 fa[2], fb[2][NB];
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
-                const i32x4 fa = *reinterpret_cast<const i32x4*>(stage + (a_off ^ (s << 5)));
+                asm volatile("ds_read_b128 %0, %1" : "=v"(fa[s]) : "v"(st_addr + (a_off ^ (s << 5))) : "memory");
 #pragma unroll
-                for (int b = 0; b < NB; ++b) {
-                    const i32x4 fb = *reinterpret_cast<const i32x4*>(stage + (b_off[b] ^ (s << 5)));
-                    acc[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa, fb, acc[b], 0, 0, 0);
-                }
+                for (int b = 0; b < NB; ++b)
+                    asm volatile("ds_read_b128 %0, %1" : "=v"(fb[s][b]) : "v"(st_addr + (b_off[b] ^ (s << 5))) : "memory");
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (k + D < nk) issue(k + D, xa[j]);
+            __builtin_amdgcn_s_waitcnt(wait_imm(63, 0));  // the fragments in registers
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+#pragma unroll
+                for (int b = 0; b < NB; ++b) acc[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[s], fb[s][b], acc[b], 0, 0, 0);
             }
         }
     }
@@ -2122,7 +2134,15 @@ template <int NB, bool ROWS = false>
 int launch_qload(kh::Device* d, const float* x, int64_t M, int64_t N, int64_t K, const unsigned* xparts,
                  int nxparts, const int8_t* b, const Epilogue& ep, unsigned* parts) {
     const unsigned grid = (unsigned)((M / kQlBM) * (N / (128 * NB)));
-    if (ep.act != kActNone || ep.residual)
+    const bool fused = ep.act != kActNone || ep.residual;
+    if (K == 384) {
+        if (fused)
+            gemm_i8_qload_kernel<NB, 5, true, ROWS, 6><<<grid, 512, 0, d->stream>>>(x, (int)M, (int)N, (int)K, xparts,
+                                                                                    nxparts, b, ep, parts);
+        else
+            gemm_i8_qload_kernel<NB, 5, false, ROWS, 6><<<grid, 512, 0, d->stream>>>(x, (int)M, (int)N, (int)K,
+                                                                                     xparts, nxparts, b, ep, parts);
+    } else if (fused)
         gemm_i8_qload_kernel<NB, 5, true, ROWS><<<grid, 512, 0, d->stream>>>(x, (int)M, (int)N, (int)K, xparts,
                                                                              nxparts, b, ep, parts);
     else
