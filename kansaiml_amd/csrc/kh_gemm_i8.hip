@@ -2151,7 +2151,9 @@ int qload_nb(const float* x, const int8_t* b, int64_t M, int64_t N, int64_t K) {
 
 template <int NB, bool ROWS = false>
 int launch_qload(kh::Device* d, const float* x, int64_t M, int64_t N, int64_t K, const unsigned* xparts,
-                 int nxparts, const int8_t* b, const Epilogue& ep, unsigned* parts) {
+                 int nxparts, const int8_t* b, const Epilogue& ep_in, unsigned* parts) {
+    Epilogue ep = ep_in;
+    ep.stream_out = M * N * (int64_t)sizeof(float) > kStreamOutBytes;
     const unsigned grid = (unsigned)((M / kQlBM) * (N / (128 * NB)));
     const bool fused = ep.act != kActNone || ep.residual;
     if (K == 384) {
