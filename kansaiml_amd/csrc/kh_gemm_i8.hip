@@ -850,7 +850,9 @@ __global__ __launch_bounds__(512, 2) void gemm_i8_qload_kernel(const float* __re
 #pragma unroll
     for (int s = 0; s < D; ++s)
         if (s < nk) issue(s, xa[s]);
-#pragma unroll
+    // Unrolled whole where the step count is fixed (NK), not otherwise.
+    constexpr int kOuter = NK ? (NK + D - 1) / D : 1;
+#pragma unroll kOuter
     for (int k0 = 0; k0 < nk; k0 += D) {
 #pragma unroll
         for (int j = 0; j < D; ++j) {
