@@ -30,7 +30,7 @@ import numpy as np
 
 from . import _native as N
 from . import hip as H
-from .device import DeviceTensor, as_host_array, to_device
+from .device import DeviceTensor, to_device
 
 
 def _shape_of(t) -> list:
