@@ -117,6 +117,41 @@ def test_gemm_i8_c3a_full_size(hip):
     cols = gen.choice(N, size=64, replace=False)
     eacc_c = (a.astype(np.int64)[::97] @ bt[cols].astype(np.int64).T).astype(np.int32)
     np.testing.assert_array_equal(acc[::97][:, cols], eacc_c)
+    # The bench's launch asks for the output alone, which takes the full-tile
+    # kernel build (with the accumulators the general build runs); its
+    # 256 MiB output goes out through non-temporal stores.  Every value must
+    # equal the checked run's.
+    fast, none = H.gemm_i8(D.from_host(a), D.from_host(bt), D.from_host(np.array([0.01])),
+                           D.from_host(np.array([0.02])))
+    assert none is None
+    np.testing.assert_array_equal(bits32(fast.numpy()), bits32(out))
+
+
+@pytest.mark.parametrize("row_scales", [False, True])
+def test_gemm_i8_full_tile_256(hip, row_scales):
+    """The 256x256 full-tile kernel builds (output only, K > 512, at least
+    1.5 tiles per CU: C3a's launch, here with a bias and per-tensor or
+    per-row activation scales; a 100 MB output, stored with ordinary stores)
+    give the bits of the general build everywhere, and the oracle's on
+    sampled rows."""
+    H, D = hip
+    M, N, K = 4096, 6144, 1024
+    gen = np.random.Generator(np.random.PCG64(11 + int(row_scales)))
+    a = gen.integers(-127, 128, (M, K), dtype=np.int8)
+    bt = gen.integers(-127, 128, (N, K), dtype=np.int8)
+    sa = gen.uniform(1e-4, 1e-3, M) if row_scales else np.array([0.01])
+    sb = gen.uniform(1e-4, 1e-3, N)
+    bias = gen.standard_normal(N).astype(np.float32)
+    ad, bd, sad, sbd, biasd = D.from_host(a), D.from_host(bt), D.from_host(sa), D.from_host(sb), D.from_host(bias)
+    fast, _ = H.gemm_i8(ad, bd, sad, sbd, biasd)
+    general, acc = H.gemm_i8(ad, bd, sad, sbd, biasd, want_acc=True)
+    fast_h = fast.numpy()
+    np.testing.assert_array_equal(bits32(fast_h), bits32(general.numpy()))
+    rows = gen.choice(M, size=64, replace=False)
+    eacc = O.ko_gemm_i8(a[rows], bt)
+    np.testing.assert_array_equal(acc.numpy()[rows], eacc)
+    expect = O.ko_epilogue(eacc, sa[rows] if row_scales else sa, sb, bias)
+    np.testing.assert_array_equal(bits32(fast_h[rows]), bits32(expect))
 
 
 @pytest.mark.parametrize("K,N", [(4096, 11008), (4096, 4096)])
